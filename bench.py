@@ -1,0 +1,306 @@
+#!/usr/bin/env python3
+"""Quantize-kernel benchmark on one MI355X (BASELINE.json metric).
+
+A step is one weight-sync quantization pass over one synthetic weight set
+already resident in HBM:
+
+  c2 (default, the metric's config): the full Qwen3-8B linear set, 36 layers x
+     {q,k,v,o,gate,up,down}, bf16 N(0, 0.02^2) with 0.1% +-U(0.5, 4) outliers,
+     -> FP8 E4M3 with one fp32 scale per 128x128 tile, ONE grouped launch.
+  c1: one [4096, 4096] weight, 128x128 (L2/MALL flushed between launches).
+  c3: Qwen3-30B-A3B experts, 48 layers x 128 experts (gate_up [E,1536,2048],
+      down [E,2048,768]) with one zero and one inf tile per layer; one launch
+      per layer (48 per step).
+  c4: c2 shapes, Student-t(4) x 0.02/sqrt(2), MXFP8.
+  c5: c2 shapes, N(0, 0.02^2) x per-row log-uniform[0.25, 4], MXFP4.
+
+Prints ONE JSON line on stdout.  value = algorithmic bytes (bf16 in + codes +
+scales) per step / step time, in GB/s (1e9 B/s).  The roofline object uses the
+same bytes over the kernel's average launch time from HIP events on the launch
+stream.  cpu_baseline times the reference's op sequence in torch on the host
+CPU (oracle/torch_ref.py) over a bounded sample of the same weights.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+for _p in (ROOT, os.path.join(ROOT, "lumen-rl_amd")):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+HBM_PEAK_GBS = 8000.0
+QWEN3_8B = [("q_proj", 4096, 4096), ("k_proj", 1024, 4096), ("v_proj", 1024, 4096),
+            ("o_proj", 4096, 4096), ("gate_proj", 12288, 4096), ("up_proj", 12288, 4096),
+            ("down_proj", 4096, 12288)]
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def metric_name() -> str:
+    with open(os.path.join(ROOT, "BASELINE.json")) as f:
+        return json.load(f)["metric"]
+
+
+# ---------------------------------------------------------------------------
+# synthetic weights (generated on the device from a seed; per-layer seed = base + layer)
+# ---------------------------------------------------------------------------
+def gen_weight(torch, rows, cols, gen, dev, kind="normal"):
+    w = torch.empty(rows, cols, dtype=torch.float32, device=dev)
+    if kind == "student_t":
+        # t(4) = N / sqrt(chi2_4 / 4); std of t(4) is sqrt(2)
+        n = torch.randn(rows, cols, generator=gen, device=dev)
+        chi = torch.randn(4, rows, cols, generator=gen, device=dev).square_().sum(0).div_(4.0)
+        w = n.div_(chi.sqrt_()).mul_(0.02 / math.sqrt(2.0))
+        del chi
+    else:
+        w.normal_(0.0, 0.02, generator=gen)
+        if kind == "rowscale":
+            u = torch.rand(rows, 1, generator=gen, device=dev)
+            w.mul_(torch.exp(math.log(0.25) + u * (math.log(4.0) - math.log(0.25))))
+        else:
+            k = max(1, w.numel() // 1000)
+            idx = torch.randint(0, w.numel(), (k,), generator=gen, device=dev)
+            sign = torch.randint(0, 2, (k,), generator=gen, device=dev).float().mul_(2).sub_(1)
+            mag = torch.rand(k, generator=gen, device=dev).mul_(3.5).add_(0.5)
+            w.view(-1)[idx] = sign * mag
+    return w.to(torch.bfloat16)
+
+
+def qwen3_8b_set(torch, dev, seed, kind="normal", layers=36):
+    ws, names = [], []
+    for layer in range(layers):
+        gen = torch.Generator(device=dev).manual_seed(seed + layer)
+        for name, r, c in QWEN3_8B:
+            ws.append(gen_weight(torch, r, c, gen, dev, kind))
+            names.append(f"layers.{layer}.{name}")
+    return ws, names
+
+
+def moe_layer(torch, dev, seed, layer, experts=128):
+    gen = torch.Generator(device=dev).manual_seed(seed + layer)
+    gu = torch.empty(experts, 1536, 2048, dtype=torch.float32, device=dev).normal_(0.0, 0.02, generator=gen)
+    dn = torch.empty(experts, 2048, 768, dtype=torch.float32, device=dev).normal_(0.0, 0.02, generator=gen)
+    e = int(torch.randint(0, experts, (1,), generator=gen, device=dev))
+    gu[e, 128:256, 256:384] = 0.0                      # one all-zero tile
+    e2 = int(torch.randint(0, experts, (1,), generator=gen, device=dev))
+    dn[e2, 512 + 3, 128 + 5] = float("inf")            # one tile holding an inf
+    return gu.to(torch.bfloat16), dn.to(torch.bfloat16)
+
+
+# ---------------------------------------------------------------------------
+# CPU baseline: the reference's op sequence in torch on the host (bounded sample)
+# ---------------------------------------------------------------------------
+def cpu_baseline(torch, ws, fmt_block, seconds):
+    from oracle import torch_ref
+
+    threads = max(1, min(os.cpu_count() or 1, 16))
+    torch.set_num_threads(threads)
+    done_bytes = 0
+    n = 0
+    t_total = 0.0
+    for w in ws:
+        x = w.cpu()
+        t0 = time.perf_counter()
+        if fmt_block == (128, 128):
+            q, s = torch_ref.quantize_tensor_tiles(x.float(), (128, 128))
+        else:
+            q, s = torch_ref.quantize_tensor(x.float(), fmt_block[1])
+        t_total += time.perf_counter() - t0
+        done_bytes += x.numel() * 2 + q.numel() + s.numel() * 4
+        n += 1
+        if t_total >= seconds:
+            break
+    return {
+        "value": round(done_bytes / t_total / 1e9, 3),
+        "unit": "GB/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": (f"first {n} tensors of the same weight set ({done_bytes / 1e9:.2f} GB "
+                   f"algorithmic) through oracle/torch_ref.py (weight_quantizer.py op order on "
+                   f"{fmt_block[0]}x{fmt_block[1]} blocks, fp32 upcast first) with "
+                   f"torch.set_num_threads({threads}) on {os.cpu_count()} visible cores"),
+    }
+
+
+# ---------------------------------------------------------------------------
+def run(args):
+    import torch
+
+    from lumenrl_amd.quantization import ops
+
+    if not torch.cuda.is_available():
+        log("bench.py needs a HIP device")
+        sys.exit(2)
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    stream = torch.cuda.current_stream(dev)
+    cfg = args.config
+    t0 = time.time()
+
+    flush = None
+    if cfg in ("c2", "c4", "c5"):
+        kind = {"c2": "normal", "c4": "student_t", "c5": "rowscale"}[cfg]
+        fmt = {"c2": "fp8_block", "c4": "mxfp8", "c5": "mxfp4"}[cfg]
+        ws, _ = qwen3_8b_set(torch, dev, args.seed, kind)
+        plans = [ops.QuantPlan(ws, fmt, (128, 128))]
+        workload = {"c2": "qwen3-8b-linears-fp8-e4m3-128x128", "c4": "qwen3-8b-linears-mxfp8",
+                    "c5": "qwen3-8b-linears-mxfp4"}[cfg]
+        cpu_ws, cpu_blk = ws, (128, 128)
+        extra = {"tensors": len(ws), "layers": 36, "elements": sum(w.numel() for w in ws),
+                 "format": fmt, "launches_per_step": 1}
+    elif cfg == "c1":
+        g = torch.Generator(device=dev).manual_seed(args.seed)
+        ws = [gen_weight(torch, 4096, 4096, g, dev)]
+        plans = [ops.QuantPlan(ws, "fp8_block", (128, 128))]
+        flush = torch.empty(1 << 30, dtype=torch.uint8, device=dev)
+        workload = "single-4096x4096-fp8-e4m3-128x128"
+        cpu_ws, cpu_blk = ws, (128, 128)
+        extra = {"tensors": 1, "elements": ws[0].numel(), "format": "fp8_block",
+                 "launches_per_step": 1, "l2_mall_flushed": True}
+    elif cfg == "c3":
+        plans, ws = [], []
+        for layer in range(48):
+            gu, dn = moe_layer(torch, dev, args.seed, layer)
+            ws += [gu, dn]
+            plans.append(ops.QuantPlan([gu, dn], "fp8_block", (128, 128)))
+        workload = "qwen3-30b-a3b-experts-fp8-e4m3-128x128"
+        cpu_ws, cpu_blk = ws[:2], (128, 128)
+        extra = {"tensors": len(ws), "layers": 48, "experts": 128,
+                 "elements": sum(w.numel() for w in ws), "format": "fp8_block",
+                 "launches_per_step": 48}
+    else:
+        raise SystemExit(f"unknown config {cfg}")
+    torch.cuda.synchronize()
+    step_bytes = sum(p.algorithmic_bytes for p in plans)
+    log(f"[bench] {workload}: {len(ws)} tensors, {step_bytes / 1e9:.3f} GB per step, "
+        f"setup {time.time() - t0:.1f}s")
+
+    def step(ev_pairs=None):
+        for p in plans:
+            if flush is not None:
+                flush.zero_()
+            if ev_pairs is not None:
+                a = torch.cuda.Event(enable_timing=True)
+                b = torch.cuda.Event(enable_timing=True)
+                a.record(stream)
+                p.run()
+                b.record(stream)
+                ev_pairs.append((a, b, p.algorithmic_bytes))
+            else:
+                p.run()
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    # timed region: exactly K steps, synchronized on both sides
+    evs = []
+    torch.cuda.synchronize()
+    w0 = time.perf_counter()
+    for _ in range(args.steps):
+        step(evs)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - w0
+    launch_ms = [a.elapsed_time(b) for a, b, _ in evs]
+    launch_bytes = [nb for _, _, nb in evs]
+    kern_ms = sum(launch_ms) / len(launch_ms)
+    achieved = sum(launch_bytes) / len(launch_bytes) / (kern_ms * 1e-3) / 1e9
+    if flush is None:
+        ms_per_step = wall * 1e3 / args.steps
+    else:  # the L2 flush between launches is not part of the step
+        ms_per_step = sum(launch_ms) / args.steps
+    value = step_bytes / (ms_per_step * 1e-3) / 1e9
+    log(f"[bench] {ms_per_step:.4f} ms/step, {value:.1f} GB/s; kernel avg {kern_ms:.4f} ms "
+        f"({achieved:.1f} GB/s = {achieved / HBM_PEAK_GBS:.1%} of 8 TB/s)")
+
+    traffic = None
+    tfile = os.path.join(ROOT, "profiles", f"traffic_{cfg}.json")
+    if os.path.exists(tfile):
+        with open(tfile) as f:
+            traffic = json.load(f).get("hbm_bytes_per_launch")
+
+    result = {
+        "metric": metric_name(),
+        "value": round(value, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (seeded on-device bf16 weights, BASELINE.json distribution)",
+        "config": {"workload": workload, **extra, "algorithmic_bytes_per_step": step_bytes},
+        "roofline": {
+            "bound": "hbm",
+            "achieved": round(achieved, 2),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "traffic": traffic,
+            "kernel": "k_tile128" if cfg in ("c1", "c2", "c3") else "k_mx",
+            "launch_ms": round(kern_ms, 5),
+        },
+    }
+    if not args.no_cpu:
+        log("[bench] cpu baseline ...")
+        result["cpu_baseline"] = cpu_baseline(torch, cpu_ws, cpu_blk, args.cpu_seconds)
+    print(json.dumps(result), flush=True)
+
+
+def run_copy(args):
+    """Plain device copy of a known size, for scaling rocprof FETCH/WRITE counters."""
+    import torch
+
+    dev = torch.device("cuda", 0)
+    n = args.copy_bytes
+    src = torch.ones(n, dtype=torch.uint8, device=dev)
+    dst = torch.empty_like(src)
+    for _ in range(args.warmup):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record()
+    for _ in range(args.steps):
+        dst.copy_(src)
+    b.record()
+    torch.cuda.synchronize()
+    ms = a.elapsed_time(b) / args.steps
+    print(json.dumps({"mode": "copy", "bytes_read": n, "bytes_written": n, "ms": ms,
+                      "GBps": 2 * n / (ms * 1e-3) / 1e9}), flush=True)
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--config", default="c2", choices=["c1", "c2", "c3", "c4", "c5"])
+    ap.add_argument("--seed", type=int, default=1000)
+    ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--mode", default="quant", choices=["quant", "copy"])
+    ap.add_argument("--copy-bytes", type=int, default=1 << 30)
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py measures one GPU: the quantize path is per-device with no "
+              "collectives (see DESIGN.md for how it shards); run with --gpus 1", file=sys.stderr)
+        sys.exit(2)
+    if args.mode == "copy":
+        run_copy(args)
+    else:
+        run(args)
+
+
+if __name__ == "__main__":
+    main()

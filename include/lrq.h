@@ -1,0 +1,156 @@
+/*
+ * lrq.h -- C ABI of the MI355X (gfx950) weight-quantization library
+ * (liblrq.so): bf16/fp16/fp32 weights -> blockwise FP8 E4M3, MXFP8, MXFP4.
+ *
+ * The reference (Lumen-RL) is pure Python and has no FFI; each entry point
+ * below states which reference interface it replaces.  A caller binds these
+ * with ctypes (the shipped Python package does), cffi or plain C.
+ *
+ * Conventions
+ *   - Every pointer argument named in/codes/scales/out is DEVICE memory the
+ *     caller allocated (torch does, in the Python package).  The library never
+ *     allocates or frees device memory.
+ *   - Work is enqueued on `stream` (a hipStream_t; NULL = the null stream) and
+ *     is stream-ordered; no entry point synchronizes the device.
+ *   - Return 0 on success, LRQ_ERR_* (< 0) for a rejected argument, or a
+ *     positive hipError_t if the HIP runtime failed.  lrq_last_error() gives
+ *     the message of the last failure on the calling thread.
+ *   - Element counts and strides are in elements of the input dtype.
+ *   - Layouts: codes are dense row-major [batch, rows, cols] (e4m3 bytes) or
+ *     [rows, cols/2] (e2m1, element 2i in the low nibble of byte i).
+ *   - Entry points are re-entrant; the library keeps no device state.
+ */
+#ifndef LRQ_H_
+#define LRQ_H_
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct ihipStream_t* lrq_stream_t; /* == hipStream_t */
+
+/* input / scale dtypes */
+#define LRQ_DTYPE_BF16 0
+#define LRQ_DTYPE_F16 1
+#define LRQ_DTYPE_F32 2
+
+/* flags */
+#define LRQ_FLAG_POW2_SCALE 1u   /* FP8Config.use_weight_pow2_scale (fp8_config.py:22) */
+#define LRQ_FLAG_NATIVE_ARITH 2u /* arithmetic in the input dtype (quantize_tensor on a
+                                    bf16/fp16 tensor) instead of float32 */
+#define LRQ_FLAG_SCALE_BF16 4u   /* write float32-arithmetic scales rounded to bf16, the
+                                    `_fp8_scales` sidecar of quantize_state_dict
+                                    (weight_quantizer.py:111) */
+
+/* formats (grouped launches) */
+#define LRQ_FMT_FP8_BLOCK 0
+#define LRQ_FMT_MXFP8 1
+#define LRQ_FMT_MXFP4 2
+
+/* errors */
+#define LRQ_ERR_ARG (-1)      /* invalid argument (shape, dtype, block size, null) */
+#define LRQ_ERR_ALIGN (-2)    /* pointer/stride alignment a format requires */
+#define LRQ_ERR_CAPACITY (-3) /* caller buffer too small */
+#define LRQ_ERR_TABLE (-4)    /* grouped table corrupt or from another version */
+
+/*
+ * Blockwise FP8 E4M3 quantization with one scale per blk_r x blk_c block.
+ * Replaces WeightQuantizer.quantize_tensor
+ * (lumenrl/quantization/weight_quantizer.py:40-77) -- blk_r = 1,
+ * blk_c = block_size -- and the 128x128 `weight_scale_inv` tiling that vLLM /
+ * ATOM per-block FP8 loaders consume (blk_r = blk_c = 128;
+ * lumenrl/engine/inference/vllm_fp8_utils.py:104-118).
+ *   in      : batch matrices [rows, cols]; row r of matrix b at
+ *             in + b*batch_stride + r*ld (elements of in_dtype).
+ *   codes   : [batch, rows, cols] e4m3fn bytes.
+ *   scales  : [batch, ceil(rows/blk_r), ceil(cols/blk_c)]: float32, or 16-bit
+ *             words of the input dtype with LRQ_FLAG_NATIVE_ARITH, or bf16 with
+ *             LRQ_FLAG_SCALE_BF16.  Edge blocks may be partial.
+ * Bit-exact with the reference evaluated by torch on x86, including NaN, inf,
+ * all-zero and subnormal blocks.
+ */
+int lrq_fp8_block_quant(const void* in, int in_dtype, int64_t batch, int64_t rows,
+                        int64_t cols, int64_t ld, int64_t batch_stride, int64_t blk_r,
+                        int64_t blk_c, uint8_t* codes, void* scales, unsigned flags,
+                        lrq_stream_t stream);
+
+/*
+ * Inverse: out = fp32(code) * fp32(scale) per block.  Replaces
+ * WeightQuantizer.dequantize_tensor (weight_quantizer.py:79-89); out_dtype
+ * LRQ_DTYPE_BF16 adds the `.to(torch.bfloat16)` of dequantize_state_dict
+ * (:133).  scale_dtype: LRQ_DTYPE_F32 / _BF16 / _F16.  out_dtype: _F32 / _BF16.
+ */
+int lrq_fp8_block_dequant(const uint8_t* codes, const void* scales, int scale_dtype,
+                          int64_t batch, int64_t rows, int64_t cols, int64_t blk_r,
+                          int64_t blk_c, void* out, int out_dtype, lrq_stream_t stream);
+
+/*
+ * MXFP8: E4M3 codes [rows, cols] plus one E8M0 byte per 1x32 group along cols
+ * (scales [rows, cols/32]).  MXFP4: E2M1 codes [rows, cols/2] and the same
+ * scales.  cols must be a multiple of 32.  No reference function (the
+ * reference delegates MX to absent aiter/vLLM code:
+ * examples/DAPO/atom_aiter_shim/sitecustomize.py:31-32,
+ * examples/Qwen3_8B_SDDD_MI350_vLLM/configs/opd_qwen3_8b.yaml:43); the rules
+ * are OCP MX v1.0 with round-to-nearest-even and saturation.
+ */
+int lrq_mxfp8_quant(const void* in, int in_dtype, int64_t rows, int64_t cols, int64_t ld,
+                    uint8_t* codes, uint8_t* scales, lrq_stream_t stream);
+int lrq_mxfp4_quant(const void* in, int in_dtype, int64_t rows, int64_t cols, int64_t ld,
+                    uint8_t* codes, uint8_t* scales, lrq_stream_t stream);
+
+/*
+ * Grouped launch: many tensors (a layer, a whole weight set, or MoE expert
+ * stacks) quantized by ONE kernel launch.  Replaces the per-tensor Python loop
+ * of WeightQuantizer.quantize_state_dict (weight_quantizer.py:91-115) and the
+ * per-expert loaders (lumenrl/engine/inference/vllm_moe_weight_sync.py:232-283).
+ *
+ * 1. lrq_group_table_bytes() sizes a table for `n` tensors.
+ * 2. lrq_group_pack() validates the tensors and writes the table into a HOST
+ *    buffer (descriptors + a work-group -> tensor map).
+ * 3. The caller copies the table verbatim to device memory (once; tables stay
+ *    valid while the tensors' storage does) and calls lrq_quant_grouped() with
+ *    both copies: the host copy supplies the launch geometry, the device copy
+ *    is what the kernel reads.
+ * All tensors of a table share fmt, in_dtype, block shape and flags, and must
+ * all qualify for the same kernel (the pack fails otherwise).
+ */
+typedef struct lrq_tensor {
+  const void* in;       /* device input */
+  void* codes;          /* device codes */
+  void* scales;         /* device scales */
+  int64_t batch;        /* matrices (MoE experts); >= 1 */
+  int64_t rows, cols;   /* per matrix */
+  int64_t ld;           /* input row stride (elements) */
+  int64_t batch_stride; /* input matrix stride (elements) */
+} lrq_tensor;
+
+int64_t lrq_group_table_bytes(int fmt, const lrq_tensor* tensors, int64_t n, int in_dtype,
+                              int64_t blk_r, int64_t blk_c, unsigned flags);
+int lrq_group_pack(int fmt, const lrq_tensor* tensors, int64_t n, int in_dtype, int64_t blk_r,
+                   int64_t blk_c, unsigned flags, void* host_table, int64_t capacity);
+int lrq_quant_grouped(const void* host_table, const void* device_table, lrq_stream_t stream);
+/* work-groups of a packed table's launch (for bandwidth accounting) */
+int64_t lrq_group_units(const void* host_table);
+
+/* Library version string ("lrq <semver> gfx950"). */
+const char* lrq_version(void);
+/* Message of the last failed call on this thread ("" if none). */
+const char* lrq_last_error(void);
+
+/*
+ * Diagnostics (no reference counterpart): the device element encoders applied
+ * to raw inputs, so tests can compare them with the CPU oracle exhaustively.
+ *   lrq_diag_e4m3_bits: out[i] = e4m3(float with bit pattern start + i), via
+ *     the hardware pack-convert the kernels use; n a multiple of 4.
+ *   lrq_diag_e2m1: out[i] = E2M1 nibble of in[i] (finite inputs).
+ */
+int lrq_diag_e4m3_bits(uint32_t start, int64_t n, uint8_t* out, lrq_stream_t stream);
+int lrq_diag_e2m1(const float* in, uint8_t* out, int64_t n, lrq_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* LRQ_H_ */

@@ -1,0 +1,365 @@
+// C ABI of liblrq (include/lrq.h): argument checks, kernel choice, grouped
+// tables, error reporting.  No device memory is allocated here.
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+
+#include <string>
+
+#include "lrq.h"
+#include "lrq_device.hpp"
+#include "lrq_internal.hpp"
+
+namespace lrq {
+hipError_t launch_fp8(const LaunchCfg&, const Desc&, const Desc*, const uint32_t*, int64_t, hipStream_t);
+hipError_t launch_mx(const LaunchCfg&, const Desc&, const Desc*, const uint32_t*, int64_t, hipStream_t);
+}  // namespace lrq
+
+using lrq::Desc;
+using lrq::LaunchCfg;
+
+namespace {
+
+thread_local std::string g_err;
+
+int fail(int code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  g_err = buf;
+  return code;
+}
+
+int check_hip(hipError_t e, const char* what) {
+  if (e == hipSuccess) return 0;
+  return fail((int)e, "%s: %s", what, hipGetErrorString(e));
+}
+
+int64_t esize(int dt) { return dt == lrq::kF32 ? 4 : 2; }
+bool aligned(const void* p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
+bool valid_dtype(int dt) { return dt == lrq::kBF16 || dt == lrq::kF16 || dt == lrq::kF32; }
+bool pow2_block(int64_t b) { return b == 32 || b == 64 || b == 128 || b == 256 || b == 512; }
+
+constexpr uint32_t kMagic = 0x4C525154u;  // "LRQT"
+constexpr uint32_t kTableVersion = 1u;
+constexpr int64_t kMaxGrid = 0x7FFFFFFF;
+
+struct GroupHeader {
+  uint32_t magic, version;
+  LaunchCfg cfg;
+  int64_t n, units, desc_off, map_off, bytes;
+};
+
+int64_t align_up(int64_t x, int64_t a) { return (x + a - 1) / a * a; }
+
+// Fill a Desc from a tensor and check its shape.
+int make_desc(const lrq_tensor& t, Desc& d) {
+  if (t.batch < 0 || t.rows < 0 || t.cols < 0) return fail(LRQ_ERR_ARG, "negative extent");
+  if (t.batch == 0 || t.rows == 0 || t.cols == 0) {
+    memset(&d, 0, sizeof(d));
+    d.batch = t.batch; d.rows = t.rows; d.cols = t.cols;
+    return 0;
+  }
+  if (t.ld < t.cols) return fail(LRQ_ERR_ARG, "ld (%lld) < cols (%lld)", (long long)t.ld, (long long)t.cols);
+  if (t.batch > 1 && t.batch_stride < (t.rows - 1) * t.ld + t.cols)
+    return fail(LRQ_ERR_ARG, "batch_stride (%lld) overlaps matrices", (long long)t.batch_stride);
+  if (!t.in || !t.codes || !t.scales) return fail(LRQ_ERR_ARG, "null pointer");
+  memset(&d, 0, sizeof(d));
+  d.in = t.in;
+  d.codes = static_cast<uint8_t*>(t.codes);
+  d.scales = t.scales;
+  d.batch = t.batch; d.rows = t.rows; d.cols = t.cols; d.ld = t.ld;
+  d.bstride = t.batch > 1 ? t.batch_stride : t.rows * t.ld;
+  return 0;
+}
+
+// Fold the batch into rows when matrices are evenly spaced (1-D kernels).
+bool fold_batch(Desc& d) {
+  if (d.batch == 1) return true;
+  if (d.bstride != d.rows * d.ld) return false;
+  d.rows *= d.batch;
+  d.batch = 1;
+  d.bstride = d.rows * d.ld;
+  return true;
+}
+
+int fp8_kernel_for(const Desc& d, int in_dtype, int64_t blk_r, int64_t blk_c) {
+  const int64_t es = esize(in_dtype);
+  const bool vec = aligned(d.in, 16) && (d.ld * es) % 16 == 0 &&
+                   (d.batch == 1 || (d.bstride * es) % 16 == 0) && aligned(d.codes, 8) &&
+                   d.cols % 8 == 0;
+  if (blk_r == 128 && blk_c == 128 && vec) return lrq::kKernTile128;
+  if (blk_r == 1 && pow2_block(blk_c) && d.cols % blk_c == 0 && vec &&
+      (d.batch == 1 || d.bstride == d.rows * d.ld))
+    return lrq::kKernRowQuad;
+  return lrq::kKernGenericFp8;
+}
+
+int mx_kernel_for(const Desc& d, int in_dtype, int fmt) {
+  const int64_t es = esize(in_dtype);
+  const bool vec = aligned(d.in, 16) && (d.ld * es) % 16 == 0 &&
+                   (d.batch == 1 || d.bstride == d.rows * d.ld) &&
+                   aligned(d.codes, fmt == 8 ? 8 : 4);
+  return vec ? lrq::kKernMx : lrq::kKernGenericMx;
+}
+
+}  // namespace
+
+namespace lrq {
+
+bool plan_units(const LaunchCfg& cfg, Desc& d) {
+  if (d.batch == 0 || d.rows == 0 || d.cols == 0) {
+    d.units = 0;
+    return true;
+  }
+  switch (cfg.kernel) {
+    case kKernTile128:
+    case kKernGenericFp8:
+      d.units_r = (d.rows + cfg.blk_r - 1) / cfg.blk_r;
+      d.units_c = (d.cols + cfg.blk_c - 1) / cfg.blk_c;
+      d.units = d.batch * d.units_r * d.units_c;
+      return true;
+    case kKernRowQuad:
+      if (!fold_batch(d)) return false;
+      d.bpr = d.cols / cfg.blk_c;
+      d.nblocks = d.rows * d.bpr;
+      d.units = (d.nblocks + 63) / 64;
+      return true;
+    case kKernMx:
+    case kKernGenericMx:
+      if (!fold_batch(d)) {
+        // generic MX walks rows through `ld` only; a ragged batch stride is
+        // handled by the caller (one launch per matrix)
+        return false;
+      }
+      d.bpr = d.cols / 32;
+      d.nblocks = d.rows * d.bpr;
+      d.units = (d.nblocks + 255) / 256;
+      return true;
+  }
+  return false;
+}
+
+hipError_t launch(const LaunchCfg& cfg, const Desc& single, const Desc* descs_dev,
+                  const uint32_t* map_dev, int64_t total_units, hipStream_t stream) {
+  if (cfg.kernel == kKernMx || cfg.kernel == kKernGenericMx)
+    return launch_mx(cfg, single, descs_dev, map_dev, total_units, stream);
+  return launch_fp8(cfg, single, descs_dev, map_dev, total_units, stream);
+}
+
+}  // namespace lrq
+
+namespace {
+
+int run_single(const LaunchCfg& cfg, Desc& d, hipStream_t stream) {
+  if (!lrq::plan_units(cfg, d))
+    return fail(LRQ_ERR_ARG, "batch stride must equal rows*ld for this format");
+  if (d.units == 0) return 0;
+  if (d.units > kMaxGrid) return fail(LRQ_ERR_ARG, "tensor too large for one launch");
+  d.unit0 = 0;
+  return check_hip(lrq::launch(cfg, d, nullptr, nullptr, d.units, stream), "kernel launch");
+}
+
+int mx_quant(int fmt, const void* in, int in_dtype, int64_t rows, int64_t cols, int64_t ld,
+             uint8_t* codes, uint8_t* scales, hipStream_t stream) {
+  g_err.clear();
+  if (!valid_dtype(in_dtype)) return fail(LRQ_ERR_ARG, "bad input dtype %d", in_dtype);
+  if (cols % 32 != 0) return fail(LRQ_ERR_ARG, "cols (%lld) must be a multiple of 32", (long long)cols);
+  lrq_tensor t{in, codes, scales, 1, rows, cols, ld, rows * ld};
+  Desc d;
+  if (int rc = make_desc(t, d)) return rc;
+  LaunchCfg cfg{};
+  cfg.in_dtype = in_dtype;
+  cfg.mx_fmt = fmt;
+  cfg.kernel = mx_kernel_for(d, in_dtype, fmt);
+  return run_single(cfg, d, stream);
+}
+
+int64_t table_layout(int64_t n, int64_t units, int64_t* desc_off, int64_t* map_off) {
+  const int64_t h = align_up((int64_t)sizeof(GroupHeader), 256);
+  *desc_off = h;
+  *map_off = align_up(h + n * (int64_t)sizeof(Desc), 256);
+  return *map_off + units * 4;
+}
+
+// Build the launch configuration and descriptors for a group; `ds` may be null
+// (sizing only).  Returns 0 or an error; *units_out = total work-groups.
+int plan_group(int fmt, const lrq_tensor* ts, int64_t n, int in_dtype, int64_t blk_r,
+               int64_t blk_c, unsigned flags, LaunchCfg* cfg_out, Desc* ds, int64_t* units_out) {
+  if (n < 0 || (n > 0 && !ts)) return fail(LRQ_ERR_ARG, "bad tensor list");
+  if (!valid_dtype(in_dtype)) return fail(LRQ_ERR_ARG, "bad input dtype %d", in_dtype);
+  LaunchCfg cfg{};
+  cfg.in_dtype = in_dtype;
+  if (fmt == LRQ_FMT_FP8_BLOCK) {
+    if (blk_r < 1 || blk_c < 1 || blk_r > (1 << 20) || blk_c > (1 << 20))
+      return fail(LRQ_ERR_ARG, "bad block %lldx%lld", (long long)blk_r, (long long)blk_c);
+    cfg.blk_r = (int)blk_r;
+    cfg.blk_c = (int)blk_c;
+    cfg.pow2 = (flags & LRQ_FLAG_POW2_SCALE) ? 1 : 0;
+    cfg.arith = (flags & LRQ_FLAG_NATIVE_ARITH) && in_dtype != lrq::kF32 ? 1 : 0;
+    cfg.scale_bf16 = (flags & LRQ_FLAG_SCALE_BF16) && !cfg.arith ? 1 : 0;
+  } else if (fmt == LRQ_FMT_MXFP8 || fmt == LRQ_FMT_MXFP4) {
+    cfg.mx_fmt = fmt == LRQ_FMT_MXFP8 ? 8 : 4;
+  } else {
+    return fail(LRQ_ERR_ARG, "bad format %d", fmt);
+  }
+  int kernel = -1;
+  int64_t units = 0;
+  for (int64_t i = 0; i < n; ++i) {
+    Desc d;
+    if (int rc = make_desc(ts[i], d)) return fail(rc, "tensor %lld: %s", (long long)i, g_err.c_str());
+    if (d.batch == 0 || d.rows == 0 || d.cols == 0) {
+      if (ds) { ds[i] = d; ds[i].unit0 = units; ds[i].units = 0; }
+      continue;
+    }
+    int k;
+    if (fmt == LRQ_FMT_FP8_BLOCK) {
+      k = fp8_kernel_for(d, in_dtype, blk_r, blk_c);
+    } else {
+      if (d.cols % 32 != 0) return fail(LRQ_ERR_ARG, "tensor %lld: cols %% 32 != 0", (long long)i);
+      k = mx_kernel_for(d, in_dtype, cfg.mx_fmt);
+    }
+    if (kernel < 0) kernel = k;
+    if (k != kernel)
+      return fail(LRQ_ERR_ARG, "tensor %lld needs a different kernel than tensor 0 "
+                  "(alignment/shape); group it separately", (long long)i);
+    cfg.kernel = k;
+    if (!lrq::plan_units(cfg, d))
+      return fail(LRQ_ERR_ARG, "tensor %lld: batch stride must equal rows*ld", (long long)i);
+    d.unit0 = units;
+    units += d.units;
+    if (ds) ds[i] = d;
+  }
+  if (kernel < 0) cfg.kernel = fmt == LRQ_FMT_FP8_BLOCK ? lrq::kKernGenericFp8 : lrq::kKernGenericMx;
+  if (units > kMaxGrid) return fail(LRQ_ERR_ARG, "group too large for one launch");
+  *cfg_out = cfg;
+  *units_out = units;
+  return 0;
+}
+
+}  // namespace
+
+extern "C" {
+
+int lrq_fp8_block_quant(const void* in, int in_dtype, int64_t batch, int64_t rows, int64_t cols,
+                        int64_t ld, int64_t batch_stride, int64_t blk_r, int64_t blk_c,
+                        uint8_t* codes, void* scales, unsigned flags, lrq_stream_t stream) {
+  g_err.clear();
+  lrq_tensor t{in, codes, scales, batch, rows, cols, ld, batch_stride};
+  LaunchCfg cfg;
+  Desc d;
+  int64_t units;
+  if (int rc = plan_group(LRQ_FMT_FP8_BLOCK, &t, 1, in_dtype, blk_r, blk_c, flags, &cfg, &d, &units))
+    return rc;
+  if (units == 0) return 0;
+  d.unit0 = 0;
+  return check_hip(lrq::launch(cfg, d, nullptr, nullptr, units, (hipStream_t)stream), "kernel launch");
+}
+
+int lrq_fp8_block_dequant(const uint8_t* codes, const void* scales, int scale_dtype,
+                          int64_t batch, int64_t rows, int64_t cols, int64_t blk_r,
+                          int64_t blk_c, void* out, int out_dtype, lrq_stream_t stream) {
+  g_err.clear();
+  if (!valid_dtype(scale_dtype)) return fail(LRQ_ERR_ARG, "bad scale dtype %d", scale_dtype);
+  if (out_dtype != lrq::kF32 && out_dtype != lrq::kBF16) return fail(LRQ_ERR_ARG, "bad out dtype %d", out_dtype);
+  if (batch < 0 || rows < 0 || cols < 0 || blk_r < 1 || blk_c < 1 || blk_r > (1 << 20) || blk_c > (1 << 20))
+    return fail(LRQ_ERR_ARG, "bad shape or block");
+  if (batch * rows * cols == 0) return 0;
+  if (!codes || !scales || !out) return fail(LRQ_ERR_ARG, "null pointer");
+  return check_hip(lrq::launch_dequant(codes, scales, scale_dtype, batch, rows, cols, (int)blk_r,
+                                       (int)blk_c, out, out_dtype, (hipStream_t)stream),
+                   "kernel launch");
+}
+
+int lrq_mxfp8_quant(const void* in, int in_dtype, int64_t rows, int64_t cols, int64_t ld,
+                    uint8_t* codes, uint8_t* scales, lrq_stream_t stream) {
+  return mx_quant(8, in, in_dtype, rows, cols, ld, codes, scales, (hipStream_t)stream);
+}
+
+int lrq_mxfp4_quant(const void* in, int in_dtype, int64_t rows, int64_t cols, int64_t ld,
+                    uint8_t* codes, uint8_t* scales, lrq_stream_t stream) {
+  return mx_quant(4, in, in_dtype, rows, cols, ld, codes, scales, (hipStream_t)stream);
+}
+
+int64_t lrq_group_table_bytes(int fmt, const lrq_tensor* tensors, int64_t n, int in_dtype,
+                              int64_t blk_r, int64_t blk_c, unsigned flags) {
+  g_err.clear();
+  LaunchCfg cfg;
+  int64_t units;
+  if (int rc = plan_group(fmt, tensors, n, in_dtype, blk_r, blk_c, flags, &cfg, nullptr, &units))
+    return rc;
+  int64_t a, b;
+  return table_layout(n, units, &a, &b);
+}
+
+int lrq_group_pack(int fmt, const lrq_tensor* tensors, int64_t n, int in_dtype, int64_t blk_r,
+                   int64_t blk_c, unsigned flags, void* host_table, int64_t capacity) {
+  g_err.clear();
+  if (!host_table) return fail(LRQ_ERR_ARG, "null table");
+  LaunchCfg cfg;
+  int64_t units;
+  if (int rc = plan_group(fmt, tensors, n, in_dtype, blk_r, blk_c, flags, &cfg, nullptr, &units))
+    return rc;
+  GroupHeader h{};
+  const int64_t bytes = table_layout(n, units, &h.desc_off, &h.map_off);
+  if (capacity < bytes)
+    return fail(LRQ_ERR_CAPACITY, "table needs %lld bytes, have %lld", (long long)bytes, (long long)capacity);
+  char* base = static_cast<char*>(host_table);
+  memset(base, 0, (size_t)h.map_off);
+  Desc* ds = reinterpret_cast<Desc*>(base + h.desc_off);
+  if (int rc = plan_group(fmt, tensors, n, in_dtype, blk_r, blk_c, flags, &cfg, ds, &units)) return rc;
+  uint32_t* map = reinterpret_cast<uint32_t*>(base + h.map_off);
+  for (int64_t i = 0; i < n; ++i)
+    for (int64_t w = 0; w < ds[i].units; ++w) map[ds[i].unit0 + w] = (uint32_t)i;
+  h.magic = kMagic;
+  h.version = kTableVersion;
+  h.cfg = cfg;
+  h.n = n;
+  h.units = units;
+  h.bytes = bytes;
+  memcpy(base, &h, sizeof(h));
+  return 0;
+}
+
+int lrq_quant_grouped(const void* host_table, const void* device_table, lrq_stream_t stream) {
+  g_err.clear();
+  if (!host_table || !device_table) return fail(LRQ_ERR_ARG, "null table");
+  GroupHeader h;
+  memcpy(&h, host_table, sizeof(h));
+  if (h.magic != kMagic || h.version != kTableVersion) return fail(LRQ_ERR_TABLE, "not an lrq table");
+  if (h.units == 0) return 0;
+  const char* dev = static_cast<const char*>(device_table);
+  const Desc* descs = reinterpret_cast<const Desc*>(dev + h.desc_off);
+  const uint32_t* map = reinterpret_cast<const uint32_t*>(dev + h.map_off);
+  Desc dummy;
+  memset(&dummy, 0, sizeof(dummy));
+  return check_hip(lrq::launch(h.cfg, dummy, descs, map, h.units, (hipStream_t)stream), "kernel launch");
+}
+
+int64_t lrq_group_units(const void* host_table) {
+  GroupHeader h;
+  memcpy(&h, host_table, sizeof(h));
+  if (h.magic != kMagic || h.version != kTableVersion) return fail(LRQ_ERR_TABLE, "not an lrq table");
+  return h.units;
+}
+
+const char* lrq_version(void) { return "lrq 0.1.0 gfx950"; }
+const char* lrq_last_error(void) { return g_err.c_str(); }
+
+int lrq_diag_e4m3_bits(uint32_t start, int64_t n, uint8_t* out, lrq_stream_t stream) {
+  g_err.clear();
+  if (n <= 0 || n % 4 != 0 || !out || !aligned(out, 4)) return fail(LRQ_ERR_ARG, "bad diag args");
+  if ((n / 4 + 255) / 256 > kMaxGrid) return fail(LRQ_ERR_ARG, "n too large");
+  return check_hip(lrq::launch_diag_e4m3_bits(start, n, out, (hipStream_t)stream), "kernel launch");
+}
+
+int lrq_diag_e2m1(const float* in, uint8_t* out, int64_t n, lrq_stream_t stream) {
+  g_err.clear();
+  if (n <= 0 || !in || !out) return fail(LRQ_ERR_ARG, "bad diag args");
+  if ((n + 255) / 256 > kMaxGrid) return fail(LRQ_ERR_ARG, "n too large");
+  return check_hip(lrq::launch_diag_e2m1(in, out, n, (hipStream_t)stream), "kernel launch");
+}
+
+}  // extern "C"

@@ -1,0 +1,347 @@
+// FP8 E4M3 blockwise quantization kernels (gfx950, wave64).
+//
+// Restates WeightQuantizer.quantize_tensor
+// (lumenrl/quantization/weight_quantizer.py:40-77): per block amax -> /448 ->
+// clamp(tiny) -> [pow2] -> x/s -> float8_e4m3fn, in one HBM pass (bf16 in,
+// e4m3 + scale out).  Three kernels:
+//   k_tile128  : 128x128 tiles (the vLLM/ATOM `weight_scale_inv` layout), one
+//                256-thread work-group per tile, the tile held in VGPRs.
+//   k_rowquad  : 1xB row blocks (the reference's own layout), one quad of lanes
+//                per block, B/32 chunks of 8 elements per lane.
+//   k_generic  : any block shape, stride or alignment (one work-group per
+//                block, scalar loads); the fallback for odd inputs.
+// All of them share lrq_device.hpp's block_scale / block_quot / special_code.
+#include "lrq_device.hpp"
+#include "lrq_internal.hpp"
+
+namespace lrq {
+
+// 8 consecutive input elements.
+template <int DT>
+struct Chunk {
+  static constexpr int kWords = DT == kF32 ? 8 : 4;
+  uint32_t w[kWords];
+};
+
+template <int DT>
+__device__ __forceinline__ void load_chunk(Chunk<DT>& c, const void* base, int64_t off) {
+  if constexpr (DT == kF32) {
+    const uint4* p = reinterpret_cast<const uint4*>(static_cast<const float*>(base) + off);
+    uint4 a = p[0], b = p[1];
+    c.w[0] = a.x; c.w[1] = a.y; c.w[2] = a.z; c.w[3] = a.w;
+    c.w[4] = b.x; c.w[5] = b.y; c.w[6] = b.z; c.w[7] = b.w;
+  } else {
+    const uint4* p = reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(base) + off);
+    uint4 a = p[0];
+    c.w[0] = a.x; c.w[1] = a.y; c.w[2] = a.z; c.w[3] = a.w;
+  }
+}
+
+template <int DT>
+__device__ __forceinline__ void zero_chunk(Chunk<DT>& c) {
+#pragma unroll
+  for (int i = 0; i < Chunk<DT>::kWords; ++i) c.w[i] = 0u;
+}
+
+template <int DT>
+__device__ __forceinline__ float elem(const Chunk<DT>& c, int i) {
+  if constexpr (DT == kF32) return u2f(c.w[i]);
+  else if constexpr (DT == kBF16) return (i & 1) ? bf16_hi(c.w[i >> 1]) : bf16_lo(c.w[i >> 1]);
+  else return f16_to_f32((i & 1) ? (c.w[i >> 1] >> 16) : (c.w[i >> 1] & 0xFFFFu));
+}
+
+// Running amax: 16-bit inputs keep packed u16 maxima of |bits|, float32 keeps
+// the max of |bits|.  Magnitude bit patterns order like the values, with NaN
+// above inf, so integer max is an exact, NaN-detecting amax.
+template <int DT>
+struct Amax {
+  u16x2 m16;
+  uint32_t m32;
+  __device__ __forceinline__ void init() { m16 = u16x2{0, 0}; m32 = 0u; }
+  __device__ __forceinline__ void add(const Chunk<DT>& c) {
+    if constexpr (DT == kF32) {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        uint32_t a = c.w[i] & 0x7FFFFFFFu;
+        m32 = a > m32 ? a : m32;
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) m16 = amax_bf16x2(m16, c.w[i]);
+    }
+  }
+  // float32 bits of the amax (non-negative)
+  __device__ __forceinline__ uint32_t bits() const {
+    if constexpr (DT == kF32) return m32;
+    uint32_t a = m16.x > m16.y ? m16.x : m16.y;
+    if constexpr (DT == kBF16) return a << 16;
+    return f2u(f16_to_f32(a));
+  }
+};
+
+// 8 elements -> 8 e4m3 bytes (element 0 lowest).
+template <int DT, int CDT>
+__device__ __forceinline__ uint2 encode_chunk(const Chunk<DT>& c, const BlockScale& b) {
+  uint2 r;
+  if (b.kind == kScaleFast) {
+    float q[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) q[i] = block_quot<CDT>(elem<DT>(c, i), b);
+    r.x = cvt_e4m3x4(q[0], q[1], q[2], q[3]);
+    r.y = cvt_e4m3x4(q[4], q[5], q[6], q[7]);
+  } else if (b.kind == kScaleExact) {
+    float q[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) q[i] = block_quot<CDT>(elem<DT>(c, i), b);
+    r.x = cvt_e4m3x4(q[0], q[1], q[2], q[3]);
+    r.y = cvt_e4m3x4(q[4], q[5], q[6], q[7]);
+  } else {
+    uint32_t lo = 0u, hi = 0u;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      lo |= special_code<CDT>(elem<DT>(c, i), b) << (8 * i);
+      hi |= special_code<CDT>(elem<DT>(c, i + 4), b) << (8 * i);
+    }
+    r.x = lo;
+    r.y = hi;
+  }
+  return r;
+}
+
+template <int CDT>
+__device__ __forceinline__ void store_scale(void* scales, int64_t idx, float s, int scale_bf16) {
+  if (CDT == kF32 && !scale_bf16) {
+    static_cast<float*>(scales)[idx] = s;
+  } else {
+    uint32_t h = (CDT == kF16) ? f16_bits(s) : bf16_bits(s);
+    static_cast<uint16_t*>(scales)[idx] = (uint16_t)h;
+  }
+}
+
+__device__ __forceinline__ void pick_desc(const Desc& single, const Desc* descs,
+                                          const uint32_t* map, Desc& d, int64_t& u) {
+  if (map != nullptr) {
+    const uint32_t t = map[blockIdx.x];
+    d = descs[t];
+    u = (int64_t)blockIdx.x - d.unit0;
+  } else {
+    d = single;
+    u = blockIdx.x;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// 128x128 tiles.  Thread t owns column chunk (t & 15) of rows (t >> 4) + 16i,
+// i = 0..7: each load instruction of a wave reads 4 full 256-byte rows.
+// ---------------------------------------------------------------------------
+template <int DT, int CDT>
+__global__ __launch_bounds__(256) void k_tile128(Desc single, const Desc* __restrict__ descs,
+                                                 const uint32_t* __restrict__ map, int pow2,
+                                                 int scale_bf16) {
+  __shared__ uint32_t red[4];
+  Desc d;
+  int64_t u;
+  pick_desc(single, descs, map, d, u);
+
+  const int64_t per = d.units_r * d.units_c;
+  const int64_t b = u / per;
+  const int64_t rem = u - b * per;
+  const int64_t tr = rem / d.units_c;
+  const int64_t tc = rem - tr * d.units_c;
+  const int64_t r0 = tr * 128, c0 = tc * 128;
+  const int tid = threadIdx.x;
+  const int64_t col = c0 + (tid & 15) * 8;
+  const int rr = tid >> 4;
+  const int64_t in_base = b * d.bstride + (r0 + rr) * d.ld + col;
+  const int64_t out_base = (b * d.rows + r0 + rr) * d.cols + col;
+  const bool full = (r0 + 128 <= d.rows) && (c0 + 128 <= d.cols);
+  const bool col_ok = col < d.cols;
+
+  Chunk<DT> ch[8];
+  if (full) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) load_chunk<DT>(ch[i], d.in, in_base + (int64_t)(16 * i) * d.ld);
+  } else {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      if (col_ok && r0 + rr + 16 * i < d.rows) load_chunk<DT>(ch[i], d.in, in_base + (int64_t)(16 * i) * d.ld);
+      else zero_chunk<DT>(ch[i]);
+    }
+  }
+
+  Amax<DT> am;
+  am.init();
+#pragma unroll
+  for (int i = 0; i < 8; ++i) am.add(ch[i]);
+  uint32_t a = wave_max(am.bits());
+  if ((tid & 63) == 0) red[tid >> 6] = a;
+  __syncthreads();
+  a = red[0];
+  a = red[1] > a ? red[1] : a;
+  a = red[2] > a ? red[2] : a;
+  a = red[3] > a ? red[3] : a;
+
+  const BlockScale bs = block_scale<CDT>(a, pow2 != 0);
+  if (tid == 0) store_scale<CDT>(d.scales, u, bs.s, scale_bf16);
+
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const uint2 q = encode_chunk<DT, CDT>(ch[i], bs);
+    if (full || (col_ok && r0 + rr + 16 * i < d.rows))
+      *reinterpret_cast<uint2*>(d.codes + out_base + (int64_t)(16 * i) * d.cols) = q;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// 1xB row blocks, B = 32*CPL.  Quad q of the work-group takes block
+// 64u + q; lane p of the quad loads chunks p, p+4, ... of the block, so each
+// load instruction reads 64 contiguous bytes per quad.  Rows are folded over
+// the batch by the host; `ld` is the row stride.
+// ---------------------------------------------------------------------------
+template <int DT, int CDT, int CPL>
+__global__ __launch_bounds__(256) void k_rowquad(Desc single, const Desc* __restrict__ descs,
+                                                 const uint32_t* __restrict__ map, int pow2,
+                                                 int scale_bf16) {
+  constexpr int B = 32 * CPL;
+  Desc d;
+  int64_t u;
+  pick_desc(single, descs, map, d, u);
+  const int tid = threadIdx.x;
+  const int p = tid & 3;
+  const int64_t gb = u * 64 + (tid >> 2);
+  if (gb >= d.nblocks) return;  // whole quads leave together; no barriers below
+
+  int64_t in_base;
+  if (d.ld == d.cols) {
+    in_base = gb * B;
+  } else {
+    const int64_t row = gb / d.bpr;
+    in_base = row * d.ld + (gb - row * d.bpr) * B;
+  }
+  const int64_t out_base = gb * B;
+
+  Chunk<DT> ch[CPL];
+#pragma unroll
+  for (int j = 0; j < CPL; ++j) load_chunk<DT>(ch[j], d.in, in_base + (p + 4 * j) * 8);
+
+  Amax<DT> am;
+  am.init();
+#pragma unroll
+  for (int j = 0; j < CPL; ++j) am.add(ch[j]);
+  const uint32_t a = quad_max(am.bits());
+
+  const BlockScale bs = block_scale<CDT>(a, pow2 != 0);
+  if (p == 0) store_scale<CDT>(d.scales, gb, bs.s, scale_bf16);
+#pragma unroll
+  for (int j = 0; j < CPL; ++j) {
+    const uint2 q = encode_chunk<DT, CDT>(ch[j], bs);
+    *reinterpret_cast<uint2*>(d.codes + out_base + (p + 4 * j) * 8) = q;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Generic: one work-group per block of any shape; scalar loads; edge blocks
+// partial.  Unit u = (b, tile row, tile col) row-major = the scale index.
+// ---------------------------------------------------------------------------
+template <int DT>
+__device__ __forceinline__ float load_elem(const void* base, int64_t off) {
+  if constexpr (DT == kF32) return static_cast<const float*>(base)[off];
+  else if constexpr (DT == kBF16) return u2f((uint32_t)static_cast<const uint16_t*>(base)[off] << 16);
+  else return f16_to_f32(static_cast<const uint16_t*>(base)[off]);
+}
+
+template <int DT, int CDT>
+__global__ __launch_bounds__(256) void k_generic(Desc single, const Desc* __restrict__ descs,
+                                                 const uint32_t* __restrict__ map, int pow2,
+                                                 int scale_bf16, int blk_r, int blk_c) {
+  __shared__ uint32_t red[4];
+  Desc d;
+  int64_t u;
+  pick_desc(single, descs, map, d, u);
+  const int64_t per = d.units_r * d.units_c;
+  const int64_t b = u / per;
+  const int64_t rem = u - b * per;
+  const int64_t tr = rem / d.units_c;
+  const int64_t tc = rem - tr * d.units_c;
+  const int64_t r0 = tr * blk_r, c0 = tc * blk_c;
+  const int64_t nr = (r0 + blk_r <= d.rows ? blk_r : d.rows - r0);
+  const int64_t nc = (c0 + blk_c <= d.cols ? blk_c : d.cols - c0);
+  const int64_t n = nr * nc;
+  const int tid = threadIdx.x;
+
+  uint32_t a = 0u;
+  for (int64_t i = tid; i < n; i += 256) {
+    const int64_t r = r0 + i / nc, c = c0 + i % nc;
+    const uint32_t v = f2u(load_elem<DT>(d.in, b * d.bstride + r * d.ld + c)) & 0x7FFFFFFFu;
+    a = v > a ? v : a;
+  }
+  a = wave_max(a);
+  if ((tid & 63) == 0) red[tid >> 6] = a;
+  __syncthreads();
+  a = red[0];
+  a = red[1] > a ? red[1] : a;
+  a = red[2] > a ? red[2] : a;
+  a = red[3] > a ? red[3] : a;
+
+  const BlockScale bs = block_scale<CDT>(a, pow2 != 0);
+  if (tid == 0) store_scale<CDT>(d.scales, u, bs.s, scale_bf16);
+  for (int64_t i = tid; i < n; i += 256) {
+    const int64_t r = r0 + i / nc, c = c0 + i % nc;
+    const float x = load_elem<DT>(d.in, b * d.bstride + r * d.ld + c);
+    const uint32_t code =
+        bs.kind <= kScaleExact ? sw_e4m3(block_quot<CDT>(x, bs)) : special_code<CDT>(x, bs);
+    d.codes[(b * d.rows + r) * d.cols + c] = (uint8_t)code;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// host-side dispatch
+// ---------------------------------------------------------------------------
+template <int DT, int CDT>
+static hipError_t launch_fp8_typed(const LaunchCfg& cfg, const Desc& single, const Desc* descs,
+                                   const uint32_t* map, int64_t units, hipStream_t stream) {
+  const dim3 grid((unsigned)units), block(256);
+  switch (cfg.kernel) {
+    case kKernTile128:
+      hipLaunchKernelGGL((k_tile128<DT, CDT>), grid, block, 0, stream, single, descs, map,
+                         cfg.pow2, cfg.scale_bf16);
+      break;
+    case kKernRowQuad:
+      switch (cfg.blk_c) {
+        case 32: hipLaunchKernelGGL((k_rowquad<DT, CDT, 1>), grid, block, 0, stream, single, descs, map, cfg.pow2, cfg.scale_bf16); break;
+        case 64: hipLaunchKernelGGL((k_rowquad<DT, CDT, 2>), grid, block, 0, stream, single, descs, map, cfg.pow2, cfg.scale_bf16); break;
+        case 128: hipLaunchKernelGGL((k_rowquad<DT, CDT, 4>), grid, block, 0, stream, single, descs, map, cfg.pow2, cfg.scale_bf16); break;
+        case 256: hipLaunchKernelGGL((k_rowquad<DT, CDT, 8>), grid, block, 0, stream, single, descs, map, cfg.pow2, cfg.scale_bf16); break;
+        case 512: hipLaunchKernelGGL((k_rowquad<DT, CDT, 16>), grid, block, 0, stream, single, descs, map, cfg.pow2, cfg.scale_bf16); break;
+        default: return hipErrorInvalidValue;
+      }
+      break;
+    case kKernGenericFp8:
+      hipLaunchKernelGGL((k_generic<DT, CDT>), grid, block, 0, stream, single, descs, map,
+                         cfg.pow2, cfg.scale_bf16, cfg.blk_r, cfg.blk_c);
+      break;
+    default:
+      return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
+hipError_t launch_fp8(const LaunchCfg& cfg, const Desc& single, const Desc* descs,
+                      const uint32_t* map, int64_t units, hipStream_t stream) {
+  if (cfg.arith == 0) {
+    switch (cfg.in_dtype) {
+      case kBF16: return launch_fp8_typed<kBF16, kF32>(cfg, single, descs, map, units, stream);
+      case kF16: return launch_fp8_typed<kF16, kF32>(cfg, single, descs, map, units, stream);
+      case kF32: return launch_fp8_typed<kF32, kF32>(cfg, single, descs, map, units, stream);
+    }
+  } else {
+    switch (cfg.in_dtype) {
+      case kBF16: return launch_fp8_typed<kBF16, kBF16>(cfg, single, descs, map, units, stream);
+      case kF16: return launch_fp8_typed<kF16, kF16>(cfg, single, descs, map, units, stream);
+      case kF32: return launch_fp8_typed<kF32, kF32>(cfg, single, descs, map, units, stream);
+    }
+  }
+  return hipErrorInvalidValue;
+}
+
+}  // namespace lrq

@@ -1,0 +1,63 @@
+// Internal launch interface shared by the kernel files and the C-ABI layer.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace lrq {
+
+// One tensor of a launch: `batch` matrices of [rows, cols], input row stride
+// `ld` and matrix stride `bstride` (elements); codes and scales are dense.
+// For a grouped launch `unit0` is the first work-group of this tensor.
+struct Desc {
+  const void* in;
+  uint8_t* codes;
+  void* scales;
+  int64_t batch, rows, cols, ld, bstride;
+  int64_t unit0;
+  int64_t units;     // work-groups of this tensor
+  int64_t units_c;   // tile kernel: tiles per row band; row/MX kernels: unused
+  int64_t units_r;   // tile kernel: tile rows per matrix
+  int64_t nblocks;   // row/MX kernels: number of blocks/groups
+  int64_t bpr;       // row/MX kernels: blocks (groups) per row
+};
+static_assert(sizeof(Desc) == 112, "Desc layout is part of the grouped table format");
+
+enum Kernel : int {
+  kKernTile128 = 0,   // 128x128 FP8 tiles, one work-group per tile
+  kKernRowQuad = 1,   // 1xB FP8 blocks, one quad per block
+  kKernGenericFp8 = 2,
+  kKernMx = 3,        // MXFP8 / MXFP4, one quad per 32-group
+  kKernGenericMx = 4,
+};
+
+// Launch parameters common to every tensor of one launch.
+struct LaunchCfg {
+  int kernel;     // Kernel
+  int in_dtype;   // kBF16 / kF16 / kF32
+  int arith;      // 0: float32 arithmetic, 1: input dtype's arithmetic
+  int pow2;       // pow2 scale rounding
+  int blk_r, blk_c;
+  int mx_fmt;     // 8 or 4
+  int scale_bf16; // FP8 kernels: write the float32 scales rounded to bf16
+};
+
+// Work-groups a tensor needs under `cfg` (filled into d.units and the unit
+// geometry fields).  Returns false if the kernel cannot take the tensor.
+bool plan_units(const LaunchCfg& cfg, Desc& d);
+
+// Enqueue one launch over `n` descriptors.  Single tensor: descs_dev == null
+// and `single` is passed by value.  Grouped: descs_dev/map_dev are device
+// arrays (map_dev[wg] = descriptor index) and total_units work-groups run.
+hipError_t launch(const LaunchCfg& cfg, const Desc& single, const Desc* descs_dev,
+                  const uint32_t* map_dev, int64_t total_units, hipStream_t stream);
+
+hipError_t launch_dequant(const uint8_t* codes, const void* scales, int scale_dtype,
+                          int64_t batch, int64_t rows, int64_t cols, int blk_r, int blk_c,
+                          void* out, int out_dtype, hipStream_t stream);
+
+// Diagnostics: element encoders applied to raw inputs.
+hipError_t launch_diag_e4m3_bits(uint32_t start, int64_t n, uint8_t* out, hipStream_t stream);
+hipError_t launch_diag_e2m1(const float* in, uint8_t* out, int64_t n, hipStream_t stream);
+
+}  // namespace lrq

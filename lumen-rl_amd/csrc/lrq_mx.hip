@@ -1,0 +1,243 @@
+// MXFP8 / MXFP4 quantization kernels (OCP Microscaling v1.0), gfx950 wave64.
+//
+// No counterpart kernel exists in the reference tree: LumenRL hands MX weights
+// to vLLM/ATOM/aiter (`quantization: mxfp4`,
+// examples/Qwen3_8B_SDDD_MI350_vLLM/configs/opd_qwen3_8b.yaml:43;
+// aiter quant_mxfp8, examples/DAPO/atom_aiter_shim/sitecustomize.py:31-32).
+// Per 1x32 group along the last dim: E8M0 = clamp(floor(log2 amax) - emax +
+// 127, 0, 254) (0xFF for inf/NaN groups); elements x * 2^(127-E8M0) rounded to
+// nearest even, saturating (E4M3 +-448, E2M1 +-6).
+//
+// k_mx: a quad of lanes per group (8 elements per lane); wave w of the
+// work-group takes groups 256u + 64w + 16j + (lane>>2), j = 0..3, so each load
+// instruction of a wave reads 16 whole groups = 1 KiB contiguous.
+#include "lrq_device.hpp"
+#include "lrq_internal.hpp"
+
+namespace lrq {
+
+template <int DT>
+__device__ __forceinline__ void mx_load8(const void* base, int64_t off, uint32_t (&w)[8]) {
+  if constexpr (DT == kF32) {
+    const uint4* p = reinterpret_cast<const uint4*>(static_cast<const float*>(base) + off);
+    uint4 a = p[0], b = p[1];
+    w[0] = a.x; w[1] = a.y; w[2] = a.z; w[3] = a.w;
+    w[4] = b.x; w[5] = b.y; w[6] = b.z; w[7] = b.w;
+  } else {
+    const uint4* p = reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(base) + off);
+    uint4 a = p[0];
+    w[0] = a.x; w[1] = a.y; w[2] = a.z; w[3] = a.w;
+  }
+}
+
+template <int DT>
+__device__ __forceinline__ float mx_elem(const uint32_t (&w)[8], int i) {
+  if constexpr (DT == kF32) return u2f(w[i]);
+  else if constexpr (DT == kBF16) return (i & 1) ? bf16_hi(w[i >> 1]) : bf16_lo(w[i >> 1]);
+  else return f16_to_f32((i & 1) ? (w[i >> 1] >> 16) : (w[i >> 1] & 0xFFFFu));
+}
+
+template <int DT>
+__device__ __forceinline__ uint32_t mx_amax8(const uint32_t (&w)[8]) {
+  if constexpr (DT == kF32) {
+    uint32_t m = 0u;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const uint32_t a = w[i] & 0x7FFFFFFFu;
+      m = a > m ? a : m;
+    }
+    return m;
+  } else {
+    u16x2 m = u16x2{0, 0};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) m = amax_bf16x2(m, w[i]);
+    const uint32_t a = m.x > m.y ? m.x : m.y;
+    if constexpr (DT == kBF16) return a << 16;
+    return f2u(f16_to_f32(a));
+  }
+}
+
+// 8 elements of a finite group -> E4M3 bytes (8) or E2M1 nibbles (8 in a dword).
+template <int DT, int FMT>
+__device__ __forceinline__ uint2 mx_encode8(const uint32_t (&w)[8], uint32_t e8m0) {
+  uint2 r;
+  if (e8m0 != 0xFFu) {
+    const float mult = mx_mult(e8m0);
+    float v[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) v[i] = mx_elem<DT>(w, i) * mult;
+    if constexpr (FMT == 8) {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) v[i] = __builtin_amdgcn_fmed3f(v[i], -448.0f, 448.0f);
+      r.x = cvt_e4m3x4(v[0], v[1], v[2], v[3]);
+      r.y = cvt_e4m3x4(v[4], v[5], v[6], v[7]);
+    } else {
+      uint32_t n = 0u;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) n |= e2m1_code(v[i]) << (4 * i);
+      r.x = n;
+      r.y = 0u;
+    }
+  } else {
+    // inf/NaN group: E4M3 NaN|sign for inf/NaN elements, +-0 otherwise;
+    // E2M1 has no NaN: +-0 for every element.
+    uint32_t lo = 0u, hi = 0u;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const uint32_t u = f2u(mx_elem<DT>(w, i));
+      uint32_t c;
+      if constexpr (FMT == 8) {
+        c = ((u >> 24) & 0x80u) | ((u & 0x7FFFFFFFu) >= 0x7F800000u ? 0x7Fu : 0u);
+        if (i < 4) lo |= c << (8 * i);
+        else hi |= c << (8 * (i - 4));
+      } else {
+        c = (u >> 28) & 0x8u;
+        lo |= c << (4 * i);
+      }
+    }
+    r.x = lo;
+    r.y = hi;
+  }
+  return r;
+}
+
+template <int DT, int FMT>
+__global__ __launch_bounds__(256) void k_mx(Desc single, const Desc* __restrict__ descs,
+                                            const uint32_t* __restrict__ map) {
+  constexpr int kEmax = FMT == 8 ? 8 : 2;
+  Desc d;
+  int64_t u;
+  if (map != nullptr) {
+    const uint32_t t = map[blockIdx.x];
+    d = descs[t];
+    u = (int64_t)blockIdx.x - d.unit0;
+  } else {
+    d = single;
+    u = blockIdx.x;
+  }
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int p = lane & 3;
+  const int64_t g0 = u * 256 + (tid >> 6) * 64 + (lane >> 2);
+
+  uint32_t w[4][8];
+  bool ok[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int64_t g = g0 + 16 * j;
+    ok[j] = g < d.nblocks;
+    if (ok[j]) {
+      int64_t off;
+      if (d.ld == d.cols) {
+        off = g * 32 + p * 8;
+      } else {
+        const int64_t row = g / d.bpr;
+        off = row * d.ld + (g - row * d.bpr) * 32 + p * 8;
+      }
+      mx_load8<DT>(d.in, off, w[j]);
+    } else {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) w[j][i] = 0u;
+    }
+  }
+
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    // quads are either wholly in range or wholly out: the DPP stays in-quad
+    const uint32_t a = quad_max(mx_amax8<DT>(w[j]));
+    const uint32_t e = mx_e8m0<kEmax>(a);
+    if (!ok[j]) continue;
+    const int64_t g = g0 + 16 * j;
+    const uint2 c = mx_encode8<DT, FMT>(w[j], e);
+    if constexpr (FMT == 8) {
+      *reinterpret_cast<uint2*>(d.codes + g * 32 + p * 8) = c;
+    } else {
+      *reinterpret_cast<uint32_t*>(d.codes + g * 16 + p * 4) = c.x;
+    }
+    if (p == 0) static_cast<uint8_t*>(d.scales)[g] = (uint8_t)e;
+  }
+}
+
+// Generic: one thread per group, scalar loads, any stride/alignment.
+template <int DT, int FMT>
+__global__ __launch_bounds__(256) void k_mx_generic(Desc single, const Desc* __restrict__ descs,
+                                                    const uint32_t* __restrict__ map) {
+  constexpr int kEmax = FMT == 8 ? 8 : 2;
+  Desc d;
+  int64_t u;
+  if (map != nullptr) {
+    const uint32_t t = map[blockIdx.x];
+    d = descs[t];
+    u = (int64_t)blockIdx.x - d.unit0;
+  } else {
+    d = single;
+    u = blockIdx.x;
+  }
+  const int64_t g = u * 256 + threadIdx.x;
+  if (g >= d.nblocks) return;
+  const int64_t row = g / d.bpr;
+  const int64_t base = row * d.ld + (g - row * d.bpr) * 32;
+  float x[32];
+  uint32_t a = 0u;
+#pragma unroll
+  for (int i = 0; i < 32; ++i) {
+    if constexpr (DT == kF32) x[i] = static_cast<const float*>(d.in)[base + i];
+    else if constexpr (DT == kBF16) x[i] = u2f((uint32_t)static_cast<const uint16_t*>(d.in)[base + i] << 16);
+    else x[i] = f16_to_f32(static_cast<const uint16_t*>(d.in)[base + i]);
+    const uint32_t m = f2u(x[i]) & 0x7FFFFFFFu;
+    a = m > a ? m : a;
+  }
+  const uint32_t e = mx_e8m0<kEmax>(a);
+  static_cast<uint8_t*>(d.scales)[g] = (uint8_t)e;
+  const float mult = e != 0xFFu ? mx_mult(e) : 0.0f;
+  if constexpr (FMT == 8) {
+    uint8_t* out = d.codes + g * 32;
+    for (int i = 0; i < 32; ++i) {
+      const uint32_t ux = f2u(x[i]);
+      uint32_t c;
+      if (e == 0xFFu) c = ((ux >> 24) & 0x80u) | ((ux & 0x7FFFFFFFu) >= 0x7F800000u ? 0x7Fu : 0u);
+      else c = sw_e4m3(__builtin_amdgcn_fmed3f(x[i] * mult, -448.0f, 448.0f));
+      out[i] = (uint8_t)c;
+    }
+  } else {
+    uint8_t* out = d.codes + g * 16;
+    for (int i = 0; i < 32; i += 2) {
+      uint32_t lo, hi;
+      if (e == 0xFFu) {
+        lo = (f2u(x[i]) >> 28) & 0x8u;
+        hi = (f2u(x[i + 1]) >> 28) & 0x8u;
+      } else {
+        lo = e2m1_code(x[i] * mult);
+        hi = e2m1_code(x[i + 1] * mult);
+      }
+      out[i / 2] = (uint8_t)(lo | (hi << 4));
+    }
+  }
+}
+
+template <int DT>
+static hipError_t launch_mx_typed(const LaunchCfg& cfg, const Desc& single, const Desc* descs,
+                                  const uint32_t* map, int64_t units, hipStream_t stream) {
+  const dim3 grid((unsigned)units), block(256);
+  const bool gen = cfg.kernel == kKernGenericMx;
+  if (cfg.mx_fmt == 8) {
+    if (gen) hipLaunchKernelGGL((k_mx_generic<DT, 8>), grid, block, 0, stream, single, descs, map);
+    else hipLaunchKernelGGL((k_mx<DT, 8>), grid, block, 0, stream, single, descs, map);
+  } else {
+    if (gen) hipLaunchKernelGGL((k_mx_generic<DT, 4>), grid, block, 0, stream, single, descs, map);
+    else hipLaunchKernelGGL((k_mx<DT, 4>), grid, block, 0, stream, single, descs, map);
+  }
+  return hipGetLastError();
+}
+
+hipError_t launch_mx(const LaunchCfg& cfg, const Desc& single, const Desc* descs,
+                     const uint32_t* map, int64_t units, hipStream_t stream) {
+  switch (cfg.in_dtype) {
+    case kBF16: return launch_mx_typed<kBF16>(cfg, single, descs, map, units, stream);
+    case kF16: return launch_mx_typed<kF16>(cfg, single, descs, map, units, stream);
+    case kF32: return launch_mx_typed<kF32>(cfg, single, descs, map, units, stream);
+  }
+  return hipErrorInvalidValue;
+}
+
+}  // namespace lrq

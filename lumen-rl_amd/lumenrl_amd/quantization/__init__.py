@@ -1,0 +1,31 @@
+"""Weight quantization for trainer -> rollout weight sync (lumenrl/quantization mirror)."""
+
+from lumenrl_amd.quantization.fp8_config import (
+    FP8Config,
+    QuantizationConfig,
+    RolloutQuantConfig,
+    TrainingQuantConfig,
+)
+from lumenrl_amd.quantization.ops import (
+    QuantPlan,
+    quantize_fp8_blockwise,
+    quantize_mxfp4,
+    quantize_mxfp8,
+)
+from lumenrl_amd.quantization.ops import fp8_block_dequant, fp8_block_quant
+from lumenrl_amd.quantization.weight_quantizer import WeightQuantizer, fp8_e4m3_max
+
+__all__ = [
+    "FP8Config",
+    "QuantizationConfig",
+    "QuantPlan",
+    "RolloutQuantConfig",
+    "TrainingQuantConfig",
+    "WeightQuantizer",
+    "fp8_block_dequant",
+    "fp8_block_quant",
+    "fp8_e4m3_max",
+    "quantize_fp8_blockwise",
+    "quantize_mxfp4",
+    "quantize_mxfp8",
+]

@@ -1,0 +1,187 @@
+"""Drop-in ``WeightQuantizer`` running on MI355X HIP kernels.
+
+Mirrors lumenrl/quantization/weight_quantizer.py (same class, method names,
+arguments, return layouts and ValueError texts); the arithmetic runs in
+liblrq's kernels and is bit-identical to the reference evaluated by torch on an
+x86 CPU:
+
+* ``quantize_tensor`` on a float32 tensor computes in float32; on a bf16 or
+  fp16 tensor it computes in that dtype, as the reference's torch ops do
+  (:59-71).  NaN blocks in bf16 arithmetic give scale 0xFFFF and codes 0xFF
+  (torch's vectorized x86 kernels; its scalar tail loop writes 0x7FC0/0x7F).
+* ``quantize_state_dict`` upcasts to float32 (:109); for bf16/fp16 weights the
+  upcast is exact, so the kernel reads them directly in float32 arithmetic and
+  writes the bf16 ``_fp8_scales`` sidecar itself (:111).  All eligible weights
+  go through ONE grouped kernel launch.
+
+Tensors on the CPU are staged through the current HIP device and the results
+copied back, so the reference's CPU-tensor call sites keep working; there is no
+CPU compute path.  float64 tensors are accepted where the reference upcasts
+them (quantize_state_dict); ``quantize_tensor`` on float64 (float64 arithmetic
+in the reference) raises TypeError.
+"""
+
+from __future__ import annotations
+
+import logging
+from typing import Any
+
+import torch
+from torch import Tensor
+
+from lumenrl_amd.quantization import ops
+from lumenrl_amd.quantization.fp8_config import FP8Config
+
+logger = logging.getLogger(__name__)
+
+_FP8_DTYPE = getattr(torch, "float8_e4m3fn", None)
+
+
+def fp8_e4m3_max() -> float:
+    """weight_quantizer.py:18-21."""
+    if _FP8_DTYPE is not None:
+        return float(torch.finfo(_FP8_DTYPE).max)
+    return 448.0
+
+
+def _stage(t: Tensor) -> tuple[Tensor, torch.device | None]:
+    """Device copy of a CPU tensor (and the device to return results to)."""
+    if t.is_cuda:
+        return t, None
+    dev = ops.require_device()
+    return t.to(dev, non_blocking=False), t.device
+
+
+class WeightQuantizer:
+    """BF16 <-> FP8 (E4M3) blockwise transforms for ``state_dict`` tensors (:30-134)."""
+
+    def __init__(self, config: FP8Config) -> None:
+        self._config = config
+        if _FP8_DTYPE is None:  # pragma: no cover - torch 2.10 has it
+            raise RuntimeError("torch.float8_e4m3fn is required by lumenrl_amd")
+
+    # -- single tensors ------------------------------------------------------
+    def quantize_tensor(self, tensor: Tensor, block_size: int = 128) -> tuple[Tensor, Tensor]:
+        """Blockwise FP8 quantization along the last dimension (:40-77).
+
+        Returns ``(quantized, scales)``: ``quantized`` is float8_e4m3fn with the
+        input shape, ``scales`` has shape ``tensor.shape[:-1] + (last // block_size,)``
+        and the compute dtype (float32 for float32 input, else the input dtype).
+        """
+        if tensor.dim() < 1:
+            raise ValueError("quantize_tensor expects tensor.dim() >= 1")
+        last = tensor.shape[-1]
+        if last % block_size != 0:
+            raise ValueError(f"Last dim {last} must be divisible by block_size={block_size}")
+        if tensor.dtype == torch.float64:
+            raise TypeError("lumenrl_amd quantize_tensor computes in bf16/fp16/fp32; "
+                            "cast float64 tensors to float32 first")
+        x, home = _stage(tensor)
+        leading = 1
+        for d in tensor.shape[:-1]:
+            leading *= int(d)
+        flat = x.reshape(leading, last)
+        q, s = ops.fp8_block_quant(flat, (1, block_size), native_arith=True,
+                                   pow2=self._config.use_weight_pow2_scale)
+        q = q.reshape(tensor.shape)
+        s = s.reshape(tuple(tensor.shape[:-1]) + (last // block_size,))
+        if home is not None:
+            q, s = q.to(home), s.to(home)
+        return q, s
+
+    def dequantize_tensor(self, quantized: Tensor, scales: Tensor, block_size: int = 128) -> Tensor:
+        """Inverse of :meth:`quantize_tensor` for a single tensor (:79-89): float32 out."""
+        return self._dequant(quantized, scales, block_size, torch.float32)
+
+    def _dequant(self, quantized: Tensor, scales: Tensor, block_size: int,
+                 out_dtype: torch.dtype) -> Tensor:
+        last = quantized.shape[-1]
+        q, home = _stage(quantized)
+        s = scales.to(q.device)
+        if s.dtype == torch.float64:
+            s = s.to(torch.float32)
+        leading = 1
+        for d in quantized.shape[:-1]:
+            leading *= int(d)
+        qm = q.reshape(leading, last)
+        sm = s.reshape(leading, last // block_size)
+        out = ops.fp8_block_dequant(qm, sm, (1, block_size), out_dtype).reshape(quantized.shape)
+        return out.to(home) if home is not None else out
+
+    # -- state dicts ---------------------------------------------------------
+    @staticmethod
+    def _eligible(value: Any) -> bool:
+        """Pass-through rules of quantize_state_dict (:95-108)."""
+        if not isinstance(value, Tensor):
+            return False
+        if value.dtype not in (torch.bfloat16, torch.float16, torch.float32, torch.float64):
+            return False
+        if value.ndim != 2:
+            return False
+        if value.shape[1] % 128 != 0:
+            logger.debug("Skipping tensor: in_features=%s not aligned to 128", value.shape[1])
+            return False
+        return True
+
+    def quantize_state_dict(self, state_dict: dict[str, Tensor]) -> dict[str, Tensor | Any]:
+        """Return a new dict with 2-D float weights converted to FP8 + sidecar scales (:91-115)."""
+        staged: dict[str, tuple[Tensor, torch.device | None]] = {}
+        for key, value in state_dict.items():
+            if self._eligible(value):
+                x, home = _stage(value)
+                if x.dtype == torch.float64:
+                    x = x.to(torch.float32)  # the reference's own upcast (:109)
+                staged[key] = (x if x.is_contiguous() else x.contiguous(), home)
+
+        pow2 = self._config.use_weight_pow2_scale
+        results: dict[str, tuple[Tensor, Tensor]] = {}
+        # One grouped kernel launch per (dtype, device) for 16-byte aligned
+        # weights; anything else is quantized by a single launch.
+        groups: dict[tuple[torch.dtype, torch.device], list[str]] = {}
+        for key, (x, _) in staged.items():
+            if x.data_ptr() % 16 == 0 and x.numel() > 0:
+                groups.setdefault((x.dtype, x.device), []).append(key)
+            else:
+                results[key] = ops.fp8_block_quant(x, (1, 128), pow2=pow2,
+                                                   scale_dtype=torch.bfloat16)
+        for keys in groups.values():
+            plan = ops.QuantPlan([staged[k][0] for k in keys], "fp8_block", (1, 128),
+                                 use_pow2_scale=pow2, scale_dtype=torch.bfloat16)
+            plan.run()
+            results.update(zip(keys, plan.outputs))
+
+        out: dict[str, Tensor | Any] = {}
+        for key, value in state_dict.items():
+            if key not in staged:
+                out[key] = value
+                continue
+            x, home = staged[key]
+            q, s = results[key]
+            out_features, in_features = x.shape
+            s = s.reshape(out_features, in_features // 128)
+            if home is not None:
+                q, s = q.to(home), s.to(home)
+            out[key] = q
+            out[f"{key}_fp8_scales"] = s
+            out[f"{key}_fp8_meta"] = torch.tensor(
+                [out_features, in_features], dtype=torch.int64, device="cpu"
+            )
+        return out
+
+    def dequantize_state_dict(self, state_dict: dict[str, Tensor]) -> dict[str, Tensor | Any]:
+        """Strip FP8 tensors back to BF16 weights using stored scales (:117-134)."""
+        consumed_suffixes = {"_fp8_scales", "_fp8_meta"}
+        out: dict[str, Tensor | Any] = {}
+        for key, value in state_dict.items():
+            if any(key.endswith(sfx) for sfx in consumed_suffixes):
+                continue
+            if not isinstance(value, Tensor):
+                out[key] = value
+                continue
+            scale_key = f"{key}_fp8_scales"
+            if scale_key not in state_dict:
+                out[key] = value
+                continue
+            scales = state_dict[scale_key]
+            out[key] = self._dequant(value, scales.to(value.device), 128, torch.bfloat16)
+        return out

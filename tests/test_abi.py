@@ -1,0 +1,167 @@
+"""The C-ABI library (no GPU needed): loads, exports include/lrq.h, host-side logic.
+
+Only calls that return before touching the HIP runtime are made here:
+argument validation and the grouped-table packer, which works on host memory.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import re
+
+import numpy as np
+import pytest
+
+from conftest import ROOT
+from lumenrl_amd import _lib
+
+HEADER = os.path.join(ROOT, "include", "lrq.h")
+
+
+def declared_functions() -> list[str]:
+    txt = open(HEADER).read()
+    txt = re.sub(r"/\*.*?\*/", "", txt, flags=re.S)
+    return sorted(set(re.findall(r"\b(lrq_[a-z0-9_]+)\s*\(", txt)))
+
+
+def test_library_built_and_exports_every_declared_symbol():
+    assert os.path.exists(_lib.LIB_PATH), "run __graft_entry__.build() / make -C lumen-rl_amd"
+    L = ctypes.CDLL(_lib.LIB_PATH)
+    names = declared_functions()
+    assert len(names) >= 12
+    missing = [n for n in names if not hasattr(L, n)]
+    assert not missing
+    # the Python binding declares a signature for each of them
+    assert sorted(_lib.SIGNATURES) == names
+
+
+def test_library_targets_gfx950_only():
+    blob = open(_lib.LIB_PATH, "rb").read()
+    assert b"gfx950" in blob
+    for other in (b"gfx942", b"gfx90a", b"sm_"):
+        assert other not in blob
+
+
+def test_version():
+    assert _lib.version().startswith("lrq ") and "gfx950" in _lib.version()
+
+
+def L():
+    return _lib.lib()
+
+
+def test_argument_errors_need_no_device():
+    fake = ctypes.c_void_p(0x10000)
+    # bad dtype
+    rc = L().lrq_fp8_block_quant(fake, 7, 1, 4, 128, 128, 512, 1, 128, fake, fake, 0, None)
+    assert rc == _lib.ERR_ARG and "dtype" in _lib.last_error()
+    # negative extent
+    rc = L().lrq_fp8_block_quant(fake, 0, 1, -4, 128, 128, 512, 1, 128, fake, fake, 0, None)
+    assert rc == _lib.ERR_ARG
+    # ld < cols
+    rc = L().lrq_fp8_block_quant(fake, 0, 1, 4, 128, 64, 512, 1, 128, fake, fake, 0, None)
+    assert rc == _lib.ERR_ARG and "ld" in _lib.last_error()
+    # null pointer with work to do
+    rc = L().lrq_fp8_block_quant(None, 0, 1, 4, 128, 128, 512, 1, 128, fake, fake, 0, None)
+    assert rc == _lib.ERR_ARG
+    # bad block
+    rc = L().lrq_fp8_block_quant(fake, 0, 1, 4, 128, 128, 512, 0, 128, fake, fake, 0, None)
+    assert rc == _lib.ERR_ARG
+    # MX needs cols % 32
+    rc = L().lrq_mxfp8_quant(fake, 0, 4, 48, 48, fake, fake, None)
+    assert rc == _lib.ERR_ARG and "32" in _lib.last_error()
+    rc = L().lrq_mxfp4_quant(fake, 9, 4, 64, 64, fake, fake, None)
+    assert rc == _lib.ERR_ARG
+    # dequant dtypes
+    rc = L().lrq_fp8_block_dequant(fake, fake, 5, 1, 4, 128, 1, 128, fake, 2, None)
+    assert rc == _lib.ERR_ARG
+    rc = L().lrq_fp8_block_dequant(fake, fake, 2, 1, 4, 128, 1, 128, fake, 1, None)
+    assert rc == _lib.ERR_ARG
+    # empty work is a no-op success (no launch)
+    rc = L().lrq_fp8_block_quant(None, 0, 1, 0, 128, 128, 0, 1, 128, None, None, 0, None)
+    assert rc == 0
+    # diagnostics
+    assert L().lrq_diag_e4m3_bits(0, 6, fake, None) == _lib.ERR_ARG
+
+
+def _tensors(shapes, base=0x100000000, align=256):
+    arr = (_lib.LrqTensor * len(shapes))()
+    p = base
+    for i, (b, r, c) in enumerate(shapes):
+        arr[i].in_ = p
+        p += b * r * c * 2 + align
+        arr[i].codes = p
+        p += b * r * c + align
+        arr[i].scales = p
+        p += b * r * c + align
+        arr[i].batch, arr[i].rows, arr[i].cols = b, r, c
+        arr[i].ld, arr[i].batch_stride = c, r * c
+    return arr
+
+
+QWEN3_8B_LAYER = [(1, 4096, 4096), (1, 1024, 4096), (1, 1024, 4096), (1, 4096, 4096),
+                  (1, 12288, 4096), (1, 12288, 4096), (1, 4096, 12288)]
+
+
+def _pack(fmt, shapes, blk=(128, 128), flags=0):
+    ts = _tensors(shapes)
+    need = L().lrq_group_table_bytes(fmt, ts, len(shapes), 0, blk[0], blk[1], flags)
+    assert need > 0, _lib.last_error()
+    buf = np.zeros(need, np.uint8)
+    rc = L().lrq_group_pack(fmt, ts, len(shapes), 0, blk[0], blk[1], flags, buf.ctypes.data, need)
+    assert rc == 0, _lib.last_error()
+    return buf
+
+
+def test_group_pack_tiles_qwen3_layer():
+    buf = _pack(_lib.FMT_FP8_BLOCK, QWEN3_8B_LAYER)
+    units = L().lrq_group_units(buf.ctypes.data)
+    tiles = [(r // 128) * (c // 128) for _, r, c in QWEN3_8B_LAYER]
+    assert units == sum(tiles)
+    # the work-group -> tensor map is the tail of the table
+    wmap = buf[-4 * units:].view(np.uint32)
+    assert np.array_equal(wmap, np.repeat(np.arange(7, dtype=np.uint32), tiles))
+
+
+def test_group_pack_rows_and_mx_units():
+    shapes = [(1, 256, 4096), (1, 64, 12288)]
+    buf = _pack(_lib.FMT_FP8_BLOCK, shapes, (1, 128))
+    blocks = 256 * 32 + 64 * 96
+    assert L().lrq_group_units(buf.ctypes.data) == -(-256 * 32 // 64) + -(-64 * 96 // 64)
+    buf = _pack(_lib.FMT_MXFP4, shapes, (1, 32))
+    assert L().lrq_group_units(buf.ctypes.data) == -(-256 * 128 // 256) + -(-64 * 384 // 256)
+    del blocks
+
+
+def test_group_pack_expert_stack_single_descriptor():
+    buf = _pack(_lib.FMT_FP8_BLOCK, [(128, 768, 2048), (128, 2048, 768)])
+    assert L().lrq_group_units(buf.ctypes.data) == 128 * 6 * 16 + 128 * 16 * 6
+
+
+def test_group_pack_rejects_mixed_kernels_and_small_buffers():
+    ts = _tensors([(1, 256, 256), (1, 256, 256)])
+    ts[1].in_ = ts[1].in_ + 2  # misaligned: needs the generic kernel
+    need = L().lrq_group_table_bytes(_lib.FMT_FP8_BLOCK, ts, 2, 0, 128, 128, 0)
+    assert need == _lib.ERR_ARG and "kernel" in _lib.last_error()
+    ts = _tensors([(1, 256, 256)])
+    need = L().lrq_group_table_bytes(_lib.FMT_FP8_BLOCK, ts, 1, 0, 128, 128, 0)
+    buf = np.zeros(need - 1, np.uint8)
+    rc = L().lrq_group_pack(_lib.FMT_FP8_BLOCK, ts, 1, 0, 128, 128, 0, buf.ctypes.data, need - 1)
+    assert rc == _lib.ERR_CAPACITY
+
+
+def test_grouped_rejects_foreign_table():
+    junk = np.zeros(4096, np.uint8)
+    rc = L().lrq_quant_grouped(junk.ctypes.data, ctypes.c_void_p(0x1000), None)
+    assert rc == _lib.ERR_TABLE
+    assert L().lrq_group_units(junk.ctypes.data) == _lib.ERR_TABLE
+
+
+def test_check_maps_codes_to_exceptions():
+    with pytest.raises(ValueError):
+        _lib.check(_lib.ERR_ARG, "x")
+    with pytest.raises(_lib.LrqError):
+        _lib.check(_lib.ERR_TABLE, "x")
+    with pytest.raises(_lib.LrqError):
+        _lib.check(1, "x")

@@ -1,0 +1,393 @@
+"""Parity of the HIP kernels with the CPU oracle (bit-exact), on an MI355X.
+
+Sizes: golden fixtures and random cases at oracle-friendly sizes, BASELINE
+config 1 ([4096, 4096]) in full, one full Qwen3-8B layer through the grouped
+launch, exhaustive (x, amax) pairs over every bf16 value, and every float32
+bit pattern through the hardware e4m3 encoder.
+"""
+
+from __future__ import annotations
+
+import os
+
+import numpy as np
+import pytest
+import torch
+
+from conftest import ROOT, load_golden
+from oracle import oracle as O
+from lumenrl_amd import _lib
+from lumenrl_amd.quantization import ops
+
+pytestmark = pytest.mark.gpu
+
+if not torch.cuda.is_available():  # pragma: no cover - CPU container
+    pytest.skip("needs a HIP device", allow_module_level=True)
+
+DEV = torch.device("cuda", 0)
+DT = {"bf16": torch.bfloat16, "f16": torch.float16, "f32": torch.float32}
+RNG = np.random.default_rng(1234)
+
+
+def say(*a):
+    print(*a, flush=True)
+
+
+def host_bits(t: torch.Tensor) -> np.ndarray:
+    t = t.detach().cpu().contiguous()
+    if t.dtype in (torch.bfloat16, torch.float16):
+        return t.view(torch.int16).numpy().view(np.uint16)
+    return t.numpy()
+
+
+def dev_from_bits(x: np.ndarray, dt: str) -> torch.Tensor:
+    if dt == "f32":
+        return torch.from_numpy(np.ascontiguousarray(x, np.float32)).to(DEV)
+    t = torch.from_numpy(np.ascontiguousarray(x, np.uint16).view(np.int16))
+    return t.view(DT[dt]).to(DEV)
+
+
+def u8(t: torch.Tensor) -> np.ndarray:
+    return t.detach().contiguous().view(torch.uint8).cpu().numpy()
+
+
+def scale_bits(t: torch.Tensor) -> np.ndarray:
+    t = t.detach().cpu().contiguous()
+    if t.dtype == torch.float32:
+        return t.numpy().view(np.uint32)
+    if t.dtype in (torch.bfloat16, torch.float16):
+        return t.view(torch.int16).numpy().view(np.uint16)
+    return t.numpy()
+
+
+def weights(shape, outlier_frac=1e-3, dt="bf16"):
+    x = RNG.normal(0.0, 0.02, shape).astype(np.float32)
+    n = max(1, int(x.size * outlier_frac))
+    idx = RNG.choice(x.size, n, replace=False)
+    x.flat[idx] = RNG.choice([-1.0, 1.0], n) * RNG.uniform(0.5, 4.0, n)
+    t = torch.from_numpy(x).to(DT[dt])
+    return t
+
+
+def assert_fp8_matches_oracle(xd, blk, arith="f32", pow2=False, scale_dtype=None):
+    dt = {torch.bfloat16: "bf16", torch.float16: "f16", torch.float32: "f32"}[xd.dtype]
+    c, s = ops.fp8_block_quant(xd, blk, native_arith=arith == "native", pow2=pow2,
+                               scale_dtype=scale_dtype)
+    torch.cuda.synchronize()
+    xh = host_bits(xd)
+    shape = xh.shape
+    x3 = xh.reshape((-1,) + shape[-2:]) if xh.ndim >= 2 else xh.reshape(1, 1, -1)
+    oc, osc = O.fp8_block_quant(x3, dt, arith, blk, pow2)
+    assert np.array_equal(u8(c).reshape(oc.shape), oc)
+    got = scale_bits(s).reshape(-1)
+    if scale_dtype == torch.bfloat16 and osc.dtype == np.float32:
+        osc = O.bf16_from_f32(osc)
+        want = osc.reshape(-1)
+    else:
+        want = osc.view(np.uint32).reshape(-1) if osc.dtype == np.float32 else osc.reshape(-1)
+    assert np.array_equal(got, want)
+
+
+# ----------------------------------------------------------------------------
+# hardware encoders
+# ----------------------------------------------------------------------------
+@pytest.mark.slow
+def test_hw_e4m3_encoder_all_float32_patterns():
+    chunk = 1 << 28
+    out = torch.empty(chunk, dtype=torch.uint8, device=DEV)
+    bad = 0
+    for k in range((1 << 32) // chunk):
+        start = k * chunk
+        rc = _lib.lib().lrq_diag_e4m3_bits(start, chunk, out.data_ptr(), None)
+        _lib.check(rc, "lrq_diag_e4m3_bits")
+        torch.cuda.synchronize()
+        got = out.cpu().numpy()
+        want = O.e4m3_from_f32_bits_range(start, chunk)
+        nb = int((got != want).sum())
+        if nb:
+            w = np.argwhere(got != want)[:4].ravel()
+            say("e4m3 mismatch", [(hex(start + int(i)), hex(got[i]), hex(want[i])) for i in w])
+        bad += nb
+    assert bad == 0
+
+
+def test_e2m1_device_encoder_vs_oracle():
+    b = np.arange(0, 1 << 16, dtype=np.uint32)
+    xb = (b << 16).view(np.float32)
+    xb = xb[np.isfinite(xb)]
+    with np.errstate(over="ignore"):
+        v = np.concatenate([xb * np.float32(2.0 ** k) for k in range(-24, 25)])
+    v = v[np.isfinite(v)].astype(np.float32)
+    vd = torch.from_numpy(v).to(DEV)
+    out = torch.empty(v.size, dtype=torch.uint8, device=DEV)
+    _lib.check(_lib.lib().lrq_diag_e2m1(vd.data_ptr(), out.data_ptr(), v.size, None), "diag")
+    torch.cuda.synchronize()
+    assert np.array_equal(out.cpu().numpy(), O.e2m1_from_f32(v))
+
+
+# ----------------------------------------------------------------------------
+# golden fixtures
+# ----------------------------------------------------------------------------
+FP8_GOLDEN = sorted(f for f in os.listdir(os.path.join(ROOT, "tests", "golden"))
+                    if f.startswith("fp8_") and f != "fp8_dequant.npz")
+
+
+@pytest.mark.parametrize("name", FP8_GOLDEN)
+def test_fp8_golden_on_device(name):
+    g = load_golden(name)
+    dt, arith, pow2 = str(g["meta"][0]), str(g["meta"][1]), bool(int(g["meta"][2]))
+    blk = tuple(int(v) for v in g["block"])
+    say("golden", name, g["x"].shape)
+    xd = dev_from_bits(g["x"], dt)
+    c, s = ops.fp8_block_quant(xd, blk, native_arith=arith == "native", pow2=pow2)
+    torch.cuda.synchronize()
+    assert np.array_equal(u8(c).reshape(g["codes"].shape), g["codes"])
+    want = g["scales"]
+    got = scale_bits(s).reshape(want.shape)
+    assert np.array_equal(got, want.view(np.uint32) if want.dtype == np.float32 else want)
+    if "scales_bf16" in g:
+        c2, s2 = ops.fp8_block_quant(xd, blk, pow2=pow2, scale_dtype=torch.bfloat16)
+        torch.cuda.synchronize()
+        assert np.array_equal(scale_bits(s2).reshape(g["scales_bf16"].shape), g["scales_bf16"])
+        assert np.array_equal(u8(c2), u8(c))
+
+
+@pytest.mark.parametrize("name", ["mxfp8_bf16.npz", "mxfp4_bf16.npz", "mxfp8_f32.npz", "mxfp4_f32.npz"])
+def test_mx_golden_on_device(name):
+    g = load_golden(name)
+    dt = "bf16" if "bf16" in name else "f32"
+    xd = dev_from_bits(g["x"], dt)
+    fn = ops.quantize_mxfp8 if name.startswith("mxfp8") else ops.quantize_mxfp4
+    c, s = fn(xd)
+    torch.cuda.synchronize()
+    assert np.array_equal(u8(s), g["scales"])
+    assert np.array_equal(u8(c), g["codes"])
+
+
+def test_dequant_golden_on_device():
+    g = load_golden("fp8_dequant.npz")
+    c = torch.from_numpy(g["codes"]).to(DEV).view(torch.float8_e4m3fn)
+    s = torch.from_numpy(g["scales"]).to(DEV)
+    out = ops.fp8_block_dequant(c, s, (1, 128), torch.float32)
+    sb = dev_from_bits(g["scales_bf16"], "bf16")
+    outb = ops.fp8_block_dequant(c, sb, (1, 128), torch.bfloat16)
+    torch.cuda.synchronize()
+    assert np.array_equal(out.cpu().numpy().view(np.uint32), g["out_f32"].view(np.uint32))
+    assert np.array_equal(host_bits(outb), g["out_bf16"])
+
+
+# ----------------------------------------------------------------------------
+# random parity, every kernel path
+# ----------------------------------------------------------------------------
+def test_config1_full_tile128_and_row128():
+    """[4096, 4096] bf16, 128x128 (32x32 scales) and 1x128."""
+    x = weights((4096, 4096)).to(DEV)
+    say("config1 tile")
+    assert_fp8_matches_oracle(x, (128, 128))
+    say("config1 row")
+    assert_fp8_matches_oracle(x, (1, 128))
+    assert_fp8_matches_oracle(x, (1, 128), scale_dtype=torch.bfloat16)
+
+
+@pytest.mark.parametrize("dt", ["bf16", "f16", "f32"])
+@pytest.mark.parametrize("arith", ["f32", "native"])
+@pytest.mark.parametrize("pow2", [False, True])
+def test_tile_and_row_kernels_dtypes(dt, arith, pow2):
+    x = weights((384, 768), dt=dt)
+    x[0, :5] = 0.0
+    x[130:140, 300] = 0.0
+    xd = x.to(DEV)
+    assert_fp8_matches_oracle(xd, (128, 128), arith, pow2)
+    assert_fp8_matches_oracle(xd, (1, 128), arith, pow2)
+
+
+@pytest.mark.parametrize("bc", [32, 64, 256, 512])
+def test_row_kernel_block_sizes(bc):
+    xd = weights((96, 2048)).to(DEV)
+    assert_fp8_matches_oracle(xd, (1, bc))
+
+
+@pytest.mark.parametrize("blk", [(1, 96), (64, 64), (1, 8), (256, 128), (128, 256), (3, 40)])
+def test_generic_kernel_odd_blocks(blk):
+    xd = weights((200, 480)).to(DEV)
+    assert_fp8_matches_oracle(xd, blk)
+
+
+def test_ragged_tiles_and_strided_views():
+    big = weights((520, 1100)).to(DEV)
+    say("ragged tiles")
+    assert_fp8_matches_oracle(big[:300, :392], (128, 128))        # strided (ld=1100), fast path
+    assert_fp8_matches_oracle(big[:300, 1:393], (128, 128))       # misaligned -> generic
+    assert_fp8_matches_oracle(big[:256, 8:520], (1, 128))         # strided rows, fast path
+    assert_fp8_matches_oracle(big[:256, 3:515], (1, 128))         # misaligned -> generic
+    c1, s1 = ops.fp8_block_quant(big[:256, 8:520], (1, 128))
+    c2, s2 = ops.fp8_block_quant(big[:256, 8:520].contiguous(), (1, 128))
+    assert torch.equal(u8t(c1), u8t(c2)) and torch.equal(s1, s2)
+
+
+def u8t(c):
+    return c.view(torch.uint8)
+
+
+def test_expert_stacks_one_launch():
+    """Config-3 shapes (fewer experts): [E,768,2048] and [E,2048,768] with a zero and an inf tile."""
+    E = 8
+    gu = weights((E, 768, 2048))
+    dn = weights((E, 2048, 768))
+    gu[3, 128:256, 512:640] = 0.0
+    dn[5, 1024 + 7, 256 + 9] = float("inf")
+    for t in (gu, dn):
+        assert_fp8_matches_oracle(t.to(DEV), (128, 128))
+
+
+def test_edge_blocks_fp8():
+    x = weights((8, 512))
+    x[0, :128] = 0.0
+    x[0, 5] = -0.0
+    x[1, 3], x[1, 4] = float("inf"), -float("inf")
+    x[2, 7] = float("nan")
+    x[3, :128] = 1e-40
+    x[4, :128] = torch.randn(128) * 1e-30
+    x[5, 9] = 3.3e38
+    x[6, 130], x[6, 131] = float("nan"), -float("inf")
+    x[7, 256:384] = 1e-38
+    xd = x.to(DEV)
+    # small tensor: native-bf16 and pow2 NaN rules are the vectorized-body ones
+    for blk in ((1, 128), (1, 64), (8, 128), (1, 96)):
+        for arith in ("f32", "native"):
+            for pow2 in (False, True):
+                assert_fp8_matches_oracle(xd, blk, arith, pow2)
+    xf = x.float().to(DEV)
+    for pow2 in (False, True):
+        assert_fp8_matches_oracle(xf, (1, 128), "f32", pow2)
+        assert_fp8_matches_oracle(xf, (128, 128), "f32", pow2)
+
+
+@pytest.mark.parametrize("fmt", [8, 4])
+@pytest.mark.parametrize("dt", ["bf16", "f16", "f32"])
+def test_mx_random_and_strided(fmt, dt):
+    x = weights((256, 1024), dt=dt)
+    x = x * torch.exp(torch.empty(256, 1).uniform_(np.log(0.25), np.log(4.0))).to(x.dtype)
+    x[0, :32] = 0.0
+    x[1, 40] = float("nan")
+    x[2, 70] = -float("inf")
+    x[3, 96:128] = 1e-40 if dt != "f16" else 1e-7
+    fn = ops.quantize_mxfp8 if fmt == 8 else ops.quantize_mxfp4
+    for xd, tag in ((x.to(DEV), "contig"), (torch.cat([x, x], 1).to(DEV)[:, 512:1536 - 0][:, :1024], "strided")):
+        c, s = fn(xd)
+        torch.cuda.synchronize()
+        oc, osc = O.mx_quant(host_bits(xd.contiguous()), dt, fmt)
+        assert np.array_equal(u8(s), osc), tag
+        assert np.array_equal(u8(c), oc), tag
+    # misaligned view -> generic MX kernel
+    big = torch.cat([x, x], 1).to(DEV)
+    xv = big[:, 1:1025 - 0][:, :992]
+    c, s = fn(xv)
+    torch.cuda.synchronize()
+    oc, osc = O.mx_quant(host_bits(xv.contiguous()), dt, fmt)
+    assert np.array_equal(u8(s), osc) and np.array_equal(u8(c), oc)
+
+
+def test_empty_tensors():
+    for shape in ((0, 256), (4, 0), (0,)):
+        x = torch.zeros(shape, dtype=torch.bfloat16, device=DEV)
+        c, s = ops.fp8_block_quant(x, (1, 128))
+        assert c.shape == x.shape
+    c, s = ops.quantize_mxfp8(torch.zeros((0, 64), dtype=torch.bfloat16, device=DEV))
+    assert c.shape == (0, 64) and s.shape == (0, 2)
+
+
+# ----------------------------------------------------------------------------
+# grouped launches
+# ----------------------------------------------------------------------------
+QWEN3_8B_LAYER = [(4096, 4096), (1024, 4096), (1024, 4096), (4096, 4096),
+                  (12288, 4096), (12288, 4096), (4096, 12288)]
+
+
+@pytest.mark.parametrize("fmt,blk", [("fp8_block", (128, 128)), ("fp8_block", (1, 128)),
+                                     ("mxfp8", None), ("mxfp4", None)])
+def test_grouped_qwen3_layer_matches_oracle(fmt, blk):
+    say("grouped layer", fmt, blk)
+    ws = [weights(s).to(DEV) for s in QWEN3_8B_LAYER]
+    plan = ops.QuantPlan(ws, fmt, blk or (1, 32))
+    plan.run()
+    torch.cuda.synchronize()
+    for w, (c, s) in zip(ws, plan.outputs):
+        xh = host_bits(w)
+        if fmt == "fp8_block":
+            oc, osc = O.fp8_block_quant(xh, "bf16", "f32", blk)
+            assert np.array_equal(u8(c).reshape(oc.shape), oc)
+            assert np.array_equal(scale_bits(s).reshape(-1), osc.view(np.uint32).reshape(-1))
+        else:
+            oc, osc = O.mx_quant(xh, "bf16", 8 if fmt == "mxfp8" else 4)
+            assert np.array_equal(u8(c), oc) and np.array_equal(u8(s), osc)
+    # re-running after the inputs change re-quantizes the new values
+    ws[0].mul_(2)
+    plan.run()
+    torch.cuda.synchronize()
+    if fmt == "fp8_block":
+        oc, osc = O.fp8_block_quant(host_bits(ws[0]), "bf16", "f32", blk)
+        assert np.array_equal(u8(plan.outputs[0][0]).reshape(oc.shape), oc)
+
+
+def test_grouped_expert_stacks_single_launch():
+    gu = weights((16, 1536, 2048))
+    dn = weights((16, 2048, 768))
+    gu[2, :128, :128] = 0.0
+    dn[9, 300, 400] = float("inf")
+    ws = [gu.to(DEV), dn.to(DEV)]
+    plan = ops.QuantPlan(ws, "fp8_block", (128, 128))
+    assert plan.units == 16 * 12 * 16 + 16 * 16 * 6
+    plan.run()
+    torch.cuda.synchronize()
+    for w, (c, s) in zip(ws, plan.outputs):
+        oc, osc = O.fp8_block_quant(host_bits(w), "bf16", "f32", (128, 128))
+        assert np.array_equal(u8(c).reshape(oc.shape), oc)
+        assert np.array_equal(scale_bits(s).reshape(-1), osc.view(np.uint32).reshape(-1))
+
+
+# ----------------------------------------------------------------------------
+# exhaustive (x, amax): every bf16 x against every finite bf16 amax
+# ----------------------------------------------------------------------------
+def exhaustive_blocks(per_block: int) -> np.ndarray:
+    """Rows of `per_block` bf16 patterns: slot 0 holds amax a, the rest every
+    bf16 x with |x| <= a (both signs), for every finite positive a."""
+    rows = []
+    for a in range(1, 0x7F80):
+        xs = np.concatenate([np.arange(0, a + 1, dtype=np.uint16),
+                             np.arange(0x8000, 0x8000 + a + 1, dtype=np.uint16)])
+        k = per_block - 1
+        nb = -(-xs.size // k)
+        pad = np.full(nb * k - xs.size, a, np.uint16)
+        blk = np.concatenate([xs, pad]).reshape(nb, k)
+        rows.append(np.concatenate([np.full((nb, 1), a, np.uint16), blk], axis=1))
+    return np.concatenate(rows)
+
+
+@pytest.mark.slow
+@pytest.mark.parametrize("arith", ["f32", "native"])
+def test_exhaustive_pairs_row_kernel(arith):
+    xb = exhaustive_blocks(128)
+    say("exhaustive row", arith, xb.shape)
+    xd = dev_from_bits(xb, "bf16")
+    c, s = ops.fp8_block_quant(xd, (1, 128), native_arith=arith == "native")
+    torch.cuda.synchronize()
+    oc, osc = O.fp8_block_quant(xb, "bf16", arith, (1, 128))
+    got = u8(c)
+    bad = int((got.reshape(oc.shape) != oc).sum())
+    assert bad == 0
+    sb = scale_bits(s).reshape(-1)
+    want = osc.view(np.uint32).reshape(-1) if osc.dtype == np.float32 else osc.reshape(-1)
+    assert np.array_equal(sb, want)
+
+
+@pytest.mark.slow
+def test_exhaustive_pairs_tile_kernel():
+    xb = exhaustive_blocks(128 * 128).reshape(-1, 128)
+    say("exhaustive tile", xb.shape)
+    xd = dev_from_bits(xb, "bf16")
+    c, s = ops.fp8_block_quant(xd, (128, 128))
+    torch.cuda.synchronize()
+    oc, osc = O.fp8_block_quant(xb, "bf16", "f32", (128, 128))
+    assert np.array_equal(u8(c).reshape(oc.shape), oc)
+    assert np.array_equal(scale_bits(s).reshape(-1), osc.view(np.uint32).reshape(-1))
