@@ -49,9 +49,10 @@ __device__ __forceinline__ float f16_round(float f) { return f16_to_f32(f16_bits
 // element encoders
 // ---------------------------------------------------------------------------
 // Two floats -> two float8_e4m3fn bytes (RNE) in the low (HI=false) or high
-// (HI=true) half of `old`.  gfx950's v_cvt_pk_fp8_f32 is the OCP e4m3 encoder;
-// only |v| <= 448 (plus zeros/subnormals) is ever fed to it on the product
-// path, and tests check it against the oracle over every float32 bit pattern.
+// (HI=true) half of `old`.  gfx950's v_cvt_pk_fp8_f32 is the OCP e4m3 encoder,
+// round-to-nearest-even; over every float32 bit pattern it matches torch's
+// float8_e4m3fn cast except on NaN inputs (0xFF for any NaN sign).  Only
+// finite |v| <= 448 is ever fed to it; inf/NaN blocks use special_code().
 template <bool HI>
 __device__ __forceinline__ uint32_t cvt_e4m3x2(float a, float b, uint32_t old) {
   return (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(a, b, (int)old, HI);

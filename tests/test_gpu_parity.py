@@ -93,9 +93,16 @@ def assert_fp8_matches_oracle(xd, blk, arith="f32", pow2=False, scale_dtype=None
 # ----------------------------------------------------------------------------
 @pytest.mark.slow
 def test_hw_e4m3_encoder_all_float32_patterns():
+    """v_cvt_pk_fp8_f32 vs the oracle's encoder on all 2^32 float32 patterns.
+
+    Identical on every non-NaN input (finite, subnormal, +-inf).  On NaN input
+    the hardware writes 0xFF whatever the sign (torch keeps the sign); the
+    kernels never feed it a NaN -- inf/NaN blocks take special_code().
+    """
     chunk = 1 << 28
     out = torch.empty(chunk, dtype=torch.uint8, device=DEV)
-    bad = 0
+    bad_non_nan = 0
+    nan_codes = set()
     for k in range((1 << 32) // chunk):
         start = k * chunk
         rc = _lib.lib().lrq_diag_e4m3_bits(start, chunk, out.data_ptr(), None)
@@ -103,12 +110,18 @@ def test_hw_e4m3_encoder_all_float32_patterns():
         torch.cuda.synchronize()
         got = out.cpu().numpy()
         want = O.e4m3_from_f32_bits_range(start, chunk)
-        nb = int((got != want).sum())
+        bits = np.arange(start, start + chunk, dtype=np.uint64).astype(np.uint32)
+        isnan = (bits & 0x7FFFFFFF) > 0x7F800000
+        diff = got != want
+        nb = int((diff & ~isnan).sum())
         if nb:
-            w = np.argwhere(got != want)[:4].ravel()
+            w = np.argwhere(diff & ~isnan)[:4].ravel()
             say("e4m3 mismatch", [(hex(start + int(i)), hex(got[i]), hex(want[i])) for i in w])
-        bad += nb
-    assert bad == 0
+        bad_non_nan += nb
+        if isnan.any():
+            nan_codes |= set(np.unique(got[isnan]).tolist())
+    assert bad_non_nan == 0
+    assert nan_codes <= {0x7F, 0xFF}
 
 
 def test_e2m1_device_encoder_vs_oracle():
