@@ -13,6 +13,7 @@ already resident in HBM:
       per layer (48 per step).
   c4: c2 shapes, Student-t(4) x 0.02/sqrt(2), MXFP8.
   c5: c2 shapes, N(0, 0.02^2) x per-row log-uniform[0.25, 4], MXFP4.
+  c2r: c2 weights with the reference's own 1x128 blocks (scales [N, K/128]).
 
 Prints ONE JSON line on stdout.  value = algorithmic bytes (bf16 in + codes +
 scales) per step / step time, in GB/s (1e9 B/s).  The roofline object uses the
@@ -99,7 +100,15 @@ def moe_layer(torch, dev, seed, layer, experts=128):
 # ---------------------------------------------------------------------------
 # CPU baseline: the reference's op sequence in torch on the host (bounded sample)
 # ---------------------------------------------------------------------------
-def cpu_baseline(torch, ws, fmt_block, seconds):
+def cpu_baseline(torch, ws, fmt, fmt_block, seconds):
+    """Time the CPU path on the host over whole tensors until `seconds` elapse.
+
+    FP8 blockwise: the reference's torch op sequence (oracle/torch_ref.py).
+    MX formats have no reference CPU path: the C oracle's MX restatement.
+    """
+    import numpy as np
+
+    from oracle import oracle as O
     from oracle import torch_ref
 
     threads = max(1, min(os.cpu_count() or 1, 16))
@@ -109,25 +118,34 @@ def cpu_baseline(torch, ws, fmt_block, seconds):
     t_total = 0.0
     for w in ws:
         x = w.cpu()
-        t0 = time.perf_counter()
-        if fmt_block == (128, 128):
-            q, s = torch_ref.quantize_tensor_tiles(x.float(), (128, 128))
+        if fmt == "fp8_block":
+            t0 = time.perf_counter()
+            if fmt_block == (128, 128):
+                q, s = torch_ref.quantize_tensor_tiles(x.float(), (128, 128))
+            else:
+                q, s = torch_ref.quantize_tensor(x.float(), fmt_block[1])
+            t_total += time.perf_counter() - t0
+            done_bytes += x.numel() * 2 + q.numel() + s.numel() * 4
         else:
-            q, s = torch_ref.quantize_tensor(x.float(), fmt_block[1])
-        t_total += time.perf_counter() - t0
-        done_bytes += x.numel() * 2 + q.numel() + s.numel() * 4
+            xb = x.view(torch.int16).numpy().view(np.uint16)
+            t0 = time.perf_counter()
+            q, s = O.mx_quant(xb, "bf16", 8 if fmt == "mxfp8" else 4, nthreads=threads)
+            t_total += time.perf_counter() - t0
+            done_bytes += x.numel() * 2 + q.size + s.size
         n += 1
         if t_total >= seconds:
             break
+    what = (f"oracle/torch_ref.py (weight_quantizer.py op order on {fmt_block[0]}x{fmt_block[1]} "
+            f"blocks, fp32 upcast first)" if fmt == "fp8_block" else
+            f"the C oracle's {fmt} restatement (the reference has no MX CPU path)")
     return {
         "value": round(done_bytes / t_total / 1e9, 3),
         "unit": "GB/s",
         "cores": threads,
         "kind": "port",
         "sample": (f"first {n} tensors of the same weight set ({done_bytes / 1e9:.2f} GB "
-                   f"algorithmic) through oracle/torch_ref.py (weight_quantizer.py op order on "
-                   f"{fmt_block[0]}x{fmt_block[1]} blocks, fp32 upcast first) with "
-                   f"torch.set_num_threads({threads}) on {os.cpu_count()} visible cores"),
+                   f"algorithmic) through {what}, {threads} threads on {os.cpu_count()} "
+                   f"visible cores"),
     }
 
 
@@ -147,14 +165,15 @@ def run(args):
     t0 = time.time()
 
     flush = None
-    if cfg in ("c2", "c4", "c5"):
-        kind = {"c2": "normal", "c4": "student_t", "c5": "rowscale"}[cfg]
-        fmt = {"c2": "fp8_block", "c4": "mxfp8", "c5": "mxfp4"}[cfg]
+    if cfg in ("c2", "c4", "c5", "c2r"):
+        kind = {"c2": "normal", "c4": "student_t", "c5": "rowscale", "c2r": "normal"}[cfg]
+        fmt = {"c2": "fp8_block", "c4": "mxfp8", "c5": "mxfp4", "c2r": "fp8_block"}[cfg]
+        blk = (1, 128) if cfg == "c2r" else (128, 128)
         ws, _ = qwen3_8b_set(torch, dev, args.seed, kind)
-        plans = [ops.QuantPlan(ws, fmt, (128, 128))]
+        plans = [ops.QuantPlan(ws, fmt, blk)]
         workload = {"c2": "qwen3-8b-linears-fp8-e4m3-128x128", "c4": "qwen3-8b-linears-mxfp8",
-                    "c5": "qwen3-8b-linears-mxfp4"}[cfg]
-        cpu_ws, cpu_blk = ws, (128, 128)
+                    "c5": "qwen3-8b-linears-mxfp4", "c2r": "qwen3-8b-linears-fp8-e4m3-1x128"}[cfg]
+        cpu_ws, cpu_blk, cpu_fmt = ws, blk, fmt
         extra = {"tensors": len(ws), "layers": 36, "elements": sum(w.numel() for w in ws),
                  "format": fmt, "launches_per_step": 1}
     elif cfg == "c1":
@@ -163,7 +182,7 @@ def run(args):
         plans = [ops.QuantPlan(ws, "fp8_block", (128, 128))]
         flush = torch.empty(1 << 30, dtype=torch.uint8, device=dev)
         workload = "single-4096x4096-fp8-e4m3-128x128"
-        cpu_ws, cpu_blk = ws, (128, 128)
+        cpu_ws, cpu_blk, cpu_fmt = ws, (128, 128), "fp8_block"
         extra = {"tensors": 1, "elements": ws[0].numel(), "format": "fp8_block",
                  "launches_per_step": 1, "l2_mall_flushed": True}
     elif cfg == "c3":
@@ -173,7 +192,7 @@ def run(args):
             ws += [gu, dn]
             plans.append(ops.QuantPlan([gu, dn], "fp8_block", (128, 128)))
         workload = "qwen3-30b-a3b-experts-fp8-e4m3-128x128"
-        cpu_ws, cpu_blk = ws[:2], (128, 128)
+        cpu_ws, cpu_blk, cpu_fmt = ws[:2], (128, 128), "fp8_block"
         extra = {"tensors": len(ws), "layers": 48, "experts": 128,
                  "elements": sum(w.numel() for w in ws), "format": "fp8_block",
                  "launches_per_step": 48}
@@ -248,13 +267,13 @@ def run(args):
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
             "traffic": traffic,
-            "kernel": "k_tile128" if cfg in ("c1", "c2", "c3") else "k_mx",
+            "kernel": {"c2r": "k_rowquad"}.get(cfg, "k_tile128" if cfg in ("c1", "c2", "c3") else "k_mx"),
             "launch_ms": round(kern_ms, 5),
         },
     }
     if not args.no_cpu:
         log("[bench] cpu baseline ...")
-        result["cpu_baseline"] = cpu_baseline(torch, cpu_ws, cpu_blk, args.cpu_seconds)
+        result["cpu_baseline"] = cpu_baseline(torch, cpu_ws, cpu_fmt, cpu_blk, args.cpu_seconds)
     print(json.dumps(result), flush=True)
 
 
@@ -285,7 +304,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--config", default="c2", choices=["c1", "c2", "c3", "c4", "c5"])
+    ap.add_argument("--config", default="c2", choices=["c1", "c2", "c3", "c4", "c5", "c2r"])
     ap.add_argument("--seed", type=int, default=1000)
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")

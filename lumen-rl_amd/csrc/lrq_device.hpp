@@ -214,6 +214,37 @@ __device__ __forceinline__ uint32_t mx_e8m0(uint32_t amax_bits) {
 __device__ __forceinline__ float mx_mult(uint32_t e8m0) { return u2f((254u - e8m0) << 23); }
 
 // ---------------------------------------------------------------------------
+// streaming memory access and XCD-aware work order
+// ---------------------------------------------------------------------------
+typedef unsigned int v4u __attribute__((ext_vector_type(4)));
+typedef unsigned int v2u __attribute__((ext_vector_type(2)));
+
+// Weights are read once and codes written once: non-temporal accesses keep
+// them from displacing anything in L2/MALL (measured +5% HBM throughput).
+__device__ __forceinline__ v4u load_nt(const void* p) {
+  return __builtin_nontemporal_load(static_cast<const v4u*>(p));
+}
+__device__ __forceinline__ void store_nt(void* p, v2u v) {
+  __builtin_nontemporal_store(v, static_cast<v2u*>(p));
+}
+__device__ __forceinline__ void store_nt(void* p, uint32_t v) {
+  __builtin_nontemporal_store(v, static_cast<uint32_t*>(p));
+}
+
+// MI355X dispatches work-group i to XCD i % 8.  Work units adjacent in memory
+// (the tiles of a 128-row band, consecutive row blocks) are given to one XCD in
+// runs of kXcdRun, so each XCD streams contiguous megabytes instead of every
+// eighth 32 KiB piece.  A bijection on [0, n); the tail past the last whole
+// run group keeps the identity order.
+constexpr int64_t kXcdRun = 32;
+__device__ __forceinline__ int64_t xcd_unit(int64_t i, int64_t n) {
+  constexpr int64_t chunk = 8 * kXcdRun;
+  if (i >= (n / chunk) * chunk) return i;
+  const int64_t r = i % chunk;
+  return (i - r) + (r % 8) * kXcdRun + r / 8;
+}
+
+// ---------------------------------------------------------------------------
 // small reductions
 // ---------------------------------------------------------------------------
 typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));

@@ -5,7 +5,8 @@
 // clamp(tiny) -> [pow2] -> x/s -> float8_e4m3fn, in one HBM pass (bf16 in,
 // e4m3 + scale out).  Three kernels:
 //   k_tile128  : 128x128 tiles (the vLLM/ATOM `weight_scale_inv` layout), one
-//                256-thread work-group per tile, the tile held in VGPRs.
+//                256-thread work-group per tile, the tile held in VGPRs;
+//                tiles handed to XCDs in runs of kXcdRun (xcd_unit).
 //   k_rowquad  : 1xB row blocks (the reference's own layout), one quad of lanes
 //                per block, B/32 chunks of 8 elements per lane.
 //   k_generic  : any block shape, stride or alignment (one work-group per
@@ -26,13 +27,12 @@ struct Chunk {
 template <int DT>
 __device__ __forceinline__ void load_chunk(Chunk<DT>& c, const void* base, int64_t off) {
   if constexpr (DT == kF32) {
-    const uint4* p = reinterpret_cast<const uint4*>(static_cast<const float*>(base) + off);
-    uint4 a = p[0], b = p[1];
+    const float* p = static_cast<const float*>(base) + off;
+    const v4u a = load_nt(p), b = load_nt(p + 4);
     c.w[0] = a.x; c.w[1] = a.y; c.w[2] = a.z; c.w[3] = a.w;
     c.w[4] = b.x; c.w[5] = b.y; c.w[6] = b.z; c.w[7] = b.w;
   } else {
-    const uint4* p = reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(base) + off);
-    uint4 a = p[0];
+    const v4u a = load_nt(static_cast<const uint16_t*>(base) + off);
     c.w[0] = a.x; c.w[1] = a.y; c.w[2] = a.z; c.w[3] = a.w;
   }
 }
@@ -81,8 +81,8 @@ struct Amax {
 
 // 8 elements -> 8 e4m3 bytes (element 0 lowest).
 template <int DT, int CDT>
-__device__ __forceinline__ uint2 encode_chunk(const Chunk<DT>& c, const BlockScale& b) {
-  uint2 r;
+__device__ __forceinline__ v2u encode_chunk(const Chunk<DT>& c, const BlockScale& b) {
+  v2u r;
   if (b.kind == kScaleFast) {
     float q[8];
 #pragma unroll
@@ -120,13 +120,14 @@ __device__ __forceinline__ void store_scale(void* scales, int64_t idx, float s, 
 
 __device__ __forceinline__ void pick_desc(const Desc& single, const Desc* descs,
                                           const uint32_t* map, Desc& d, int64_t& u) {
+  const int64_t wg = xcd_unit(blockIdx.x, gridDim.x);
   if (map != nullptr) {
-    const uint32_t t = map[blockIdx.x];
+    const uint32_t t = map[wg];
     d = descs[t];
-    u = (int64_t)blockIdx.x - d.unit0;
+    u = wg - d.unit0;
   } else {
     d = single;
-    u = blockIdx.x;
+    u = wg;
   }
 }
 
@@ -180,15 +181,16 @@ __global__ __launch_bounds__(256) void k_tile128(Desc single, const Desc* __rest
   a = red[1] > a ? red[1] : a;
   a = red[2] > a ? red[2] : a;
   a = red[3] > a ? red[3] : a;
+  a = __builtin_amdgcn_readfirstlane(a);  // tile-uniform: scalar scale math
 
   const BlockScale bs = block_scale<CDT>(a, pow2 != 0);
   if (tid == 0) store_scale<CDT>(d.scales, u, bs.s, scale_bf16);
 
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
-    const uint2 q = encode_chunk<DT, CDT>(ch[i], bs);
+    const v2u q = encode_chunk<DT, CDT>(ch[i], bs);
     if (full || (col_ok && r0 + rr + 16 * i < d.rows))
-      *reinterpret_cast<uint2*>(d.codes + out_base + (int64_t)(16 * i) * d.cols) = q;
+      store_nt(d.codes + out_base + (int64_t)(16 * i) * d.cols, q);
   }
 }
 
@@ -234,8 +236,8 @@ __global__ __launch_bounds__(256) void k_rowquad(Desc single, const Desc* __rest
   if (p == 0) store_scale<CDT>(d.scales, gb, bs.s, scale_bf16);
 #pragma unroll
   for (int j = 0; j < CPL; ++j) {
-    const uint2 q = encode_chunk<DT, CDT>(ch[j], bs);
-    *reinterpret_cast<uint2*>(d.codes + out_base + (p + 4 * j) * 8) = q;
+    const v2u q = encode_chunk<DT, CDT>(ch[j], bs);
+    store_nt(d.codes + out_base + (p + 4 * j) * 8, q);
   }
 }
 

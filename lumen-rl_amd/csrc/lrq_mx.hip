@@ -19,13 +19,12 @@ namespace lrq {
 template <int DT>
 __device__ __forceinline__ void mx_load8(const void* base, int64_t off, uint32_t (&w)[8]) {
   if constexpr (DT == kF32) {
-    const uint4* p = reinterpret_cast<const uint4*>(static_cast<const float*>(base) + off);
-    uint4 a = p[0], b = p[1];
+    const float* p = static_cast<const float*>(base) + off;
+    const v4u a = load_nt(p), b = load_nt(p + 4);
     w[0] = a.x; w[1] = a.y; w[2] = a.z; w[3] = a.w;
     w[4] = b.x; w[5] = b.y; w[6] = b.z; w[7] = b.w;
   } else {
-    const uint4* p = reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(base) + off);
-    uint4 a = p[0];
+    const v4u a = load_nt(static_cast<const uint16_t*>(base) + off);
     w[0] = a.x; w[1] = a.y; w[2] = a.z; w[3] = a.w;
   }
 }
@@ -59,8 +58,8 @@ __device__ __forceinline__ uint32_t mx_amax8(const uint32_t (&w)[8]) {
 
 // 8 elements of a finite group -> E4M3 bytes (8) or E2M1 nibbles (8 in a dword).
 template <int DT, int FMT>
-__device__ __forceinline__ uint2 mx_encode8(const uint32_t (&w)[8], uint32_t e8m0) {
-  uint2 r;
+__device__ __forceinline__ v2u mx_encode8(const uint32_t (&w)[8], uint32_t e8m0) {
+  v2u r;
   if (e8m0 != 0xFFu) {
     const float mult = mx_mult(e8m0);
     float v[8];
@@ -107,13 +106,14 @@ __global__ __launch_bounds__(256) void k_mx(Desc single, const Desc* __restrict_
   constexpr int kEmax = FMT == 8 ? 8 : 2;
   Desc d;
   int64_t u;
+  const int64_t wg = xcd_unit(blockIdx.x, gridDim.x);
   if (map != nullptr) {
-    const uint32_t t = map[blockIdx.x];
+    const uint32_t t = map[wg];
     d = descs[t];
-    u = (int64_t)blockIdx.x - d.unit0;
+    u = wg - d.unit0;
   } else {
     d = single;
-    u = blockIdx.x;
+    u = wg;
   }
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -148,11 +148,11 @@ __global__ __launch_bounds__(256) void k_mx(Desc single, const Desc* __restrict_
     const uint32_t e = mx_e8m0<kEmax>(a);
     if (!ok[j]) continue;
     const int64_t g = g0 + 16 * j;
-    const uint2 c = mx_encode8<DT, FMT>(w[j], e);
+    const v2u c = mx_encode8<DT, FMT>(w[j], e);
     if constexpr (FMT == 8) {
-      *reinterpret_cast<uint2*>(d.codes + g * 32 + p * 8) = c;
+      store_nt(d.codes + g * 32 + p * 8, c);
     } else {
-      *reinterpret_cast<uint32_t*>(d.codes + g * 16 + p * 4) = c.x;
+      store_nt(d.codes + g * 16 + p * 4, (uint32_t)c.x);
     }
     if (p == 0) static_cast<uint8_t*>(d.scales)[g] = (uint8_t)e;
   }
