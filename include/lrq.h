@@ -143,11 +143,15 @@ const char* lrq_last_error(void);
  * Diagnostics (no reference counterpart): the device element encoders applied
  * to raw inputs, so tests can compare them with the CPU oracle exhaustively.
  *   lrq_diag_e4m3_bits: out[i] = e4m3(float with bit pattern start + i), via
- *     the hardware pack-convert the kernels use; n a multiple of 4.
- *   lrq_diag_e2m1: out[i] = E2M1 nibble of in[i] (finite inputs).
+ *     the hardware pack-convert the FP8 kernels use; n a multiple of 4.
+ *   lrq_diag_mx_encode: the MXFP8 (fmt LRQ_FMT_MXFP8) or MXFP4 (LRQ_FMT_MXFP4)
+ *     element path of the MX kernel: elements 2k and 2k+1 of `in` encoded
+ *     under E8M0 byte e8m0[k]; out[i] = E4M3 byte or E2M1 nibble of in[i];
+ *     n even.
  */
 int lrq_diag_e4m3_bits(uint32_t start, int64_t n, uint8_t* out, lrq_stream_t stream);
-int lrq_diag_e2m1(const float* in, uint8_t* out, int64_t n, lrq_stream_t stream);
+int lrq_diag_mx_encode(int fmt, const float* in, const uint8_t* e8m0, uint8_t* out, int64_t n,
+                       lrq_stream_t stream);
 
 #ifdef __cplusplus
 }

@@ -121,12 +121,14 @@ bool plan_units(const LaunchCfg& cfg, Desc& d) {
       d.units_c = (d.cols + cfg.blk_c - 1) / cfg.blk_c;
       d.units = d.batch * d.units_r * d.units_c;
       return true;
-    case kKernRowQuad:
+    case kKernRowQuad: {
       if (!fold_batch(d)) return false;
       d.bpr = d.cols / cfg.blk_c;
       d.nblocks = d.rows * d.bpr;
-      d.units = (d.nblocks + 63) / 64;
+      const int64_t per_wg = 16 * (512 / cfg.blk_c);  // 4 waves x 4 instructions x blocks each
+      d.units = (d.nblocks + per_wg - 1) / per_wg;
       return true;
+    }
     case kKernMx:
     case kKernGenericMx:
       if (!fold_batch(d)) {
@@ -355,11 +357,14 @@ int lrq_diag_e4m3_bits(uint32_t start, int64_t n, uint8_t* out, lrq_stream_t str
   return check_hip(lrq::launch_diag_e4m3_bits(start, n, out, (hipStream_t)stream), "kernel launch");
 }
 
-int lrq_diag_e2m1(const float* in, uint8_t* out, int64_t n, lrq_stream_t stream) {
+int lrq_diag_mx_encode(int fmt, const float* in, const uint8_t* e8m0, uint8_t* out, int64_t n,
+                       lrq_stream_t stream) {
   g_err.clear();
-  if (n <= 0 || !in || !out) return fail(LRQ_ERR_ARG, "bad diag args");
-  if ((n + 255) / 256 > kMaxGrid) return fail(LRQ_ERR_ARG, "n too large");
-  return check_hip(lrq::launch_diag_e2m1(in, out, n, (hipStream_t)stream), "kernel launch");
+  if ((fmt != LRQ_FMT_MXFP8 && fmt != LRQ_FMT_MXFP4) || n <= 0 || n % 2 != 0 || !in || !e8m0 || !out)
+    return fail(LRQ_ERR_ARG, "bad diag args");
+  if ((n / 2 + 255) / 256 > kMaxGrid) return fail(LRQ_ERR_ARG, "n too large");
+  return check_hip(lrq::launch_diag_mx(fmt == LRQ_FMT_MXFP8 ? 8 : 4, in, e8m0, n, out,
+                                       (hipStream_t)stream), "kernel launch");
 }
 
 }  // extern "C"

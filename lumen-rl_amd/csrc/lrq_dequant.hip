@@ -81,21 +81,9 @@ __global__ __launch_bounds__(256) void k_diag_e4m3_bits(uint32_t start, int64_t 
   *reinterpret_cast<uint32_t*>(out + i) = w;
 }
 
-__global__ __launch_bounds__(256) void k_diag_e2m1(const float* in, int64_t n, uint8_t* out) {
-  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  if (i >= n) return;
-  out[i] = (uint8_t)e2m1_code(in[i]);
-}
-
 hipError_t launch_diag_e4m3_bits(uint32_t start, int64_t n, uint8_t* out, hipStream_t stream) {
   const int64_t g = (n / 4 + 255) / 256;
   hipLaunchKernelGGL(k_diag_e4m3_bits, dim3((unsigned)g), dim3(256), 0, stream, start, n, out);
-  return hipGetLastError();
-}
-
-hipError_t launch_diag_e2m1(const float* in, uint8_t* out, int64_t n, hipStream_t stream) {
-  const int64_t g = (n + 255) / 256;
-  hipLaunchKernelGGL(k_diag_e2m1, dim3((unsigned)g), dim3(256), 0, stream, in, n, out);
   return hipGetLastError();
 }
 

@@ -82,6 +82,7 @@ __device__ __forceinline__ uint32_t sw_e4m3(float f) {
 }
 
 // E2M1 nibble of a finite float: RNE onto {0,.5,1,1.5,2,3,4,6}, saturating.
+// Software form, kept for the generic (unaligned) MX kernel.
 __device__ __forceinline__ uint32_t e2m1_code(float v) {
   uint32_t u = f2u(v);
   uint32_t sign = (u >> 28) & 0x8u, a = u & 0x7FFFFFFFu;
@@ -92,6 +93,17 @@ __device__ __forceinline__ uint32_t e2m1_code(float v) {
   uint32_t nrm = (a - 0x3F000000u + 0x1FFFFFu + ((a >> 22) & 1u)) >> 22;
   nrm = nrm > 7u ? 7u : nrm;
   return sign | (af < 1.0f ? sub : nrm);
+}
+
+// Two finite elements of an MXFP4 group with E8M0 exponent e -> two E2M1
+// nibbles (first in the low nibble) written into byte SEL of `old`.
+// gfx950's v_cvt_scalef32_pk_fp4_f32 divides by 2^(e-127) -- the scale
+// operand's exponent field is read as the E8M0 byte -- then rounds to nearest
+// even and saturates at +-6; it matches the OCP rule (x * 2^(127-e) through
+// e2m1_code) on every finite bf16 x and every e (checked exhaustively).
+template <int SEL>
+__device__ __forceinline__ uint32_t mx_fp4x2(uint32_t old, float a, float b, uint32_t e8m0) {
+  return __builtin_amdgcn_cvt_scalef32_pk_fp4_f32(old, a, b, u2f(e8m0 << 23), SEL);
 }
 
 // ---------------------------------------------------------------------------

@@ -7,8 +7,9 @@
 //   k_tile128  : 128x128 tiles (the vLLM/ATOM `weight_scale_inv` layout), one
 //                256-thread work-group per tile, the tile held in VGPRs;
 //                tiles handed to XCDs in runs of kXcdRun (xcd_unit).
-//   k_rowquad  : 1xB row blocks (the reference's own layout), one quad of lanes
-//                per block, B/32 chunks of 8 elements per lane.
+//   k_row      : 1xB row blocks (the reference's own layout), B/8 consecutive
+//                lanes per block so every wave instruction is one contiguous
+//                span; one scale computation per lane, shared by shuffles.
 //   k_generic  : any block shape, stride or alignment (one work-group per
 //                block, scalar loads); the fallback for odd inputs.
 // All of them share lrq_device.hpp's block_scale / block_quot / special_code.
@@ -195,49 +196,87 @@ __global__ __launch_bounds__(256) void k_tile128(Desc single, const Desc* __rest
 }
 
 // ---------------------------------------------------------------------------
-// 1xB row blocks, B = 32*CPL.  Quad q of the work-group takes block
-// 64u + q; lane p of the quad loads chunks p, p+4, ... of the block, so each
-// load instruction reads 64 contiguous bytes per quad.  Rows are folded over
-// the batch by the host; `ld` is the row stride.
+// 1xB row blocks (B = 8*LPB, LPB = 4..64 lanes per block).  The 64 lanes of a
+// wave cover 64 consecutive 8-element chunks, so each load instruction reads
+// one contiguous span (1 KiB of bf16) and each store writes whole 128-byte
+// code lines; lane c of a block holds chunk c of it.  Instruction j of wave w
+// covers blocks (4w + j) * (64 / LPB) + lane / LPB of the work-group.
+// The block amax is reduced over its LPB lanes (DPP within 16 lanes, shuffles
+// beyond).  Each lane then computes the scale of ONE of its four blocks and
+// the four scales are exchanged by shuffles, so the IEEE divisions cost one
+// pair per lane instead of four.  Rows are folded over the batch by the host.
 // ---------------------------------------------------------------------------
-template <int DT, int CDT, int CPL>
-__global__ __launch_bounds__(256) void k_rowquad(Desc single, const Desc* __restrict__ descs,
-                                                 const uint32_t* __restrict__ map, int pow2,
-                                                 int scale_bf16) {
-  constexpr int B = 32 * CPL;
+template <int LPB>
+__device__ __forceinline__ uint32_t group_max(uint32_t v) {
+  uint32_t o;
+  if constexpr (LPB >= 2) { o = (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0xB1, 0xF, 0xF, false); v = v > o ? v : o; }
+  if constexpr (LPB >= 4) { o = (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x4E, 0xF, 0xF, false); v = v > o ? v : o; }
+  // row_half_mirror: lane i <- lane 7-i within its 8-lane half (joins the two
+  // quads of an 8-lane group); row_mirror: lane i <- lane 15-i (joins halves)
+  if constexpr (LPB >= 8) { o = (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x141, 0xF, 0xF, false); v = v > o ? v : o; }
+  if constexpr (LPB >= 16) { o = (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x140, 0xF, 0xF, false); v = v > o ? v : o; }
+  if constexpr (LPB >= 32) { o = (uint32_t)__shfl_xor((int)v, 16, 64); v = v > o ? v : o; }
+  if constexpr (LPB >= 64) { o = (uint32_t)__shfl_xor((int)v, 32, 64); v = v > o ? v : o; }
+  return v;
+}
+
+template <int DT, int CDT, int LPB>
+__global__ __launch_bounds__(256) void k_row(Desc single, const Desc* __restrict__ descs,
+                                             const uint32_t* __restrict__ map, int pow2,
+                                             int scale_bf16) {
+  constexpr int B = 8 * LPB;          // elements per block
+  constexpr int BPI = 64 / LPB;       // blocks per wave instruction
   Desc d;
   int64_t u;
   pick_desc(single, descs, map, d, u);
-  const int tid = threadIdx.x;
-  const int p = tid & 3;
-  const int64_t gb = u * 64 + (tid >> 2);
-  if (gb >= d.nblocks) return;  // whole quads leave together; no barriers below
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int c = lane & (LPB - 1);     // chunk of the block held by this lane
+  const int64_t wb = u * (16 * BPI) + (tid >> 6) * (4 * BPI) + lane / LPB;  // block at j = 0
 
-  int64_t in_base;
-  if (d.ld == d.cols) {
-    in_base = gb * B;
-  } else {
-    const int64_t row = gb / d.bpr;
-    in_base = row * d.ld + (gb - row * d.bpr) * B;
+  Chunk<DT> ch[4];
+  bool ok[4];
+  uint32_t am[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int64_t gb = wb + j * BPI;
+    ok[j] = gb < d.nblocks;
+    if (ok[j]) {
+      int64_t off;
+      if (d.ld == d.cols) {
+        off = gb * B + c * 8;
+      } else {
+        const int64_t row = gb / d.bpr;
+        off = row * d.ld + (gb - row * d.bpr) * B + c * 8;
+      }
+      load_chunk<DT>(ch[j], d.in, off);
+    } else {
+      zero_chunk<DT>(ch[j]);
+    }
   }
-  const int64_t out_base = gb * B;
-
-  Chunk<DT> ch[CPL];
 #pragma unroll
-  for (int j = 0; j < CPL; ++j) load_chunk<DT>(ch[j], d.in, in_base + (p + 4 * j) * 8);
-
-  Amax<DT> am;
-  am.init();
+  for (int j = 0; j < 4; ++j) {
+    Amax<DT> a;
+    a.init();
+    a.add(ch[j]);
+    am[j] = group_max<LPB>(a.bits());  // every lane takes part: groups never straddle
+  }
+  // lane c computes the scale of block j = c & 3 of its group; gather all four
+  const uint32_t mine = (c & 3) == 0 ? am[0] : ((c & 3) == 1 ? am[1] : ((c & 3) == 2 ? am[2] : am[3]));
+  const BlockScale own = block_scale<CDT>(mine, pow2 != 0);
+  BlockScale bs[4];
 #pragma unroll
-  for (int j = 0; j < CPL; ++j) am.add(ch[j]);
-  const uint32_t a = quad_max(am.bits());
-
-  const BlockScale bs = block_scale<CDT>(a, pow2 != 0);
-  if (p == 0) store_scale<CDT>(d.scales, gb, bs.s, scale_bf16);
+  for (int j = 0; j < 4; ++j) {
+    const int src = (lane & ~(LPB - 1)) | j;
+    bs[j].s = __shfl(own.s, src, 64);
+    bs[j].y = __shfl(own.y, src, 64);
+    bs[j].kind = __shfl(own.kind, src, 64);
+  }
 #pragma unroll
-  for (int j = 0; j < CPL; ++j) {
-    const v2u q = encode_chunk<DT, CDT>(ch[j], bs);
-    store_nt(d.codes + out_base + (p + 4 * j) * 8, q);
+  for (int j = 0; j < 4; ++j) {
+    if (!ok[j]) continue;
+    const int64_t gb = wb + j * BPI;
+    if (c == 0) store_scale<CDT>(d.scales, gb, bs[j].s, scale_bf16);
+    store_nt(d.codes + gb * B + c * 8, encode_chunk<DT, CDT>(ch[j], bs[j]));
   }
 }
 
@@ -310,11 +349,11 @@ static hipError_t launch_fp8_typed(const LaunchCfg& cfg, const Desc& single, con
       break;
     case kKernRowQuad:
       switch (cfg.blk_c) {
-        case 32: hipLaunchKernelGGL((k_rowquad<DT, CDT, 1>), grid, block, 0, stream, single, descs, map, cfg.pow2, cfg.scale_bf16); break;
-        case 64: hipLaunchKernelGGL((k_rowquad<DT, CDT, 2>), grid, block, 0, stream, single, descs, map, cfg.pow2, cfg.scale_bf16); break;
-        case 128: hipLaunchKernelGGL((k_rowquad<DT, CDT, 4>), grid, block, 0, stream, single, descs, map, cfg.pow2, cfg.scale_bf16); break;
-        case 256: hipLaunchKernelGGL((k_rowquad<DT, CDT, 8>), grid, block, 0, stream, single, descs, map, cfg.pow2, cfg.scale_bf16); break;
-        case 512: hipLaunchKernelGGL((k_rowquad<DT, CDT, 16>), grid, block, 0, stream, single, descs, map, cfg.pow2, cfg.scale_bf16); break;
+        case 32: hipLaunchKernelGGL((k_row<DT, CDT, 4>), grid, block, 0, stream, single, descs, map, cfg.pow2, cfg.scale_bf16); break;
+        case 64: hipLaunchKernelGGL((k_row<DT, CDT, 8>), grid, block, 0, stream, single, descs, map, cfg.pow2, cfg.scale_bf16); break;
+        case 128: hipLaunchKernelGGL((k_row<DT, CDT, 16>), grid, block, 0, stream, single, descs, map, cfg.pow2, cfg.scale_bf16); break;
+        case 256: hipLaunchKernelGGL((k_row<DT, CDT, 32>), grid, block, 0, stream, single, descs, map, cfg.pow2, cfg.scale_bf16); break;
+        case 512: hipLaunchKernelGGL((k_row<DT, CDT, 64>), grid, block, 0, stream, single, descs, map, cfg.pow2, cfg.scale_bf16); break;
         default: return hipErrorInvalidValue;
       }
       break;

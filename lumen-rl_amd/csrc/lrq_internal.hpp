@@ -25,7 +25,7 @@ static_assert(sizeof(Desc) == 112, "Desc layout is part of the grouped table for
 
 enum Kernel : int {
   kKernTile128 = 0,   // 128x128 FP8 tiles, one work-group per tile
-  kKernRowQuad = 1,   // 1xB FP8 blocks, one quad per block
+  kKernRowQuad = 1,   // 1xB FP8 blocks, B/8 consecutive lanes per block
   kKernGenericFp8 = 2,
   kKernMx = 3,        // MXFP8 / MXFP4, one quad per 32-group
   kKernGenericMx = 4,
@@ -58,6 +58,7 @@ hipError_t launch_dequant(const uint8_t* codes, const void* scales, int scale_dt
 
 // Diagnostics: element encoders applied to raw inputs.
 hipError_t launch_diag_e4m3_bits(uint32_t start, int64_t n, uint8_t* out, hipStream_t stream);
-hipError_t launch_diag_e2m1(const float* in, uint8_t* out, int64_t n, hipStream_t stream);
+hipError_t launch_diag_mx(int fmt, const float* in, const uint8_t* e8m0, int64_t n, uint8_t* out,
+                          hipStream_t stream);
 
 }  // namespace lrq

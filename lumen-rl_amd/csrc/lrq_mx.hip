@@ -6,7 +6,8 @@
 // aiter quant_mxfp8, examples/DAPO/atom_aiter_shim/sitecustomize.py:31-32).
 // Per 1x32 group along the last dim: E8M0 = clamp(floor(log2 amax) - emax +
 // 127, 0, 254) (0xFF for inf/NaN groups); elements x * 2^(127-E8M0) rounded to
-// nearest even, saturating (E4M3 +-448, E2M1 +-6).
+// nearest even, saturating (E4M3 +-448, E2M1 +-6).  E2M1 uses gfx950's scaled
+// FP4 pack-convert; E4M3 scales, clamps and uses the FP8 pack-convert.
 //
 // k_mx: a quad of lanes per group (8 elements per lane); wave w of the
 // work-group takes groups 256u + 64w + 16j + (lane>>2), j = 0..3, so each load
@@ -61,19 +62,18 @@ template <int DT, int FMT>
 __device__ __forceinline__ v2u mx_encode8(const uint32_t (&w)[8], uint32_t e8m0) {
   v2u r;
   if (e8m0 != 0xFFu) {
-    const float mult = mx_mult(e8m0);
-    float v[8];
-#pragma unroll
-    for (int i = 0; i < 8; ++i) v[i] = mx_elem<DT>(w, i) * mult;
     if constexpr (FMT == 8) {
+      const float mult = mx_mult(e8m0);
+      float v[8];
 #pragma unroll
-      for (int i = 0; i < 8; ++i) v[i] = __builtin_amdgcn_fmed3f(v[i], -448.0f, 448.0f);
+      for (int i = 0; i < 8; ++i) v[i] = __builtin_amdgcn_fmed3f(mx_elem<DT>(w, i) * mult, -448.0f, 448.0f);
       r.x = cvt_e4m3x4(v[0], v[1], v[2], v[3]);
       r.y = cvt_e4m3x4(v[4], v[5], v[6], v[7]);
     } else {
-      uint32_t n = 0u;
-#pragma unroll
-      for (int i = 0; i < 8; ++i) n |= e2m1_code(v[i]) << (4 * i);
+      uint32_t n = mx_fp4x2<0>(0u, mx_elem<DT>(w, 0), mx_elem<DT>(w, 1), e8m0);
+      n = mx_fp4x2<1>(n, mx_elem<DT>(w, 2), mx_elem<DT>(w, 3), e8m0);
+      n = mx_fp4x2<2>(n, mx_elem<DT>(w, 4), mx_elem<DT>(w, 5), e8m0);
+      n = mx_fp4x2<3>(n, mx_elem<DT>(w, 6), mx_elem<DT>(w, 7), e8m0);
       r.x = n;
       r.y = 0u;
     }
@@ -213,6 +213,38 @@ __global__ __launch_bounds__(256) void k_mx_generic(Desc single, const Desc* __r
       out[i / 2] = (uint8_t)(lo | (hi << 4));
     }
   }
+}
+
+// Diagnostic: the element path of k_mx on raw inputs; pair k = elements
+// (2k, 2k+1) shares E8M0 byte e8m0[k]; one output byte (code or nibble) per element.
+template <int FMT>
+__global__ __launch_bounds__(256) void k_diag_mx(const float* __restrict__ in,
+                                                 const uint8_t* __restrict__ e8m0, int64_t npairs,
+                                                 uint8_t* __restrict__ out) {
+  const int64_t k = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (k >= npairs) return;
+  uint32_t w[8];
+  w[0] = f2u(in[2 * k]);
+  w[1] = f2u(in[2 * k + 1]);
+#pragma unroll
+  for (int i = 2; i < 8; ++i) w[i] = 0u;
+  const v2u c = mx_encode8<kF32, FMT>(w, e8m0[k]);
+  if constexpr (FMT == 8) {
+    out[2 * k] = (uint8_t)(c.x & 0xFFu);
+    out[2 * k + 1] = (uint8_t)((c.x >> 8) & 0xFFu);
+  } else {
+    out[2 * k] = (uint8_t)(c.x & 0xFu);
+    out[2 * k + 1] = (uint8_t)((c.x >> 4) & 0xFu);
+  }
+}
+
+hipError_t launch_diag_mx(int fmt, const float* in, const uint8_t* e8m0, int64_t n, uint8_t* out,
+                          hipStream_t stream) {
+  const int64_t npairs = n / 2;
+  const dim3 grid((unsigned)((npairs + 255) / 256)), block(256);
+  if (fmt == 8) hipLaunchKernelGGL((k_diag_mx<8>), grid, block, 0, stream, in, e8m0, npairs, out);
+  else hipLaunchKernelGGL((k_diag_mx<4>), grid, block, 0, stream, in, e8m0, npairs, out);
+  return hipGetLastError();
 }
 
 template <int DT>

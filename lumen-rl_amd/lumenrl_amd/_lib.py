@@ -52,7 +52,7 @@ SIGNATURES = {
     "lrq_version": (ctypes.c_char_p, []),
     "lrq_last_error": (ctypes.c_char_p, []),
     "lrq_diag_e4m3_bits": (_CI, [ctypes.c_uint32, _I64, _VP, _VP]),
-    "lrq_diag_e2m1": (_CI, [_VP, _VP, _I64, _VP]),
+    "lrq_diag_mx_encode": (_CI, [_CI, _VP, _VP, _VP, _I64, _VP]),
 }
 
 _lock = threading.Lock()

@@ -128,6 +128,7 @@ def test_group_pack_rows_and_mx_units():
     shapes = [(1, 256, 4096), (1, 64, 12288)]
     buf = _pack(_lib.FMT_FP8_BLOCK, shapes, (1, 128))
     blocks = 256 * 32 + 64 * 96
+    # 1x128 rows: 16 lanes per block, 4 blocks per wave instruction, 64 blocks per work-group
     assert L().lrq_group_units(buf.ctypes.data) == -(-256 * 32 // 64) + -(-64 * 96 // 64)
     buf = _pack(_lib.FMT_MXFP4, shapes, (1, 32))
     assert L().lrq_group_units(buf.ctypes.data) == -(-256 * 128 // 256) + -(-64 * 384 // 256)

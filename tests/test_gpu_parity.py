@@ -124,18 +124,39 @@ def test_hw_e4m3_encoder_all_float32_patterns():
     assert nan_codes <= {0x7F, 0xFF}
 
 
-def test_e2m1_device_encoder_vs_oracle():
+@pytest.mark.parametrize("fmt", [8, 4])
+def test_mx_element_path_every_bf16_and_scale(fmt):
+    """The MX kernels' element encoder on every finite bf16 x under every E8M0
+    the format can produce (E4M3: 0..246, E2M1: 0..252) vs the oracle's
+    element rule: x * 2^(127-E), E4M3 clamp +-448 / E2M1 saturation, RNE."""
     b = np.arange(0, 1 << 16, dtype=np.uint32)
     xb = (b << 16).view(np.float32)
     xb = xb[np.isfinite(xb)]
-    with np.errstate(over="ignore"):
-        v = np.concatenate([xb * np.float32(2.0 ** k) for k in range(-24, 25)])
-    v = v[np.isfinite(v)].astype(np.float32)
-    vd = torch.from_numpy(v).to(DEV)
-    out = torch.empty(v.size, dtype=torch.uint8, device=DEV)
-    _lib.check(_lib.lib().lrq_diag_e2m1(vd.data_ptr(), out.data_ptr(), v.size, None), "diag")
+    if xb.size % 2:
+        xb = xb[:-1]
+    emax_byte = 246 if fmt == 8 else 252
+    es = np.arange(0, emax_byte + 1, dtype=np.uint8)
+    x = np.tile(xb, es.size)
+    e_pair = np.repeat(es, xb.size // 2)
+    e_elem = np.repeat(es, xb.size).astype(np.int64)
+    with np.errstate(over="ignore", under="ignore"):
+        v = np.ldexp(x.astype(np.float64), 127 - e_elem)
+    if fmt == 8:
+        want = O.e4m3_from_f32(np.clip(v, -448.0, 448.0).astype(np.float32))
+    else:
+        want = O.e2m1_from_f32(np.clip(v, -6.0, 6.0).astype(np.float32))
+    xd = torch.from_numpy(x).to(DEV)
+    ed = torch.from_numpy(e_pair).to(DEV)
+    out = torch.empty(x.size, dtype=torch.uint8, device=DEV)
+    rc = _lib.lib().lrq_diag_mx_encode(_lib.FMT_MXFP8 if fmt == 8 else _lib.FMT_MXFP4,
+                                       xd.data_ptr(), ed.data_ptr(), out.data_ptr(), x.size, None)
+    _lib.check(rc, "lrq_diag_mx_encode")
     torch.cuda.synchronize()
-    assert np.array_equal(out.cpu().numpy(), O.e2m1_from_f32(v))
+    got = out.cpu().numpy()
+    bad = np.argwhere(got != want).ravel()
+    if bad.size:
+        say("mx encode mismatch", [(float(x[i]), int(e_elem[i]), hex(got[i]), hex(want[i])) for i in bad[:6]])
+    assert bad.size == 0
 
 
 # ----------------------------------------------------------------------------
