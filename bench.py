@@ -42,6 +42,11 @@ QWEN3_8B = [("q_proj", 4096, 4096), ("k_proj", 1024, 4096), ("v_proj", 1024, 409
             ("down_proj", 4096, 12288)]
 
 
+PROFILE_FOR = {"c2": "k_tile128_qwen3_8b_fp8_128x128", "c2r": "k_row_qwen3_8b_fp8_1x128",
+               "c3": "k_tile128_qwen3_30b_a3b_experts", "c4": "k_mx_qwen3_8b_mxfp8",
+               "c5": "k_mx_qwen3_8b_mxfp4"}
+
+
 def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
@@ -240,11 +245,15 @@ def run(args):
     log(f"[bench] {ms_per_step:.4f} ms/step, {value:.1f} GB/s; kernel avg {kern_ms:.4f} ms "
         f"({achieved:.1f} GB/s = {achieved / HBM_PEAK_GBS:.1%} of 8 TB/s)")
 
+    # HBM bytes per launch of the dominant kernel, from the committed rocprofv3
+    # FETCH_SIZE/WRITE_SIZE summary of this workload (copy-calibrated)
     traffic = None
-    tfile = os.path.join(ROOT, "profiles", f"traffic_{cfg}.json")
-    if os.path.exists(tfile):
-        with open(tfile) as f:
-            traffic = json.load(f).get("hbm_bytes_per_launch")
+    pfile = os.path.join(ROOT, "profiles", PROFILE_FOR.get(cfg, "") + ".md")
+    if os.path.exists(pfile):
+        with open(pfile) as f:
+            for line in f:
+                if line.startswith("hbm_bytes_per_launch:"):
+                    traffic = int(line.split(":", 1)[1])
 
     result = {
         "metric": metric_name(),
