@@ -14,6 +14,8 @@ already resident in HBM:
   c4: c2 shapes, Student-t(4) x 0.02/sqrt(2), MXFP8.
   c5: c2 shapes, N(0, 0.02^2) x per-row log-uniform[0.25, 4], MXFP4.
   c2r: c2 weights with the reference's own 1x128 blocks (scales [N, K/128]).
+  c2d: dequantize_state_dict of the c2r result: e4m3 codes + bf16 1x128 scales ->
+       bf16 weights, ONE grouped launch.
 
 Prints ONE JSON line on stdout.  value = algorithmic bytes (bf16 in + codes +
 scales) per step / step time, in GB/s (1e9 B/s).  The roofline object uses the
@@ -170,7 +172,17 @@ def run(args):
     t0 = time.time()
 
     flush = None
-    if cfg in ("c2", "c4", "c5", "c2r"):
+    if cfg == "c2d":
+        ws, _ = qwen3_8b_set(torch, dev, args.seed, "normal")
+        qp = ops.QuantPlan(ws, "fp8_block", (1, 128), scale_dtype=torch.bfloat16)
+        pairs = qp.run()
+        torch.cuda.synchronize()
+        plans = [ops.DequantPlan(pairs, (1, 128), torch.bfloat16)]
+        workload = "qwen3-8b-linears-fp8-1x128-dequant-to-bf16"
+        cpu_ws, cpu_blk, cpu_fmt = [], (1, 128), "fp8_dequant"
+        extra = {"tensors": len(pairs), "layers": 36, "elements": sum(c.numel() for c, _ in pairs),
+                 "format": "fp8_dequant", "launches_per_step": 1}
+    elif cfg in ("c2", "c4", "c5", "c2r"):
         kind = {"c2": "normal", "c4": "student_t", "c5": "rowscale", "c2r": "normal"}[cfg]
         fmt = {"c2": "fp8_block", "c4": "mxfp8", "c5": "mxfp4", "c2r": "fp8_block"}[cfg]
         blk = (1, 128) if cfg == "c2r" else (128, 128)
@@ -280,7 +292,7 @@ def run(args):
             "launch_ms": round(kern_ms, 5),
         },
     }
-    if not args.no_cpu:
+    if not args.no_cpu and cpu_ws:
         log("[bench] cpu baseline ...")
         result["cpu_baseline"] = cpu_baseline(torch, cpu_ws, cpu_fmt, cpu_blk, args.cpu_seconds)
     print(json.dumps(result), flush=True)
@@ -313,7 +325,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--config", default="c2", choices=["c1", "c2", "c3", "c4", "c5", "c2r"])
+    ap.add_argument("--config", default="c2", choices=["c1", "c2", "c3", "c4", "c5", "c2r", "c2d"])
     ap.add_argument("--seed", type=int, default=1000)
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")

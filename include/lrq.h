@@ -43,11 +43,14 @@ typedef struct ihipStream_t* lrq_stream_t; /* == hipStream_t */
 #define LRQ_FLAG_SCALE_BF16 4u   /* write float32-arithmetic scales rounded to bf16, the
                                     `_fp8_scales` sidecar of quantize_state_dict
                                     (weight_quantizer.py:111) */
+#define LRQ_FLAG_OUT_BF16 8u     /* grouped dequant: bf16 output (dequantize_state_dict) */
 
 /* formats (grouped launches) */
 #define LRQ_FMT_FP8_BLOCK 0
 #define LRQ_FMT_MXFP8 1
 #define LRQ_FMT_MXFP4 2
+#define LRQ_FMT_FP8_DEQUANT 3 /* grouped dequant: lrq_tensor.in = codes, .codes = output,
+                                 in_dtype = scale dtype, LRQ_FLAG_OUT_BF16 = bf16 output */
 
 /* errors */
 #define LRQ_ERR_ARG (-1)      /* invalid argument (shape, dtype, block size, null) */
@@ -115,6 +118,8 @@ int lrq_mxfp4_quant(const void* in, int in_dtype, int64_t rows, int64_t cols, in
  *    is what the kernel reads.
  * All tensors of a table share fmt, in_dtype, block shape and flags, and must
  * all qualify for the same kernel (the pack fails otherwise).
+ * With fmt LRQ_FMT_FP8_DEQUANT the same tables drive the grouped inverse:
+ * WeightQuantizer.dequantize_state_dict (weight_quantizer.py:117-134) in one launch.
  */
 typedef struct lrq_tensor {
   const void* in;       /* device input */
@@ -144,12 +149,15 @@ const char* lrq_last_error(void);
  * to raw inputs, so tests can compare them with the CPU oracle exhaustively.
  *   lrq_diag_e4m3_bits: out[i] = e4m3(float with bit pattern start + i), via
  *     the hardware pack-convert the FP8 kernels use; n a multiple of 4.
+ *   lrq_diag_bf16_bits: out[i] = bf16 (bit pattern) of the float with bit pattern
+ *     start + i, via the hardware pack-convert the dequant kernel uses; n even.
  *   lrq_diag_mx_encode: the MXFP8 (fmt LRQ_FMT_MXFP8) or MXFP4 (LRQ_FMT_MXFP4)
  *     element path of the MX kernel: elements 2k and 2k+1 of `in` encoded
  *     under E8M0 byte e8m0[k]; out[i] = E4M3 byte or E2M1 nibble of in[i];
  *     n even.
  */
 int lrq_diag_e4m3_bits(uint32_t start, int64_t n, uint8_t* out, lrq_stream_t stream);
+int lrq_diag_bf16_bits(uint32_t start, int64_t n, uint16_t* out, lrq_stream_t stream);
 int lrq_diag_mx_encode(int fmt, const float* in, const uint8_t* e8m0, uint8_t* out, int64_t n,
                        lrq_stream_t stream);
 

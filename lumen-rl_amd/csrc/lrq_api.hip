@@ -10,11 +10,6 @@
 #include "lrq_device.hpp"
 #include "lrq_internal.hpp"
 
-namespace lrq {
-hipError_t launch_fp8(const LaunchCfg&, const Desc&, const Desc*, const uint32_t*, int64_t, hipStream_t);
-hipError_t launch_mx(const LaunchCfg&, const Desc&, const Desc*, const uint32_t*, int64_t, hipStream_t);
-}  // namespace lrq
-
 using lrq::Desc;
 using lrq::LaunchCfg;
 
@@ -97,6 +92,11 @@ int fp8_kernel_for(const Desc& d, int in_dtype, int64_t blk_r, int64_t blk_c) {
   return lrq::kKernGenericFp8;
 }
 
+int dequant_kernel_for(const Desc& d, int64_t blk_c) {
+  const bool vec = aligned(d.in, 16) && aligned(d.codes, 16) && d.cols % 16 == 0 && blk_c % 16 == 0;
+  return vec ? lrq::kKernDequant : lrq::kKernGenericDequant;
+}
+
 int mx_kernel_for(const Desc& d, int in_dtype, int fmt) {
   const int64_t es = esize(in_dtype);
   const bool vec = aligned(d.in, 16) && (d.ld * es) % 16 == 0 &&
@@ -129,6 +129,19 @@ bool plan_units(const LaunchCfg& cfg, Desc& d) {
       d.units = (d.nblocks + per_wg - 1) / per_wg;
       return true;
     }
+    case kKernDequant:
+    case kKernGenericDequant:
+      d.units_r = (d.rows + cfg.blk_r - 1) / cfg.blk_r;
+      d.units_c = (d.cols + cfg.blk_c - 1) / cfg.blk_c;
+      if (cfg.kernel == kKernDequant) {
+        const int64_t cpc = cfg.out_dtype == kBF16 ? 8 : 4;  // codes per lane-chunk
+        d.nblocks = d.batch * d.rows * d.cols / cpc;
+        d.units = (d.nblocks + 2047) / 2048;                  // 256 lanes x 8 chunks
+      } else {
+        d.nblocks = d.batch * d.rows * d.cols;
+        d.units = (d.nblocks + 255) / 256;
+      }
+      return true;
     case kKernMx:
     case kKernGenericMx:
       if (!fold_batch(d)) {
@@ -148,6 +161,8 @@ hipError_t launch(const LaunchCfg& cfg, const Desc& single, const Desc* descs_de
                   const uint32_t* map_dev, int64_t total_units, hipStream_t stream) {
   if (cfg.kernel == kKernMx || cfg.kernel == kKernGenericMx)
     return launch_mx(cfg, single, descs_dev, map_dev, total_units, stream);
+  if (cfg.kernel == kKernDequant || cfg.kernel == kKernGenericDequant)
+    return launch_dequant(cfg, single, descs_dev, map_dev, total_units, stream);
   return launch_fp8(cfg, single, descs_dev, map_dev, total_units, stream);
 }
 
@@ -204,6 +219,12 @@ int plan_group(int fmt, const lrq_tensor* ts, int64_t n, int in_dtype, int64_t b
     cfg.scale_bf16 = (flags & LRQ_FLAG_SCALE_BF16) && !cfg.arith ? 1 : 0;
   } else if (fmt == LRQ_FMT_MXFP8 || fmt == LRQ_FMT_MXFP4) {
     cfg.mx_fmt = fmt == LRQ_FMT_MXFP8 ? 8 : 4;
+  } else if (fmt == LRQ_FMT_FP8_DEQUANT) {
+    if (blk_r < 1 || blk_c < 1 || blk_r > (1 << 20) || blk_c > (1 << 20))
+      return fail(LRQ_ERR_ARG, "bad block %lldx%lld", (long long)blk_r, (long long)blk_c);
+    cfg.blk_r = (int)blk_r;
+    cfg.blk_c = (int)blk_c;
+    cfg.out_dtype = (flags & LRQ_FLAG_OUT_BF16) ? lrq::kBF16 : lrq::kF32;
   } else {
     return fail(LRQ_ERR_ARG, "bad format %d", fmt);
   }
@@ -219,6 +240,10 @@ int plan_group(int fmt, const lrq_tensor* ts, int64_t n, int in_dtype, int64_t b
     int k;
     if (fmt == LRQ_FMT_FP8_BLOCK) {
       k = fp8_kernel_for(d, in_dtype, blk_r, blk_c);
+    } else if (fmt == LRQ_FMT_FP8_DEQUANT) {
+      if (d.ld != d.cols || d.bstride != d.rows * d.cols)
+        return fail(LRQ_ERR_ARG, "tensor %lld: dequant needs dense codes (ld == cols)", (long long)i);
+      k = dequant_kernel_for(d, blk_c);
     } else {
       if (d.cols % 32 != 0) return fail(LRQ_ERR_ARG, "tensor %lld: cols %% 32 != 0", (long long)i);
       k = mx_kernel_for(d, in_dtype, cfg.mx_fmt);
@@ -235,6 +260,11 @@ int plan_group(int fmt, const lrq_tensor* ts, int64_t n, int in_dtype, int64_t b
     if (ds) ds[i] = d;
   }
   if (kernel < 0) cfg.kernel = fmt == LRQ_FMT_FP8_BLOCK ? lrq::kKernGenericFp8 : lrq::kKernGenericMx;
+  if (fmt == LRQ_FMT_FP8_DEQUANT) {
+    cfg.rows_dense = 1;
+    for (int64_t i = 0; i < n; ++i)
+      if (ts[i].cols % blk_c != 0) cfg.rows_dense = 0;
+  }
   if (units > kMaxGrid) return fail(LRQ_ERR_ARG, "group too large for one launch");
   *cfg_out = cfg;
   *units_out = units;
@@ -264,15 +294,17 @@ int lrq_fp8_block_dequant(const uint8_t* codes, const void* scales, int scale_dt
                           int64_t batch, int64_t rows, int64_t cols, int64_t blk_r,
                           int64_t blk_c, void* out, int out_dtype, lrq_stream_t stream) {
   g_err.clear();
-  if (!valid_dtype(scale_dtype)) return fail(LRQ_ERR_ARG, "bad scale dtype %d", scale_dtype);
   if (out_dtype != lrq::kF32 && out_dtype != lrq::kBF16) return fail(LRQ_ERR_ARG, "bad out dtype %d", out_dtype);
-  if (batch < 0 || rows < 0 || cols < 0 || blk_r < 1 || blk_c < 1 || blk_r > (1 << 20) || blk_c > (1 << 20))
-    return fail(LRQ_ERR_ARG, "bad shape or block");
-  if (batch * rows * cols == 0) return 0;
-  if (!codes || !scales || !out) return fail(LRQ_ERR_ARG, "null pointer");
-  return check_hip(lrq::launch_dequant(codes, scales, scale_dtype, batch, rows, cols, (int)blk_r,
-                                       (int)blk_c, out, out_dtype, (hipStream_t)stream),
-                   "kernel launch");
+  lrq_tensor t{codes, out, const_cast<void*>(scales), batch, rows, cols, cols, rows * cols};
+  LaunchCfg cfg;
+  Desc d;
+  int64_t units;
+  const unsigned flags = out_dtype == lrq::kBF16 ? LRQ_FLAG_OUT_BF16 : 0u;
+  if (int rc = plan_group(LRQ_FMT_FP8_DEQUANT, &t, 1, scale_dtype, blk_r, blk_c, flags, &cfg, &d, &units))
+    return rc;
+  if (units == 0) return 0;
+  d.unit0 = 0;
+  return check_hip(lrq::launch(cfg, d, nullptr, nullptr, units, (hipStream_t)stream), "kernel launch");
 }
 
 int lrq_mxfp8_quant(const void* in, int in_dtype, int64_t rows, int64_t cols, int64_t ld,
@@ -355,6 +387,13 @@ int lrq_diag_e4m3_bits(uint32_t start, int64_t n, uint8_t* out, lrq_stream_t str
   if (n <= 0 || n % 4 != 0 || !out || !aligned(out, 4)) return fail(LRQ_ERR_ARG, "bad diag args");
   if ((n / 4 + 255) / 256 > kMaxGrid) return fail(LRQ_ERR_ARG, "n too large");
   return check_hip(lrq::launch_diag_e4m3_bits(start, n, out, (hipStream_t)stream), "kernel launch");
+}
+
+int lrq_diag_bf16_bits(uint32_t start, int64_t n, uint16_t* out, lrq_stream_t stream) {
+  g_err.clear();
+  if (n <= 0 || n % 2 != 0 || !out || !aligned(out, 4)) return fail(LRQ_ERR_ARG, "bad diag args");
+  if ((n / 2 + 255) / 256 > kMaxGrid) return fail(LRQ_ERR_ARG, "n too large");
+  return check_hip(lrq::launch_diag_bf16_bits(start, n, out, (hipStream_t)stream), "kernel launch");
 }
 
 int lrq_diag_mx_encode(int fmt, const float* in, const uint8_t* e8m0, uint8_t* out, int64_t n,

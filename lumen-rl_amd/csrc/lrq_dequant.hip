@@ -26,47 +26,146 @@ __device__ __forceinline__ float x86_mul(float v, float s) {
   return v * s;
 }
 
+template <int SDT>
+__device__ __forceinline__ float load_scale(const void* scales, int64_t i) {
+  if constexpr (SDT == kF32) return static_cast<const float*>(scales)[i];
+  else if constexpr (SDT == kBF16) return u2f((uint32_t)static_cast<const uint16_t*>(scales)[i] << 16);
+  else return f16_to_f32(static_cast<const uint16_t*>(scales)[i]);
+}
+
+// Scale index of element (b, r, c) of a [batch, rows, cols] tensor.
+__device__ __forceinline__ int64_t scale_index(const Desc& d, int64_t e, int blk_r, int blk_c) {
+  const int64_t br = e / d.cols, c = e - br * d.cols;
+  const int64_t b = br / d.rows, r = br - b * d.rows;
+  return (b * d.units_r + r / blk_r) * d.units_c + c / blk_c;
+}
+
+// Generic: one element per thread, any shape and alignment.
 template <int SDT, int ODT>
-__global__ __launch_bounds__(256) void k_dequant(const uint8_t* __restrict__ codes,
-                                                 const void* __restrict__ scales, int64_t batch,
-                                                 int64_t rows, int64_t cols, int blk_r, int blk_c,
-                                                 void* __restrict__ out) {
-  const int64_t tr = (rows + blk_r - 1) / blk_r, tc = (cols + blk_c - 1) / blk_c;
-  const int64_t n = batch * rows * cols;
-  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) {
-    const int64_t br = i / cols, c = i - br * cols;
-    const int64_t b = br / rows, r = br - b * rows;
-    const int64_t si = (b * tr + r / blk_r) * tc + c / blk_c;
-    float s;
-    if constexpr (SDT == kF32) s = static_cast<const float*>(scales)[si];
-    else if constexpr (SDT == kBF16) s = u2f((uint32_t)static_cast<const uint16_t*>(scales)[si] << 16);
-    else s = f16_to_f32(static_cast<const uint16_t*>(scales)[si]);
-    const float o = x86_mul(e4m3_decode(codes[i]), s);
-    if constexpr (ODT == kF32) static_cast<float*>(out)[i] = o;
-    else static_cast<uint16_t*>(out)[i] = (uint16_t)bf16_bits(o);
+__global__ __launch_bounds__(256) void k_dequant_generic(Desc single, const Desc* __restrict__ descs,
+                                                         const uint32_t* __restrict__ map, int blk_r,
+                                                         int blk_c) {
+  Desc d;
+  int64_t u;
+  pick_desc(single, descs, map, d, u);
+  const int64_t i = u * 256 + threadIdx.x;
+  if (i >= d.nblocks) return;
+  const uint8_t* codes = static_cast<const uint8_t*>(d.in);
+  const float o = x86_mul(e4m3_decode(codes[i]), load_scale<SDT>(d.scales, scale_index(d, i, blk_r, blk_c)));
+  if constexpr (ODT == kF32) reinterpret_cast<float*>(d.codes)[i] = o;
+  else reinterpret_cast<uint16_t*>(d.codes)[i] = (uint16_t)bf16_bits(o);
+}
+
+// Vectorized: a lane-chunk is CPC codes (8 for bf16 output, 4 for fp32) whose
+// output is exactly one 16-byte store, so every wave load and store
+// instruction covers one contiguous span (512 B / 256 B of codes, 1 KiB out);
+// eight chunks per lane keep enough loads in flight.  A chunk lies inside one
+// block (blk_c % 16 == 0), so its scale is uniform: when the scale is finite
+// and non-zero and no code is NaN the chunk takes the hardware path
+// (v_cvt_pk_f32_fp8 -> multiply -> v_cvt_pk_bf16_f32); anything else takes the
+// explicit x86 rules.  ROWS1: 1xB blocks over dense rows (scale = element / blk_c).
+__device__ __forceinline__ bool word_has_nan_code(uint32_t w) {
+  // byte c has (c & 0x7F) == 0x7F  <=>  adding 1 to its low 7 bits carries into bit 7
+  return (((w & 0x7F7F7F7Fu) + 0x01010101u) & 0x80808080u) != 0u;
+}
+
+template <int SDT, int ODT, bool ROWS1>
+__global__ __launch_bounds__(256) void k_dequant(Desc single, const Desc* __restrict__ descs,
+                                                 const uint32_t* __restrict__ map, int blk_r, int blk_c) {
+  constexpr int CPC = ODT == kBF16 ? 8 : 4;  // codes per lane-chunk
+  constexpr int NW = CPC / 4;                // code words per chunk
+  constexpr int NCH = 8;                     // chunks per lane
+  Desc d;
+  int64_t u;
+  pick_desc(single, descs, map, d, u);
+  const int tid = threadIdx.x;
+  const uint8_t* codes = static_cast<const uint8_t*>(d.in);
+  uint32_t cw[NCH][NW];
+  float sc[NCH];
+  bool ok[NCH];
+#pragma unroll
+  for (int j = 0; j < NCH; ++j) {
+    const int64_t ch = u * (256 * NCH) + j * 256 + tid;
+    ok[j] = ch < d.nblocks;
+    if (ok[j]) {
+      if constexpr (NW == 2) {
+        const v2u v = __builtin_nontemporal_load(reinterpret_cast<const v2u*>(codes + ch * CPC));
+        cw[j][0] = v.x;
+        cw[j][1] = v.y;
+      } else {
+        cw[j][0] = __builtin_nontemporal_load(reinterpret_cast<const uint32_t*>(codes + ch * CPC));
+      }
+      const int64_t si = ROWS1 ? (ch * CPC) / blk_c : scale_index(d, ch * CPC, blk_r, blk_c);
+      sc[j] = load_scale<SDT>(d.scales, si);
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < NCH; ++j) {
+    if (!ok[j]) continue;
+    const int64_t ch = u * (256 * NCH) + j * 256 + tid;
+    const float s = sc[j];
+    const uint32_t as = f2u(s) & 0x7FFFFFFFu;
+    bool nan_code = false;
+#pragma unroll
+    for (int q = 0; q < NW; ++q) nan_code |= word_has_nan_code(cw[j][q]);
+    float o[CPC];
+    const bool fast = as < 0x7F800000u && as != 0u && !nan_code;
+    if (fast) {
+#pragma unroll
+      for (int q = 0; q < NW; ++q) {
+        const f32x2 lo = e4m3x2_to_f32<false>(cw[j][q]), hi = e4m3x2_to_f32<true>(cw[j][q]);
+        o[4 * q + 0] = lo.x * s;
+        o[4 * q + 1] = lo.y * s;
+        o[4 * q + 2] = hi.x * s;
+        o[4 * q + 3] = hi.y * s;
+      }
+    } else {
+#pragma unroll
+      for (int k = 0; k < CPC; ++k) o[k] = x86_mul(e4m3_decode((cw[j][k >> 2] >> (8 * (k & 3))) & 0xFFu), s);
+    }
+    v4u val;
+    if constexpr (ODT == kBF16) {
+      if (fast) {
+        val = {bf16x2_bits(o[0], o[1]), bf16x2_bits(o[2], o[3]), bf16x2_bits(o[4], o[5]),
+               bf16x2_bits(o[6], o[7])};
+      } else {
+        val = {bf16_bits(o[0]) | (bf16_bits(o[1]) << 16), bf16_bits(o[2]) | (bf16_bits(o[3]) << 16),
+               bf16_bits(o[4]) | (bf16_bits(o[5]) << 16), bf16_bits(o[6]) | (bf16_bits(o[7]) << 16)};
+      }
+      __builtin_nontemporal_store(val, reinterpret_cast<v4u*>(reinterpret_cast<uint16_t*>(d.codes) + ch * CPC));
+    } else {
+      val = {f2u(o[0]), f2u(o[1]), f2u(o[2]), f2u(o[3])};
+      __builtin_nontemporal_store(val, reinterpret_cast<v4u*>(reinterpret_cast<float*>(d.codes) + ch * CPC));
+    }
   }
 }
 
-hipError_t launch_dequant(const uint8_t* codes, const void* scales, int scale_dtype,
-                          int64_t batch, int64_t rows, int64_t cols, int blk_r, int blk_c,
-                          void* out, int out_dtype, hipStream_t stream) {
-  const int64_t n = batch * rows * cols;
-  int64_t g = (n + 255) / 256;
-  if (g > 65536 * 4) g = 65536 * 4;
-  if (g < 1) g = 1;
-  const dim3 grid((unsigned)g), block(256);
-#define LRQ_DQ(S, O) hipLaunchKernelGGL((k_dequant<S, O>), grid, block, 0, stream, codes, scales, batch, rows, cols, blk_r, blk_c, out)
-  if (out_dtype == kF32) {
-    if (scale_dtype == kF32) LRQ_DQ(kF32, kF32);
-    else if (scale_dtype == kBF16) LRQ_DQ(kBF16, kF32);
-    else LRQ_DQ(kF16, kF32);
-  } else {
-    if (scale_dtype == kF32) LRQ_DQ(kF32, kBF16);
-    else if (scale_dtype == kBF16) LRQ_DQ(kBF16, kBF16);
-    else LRQ_DQ(kF16, kBF16);
-  }
-#undef LRQ_DQ
+template <int SDT, int ODT>
+static hipError_t launch_dq(const LaunchCfg& cfg, const Desc& single, const Desc* descs,
+                            const uint32_t* map, int64_t units, hipStream_t stream) {
+  const dim3 grid((unsigned)units), block(256);
+  const bool rows1 = cfg.blk_r == 1 && (map != nullptr ? cfg.rows_dense : (single.cols % cfg.blk_c == 0));
+  if (cfg.kernel == kKernDequant && rows1)
+    hipLaunchKernelGGL((k_dequant<SDT, ODT, true>), grid, block, 0, stream, single, descs, map, cfg.blk_r, cfg.blk_c);
+  else if (cfg.kernel == kKernDequant)
+    hipLaunchKernelGGL((k_dequant<SDT, ODT, false>), grid, block, 0, stream, single, descs, map, cfg.blk_r, cfg.blk_c);
+  else
+    hipLaunchKernelGGL((k_dequant_generic<SDT, ODT>), grid, block, 0, stream, single, descs, map, cfg.blk_r, cfg.blk_c);
   return hipGetLastError();
+}
+
+hipError_t launch_dequant(const LaunchCfg& cfg, const Desc& single, const Desc* descs,
+                          const uint32_t* map, int64_t units, hipStream_t stream) {
+  const bool f32 = cfg.out_dtype == kF32;
+  switch (cfg.in_dtype) {
+    case kF32: return f32 ? launch_dq<kF32, kF32>(cfg, single, descs, map, units, stream)
+                          : launch_dq<kF32, kBF16>(cfg, single, descs, map, units, stream);
+    case kBF16: return f32 ? launch_dq<kBF16, kF32>(cfg, single, descs, map, units, stream)
+                           : launch_dq<kBF16, kBF16>(cfg, single, descs, map, units, stream);
+    case kF16: return f32 ? launch_dq<kF16, kF32>(cfg, single, descs, map, units, stream)
+                          : launch_dq<kF16, kBF16>(cfg, single, descs, map, units, stream);
+  }
+  return hipErrorInvalidValue;
 }
 
 // ---------------------------------------------------------------------------
@@ -79,6 +178,19 @@ __global__ __launch_bounds__(256) void k_diag_e4m3_bits(uint32_t start, int64_t 
   // n is a multiple of 4 (checked by the host): 4 encodes -> one dword
   const uint32_t w = cvt_e4m3x4(u2f(b), u2f(b + 1u), u2f(b + 2u), u2f(b + 3u));
   *reinterpret_cast<uint32_t*>(out + i) = w;
+}
+
+__global__ __launch_bounds__(256) void k_diag_bf16_bits(uint32_t start, int64_t n, uint16_t* out) {
+  const int64_t i = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 2;
+  if (i >= n) return;
+  const uint32_t b = start + (uint32_t)i;
+  *reinterpret_cast<uint32_t*>(out + i) = bf16x2_bits(u2f(b), u2f(b + 1u));
+}
+
+hipError_t launch_diag_bf16_bits(uint32_t start, int64_t n, uint16_t* out, hipStream_t stream) {
+  const int64_t g = (n / 2 + 255) / 256;
+  hipLaunchKernelGGL(k_diag_bf16_bits, dim3((unsigned)g), dim3(256), 0, stream, start, n, out);
+  return hipGetLastError();
 }
 
 hipError_t launch_diag_e4m3_bits(uint32_t start, int64_t n, uint8_t* out, hipStream_t stream) {

@@ -106,6 +106,24 @@ __device__ __forceinline__ uint32_t mx_fp4x2(uint32_t old, float a, float b, uin
   return __builtin_amdgcn_cvt_scalef32_pk_fp4_f32(old, a, b, u2f(e8m0 << 23), SEL);
 }
 
+// e4m3fn byte pair (low or high 16 bits of `w`) -> two floats, via gfx950's
+// v_cvt_pk_f32_fp8.  Exact for every non-NaN code; callers route NaN codes
+// (0x7F/0xFF) through e4m3 rules of their own.
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+template <bool HI>
+__device__ __forceinline__ f32x2 e4m3x2_to_f32(uint32_t w) {
+  return __builtin_amdgcn_cvt_pk_f32_fp8((int)w, HI);
+}
+
+// Two floats -> two bf16 (first in the low half), round to nearest even, via
+// v_cvt_pk_bf16_f32.  Matches bf16_bits() on every non-NaN float32 (checked
+// exhaustively); NaN inputs must take bf16_bits() (torch writes 0xFFFF).
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint32_t bf16x2_bits(float a, float b) {
+  const bf16x2 h = __builtin_convertvector((f32x2){a, b}, bf16x2);
+  return __builtin_bit_cast(uint32_t, h);
+}
+
 // ---------------------------------------------------------------------------
 // FP8 block scale (weight_quantizer.py:60-65)
 // ---------------------------------------------------------------------------

@@ -119,19 +119,6 @@ __device__ __forceinline__ void store_scale(void* scales, int64_t idx, float s, 
   }
 }
 
-__device__ __forceinline__ void pick_desc(const Desc& single, const Desc* descs,
-                                          const uint32_t* map, Desc& d, int64_t& u) {
-  const int64_t wg = xcd_unit(blockIdx.x, gridDim.x);
-  if (map != nullptr) {
-    const uint32_t t = map[wg];
-    d = descs[t];
-    u = wg - d.unit0;
-  } else {
-    d = single;
-    u = wg;
-  }
-}
-
 // ---------------------------------------------------------------------------
 // 128x128 tiles.  Thread t owns column chunk (t & 15) of rows (t >> 4) + 16i,
 // i = 0..7: each load instruction of a wave reads 4 full 256-byte rows.

@@ -4,6 +4,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "lrq_device.hpp"
+
 namespace lrq {
 
 // One tensor of a launch: `batch` matrices of [rows, cols], input row stride
@@ -29,7 +31,25 @@ enum Kernel : int {
   kKernGenericFp8 = 2,
   kKernMx = 3,        // MXFP8 / MXFP4, one quad per 32-group
   kKernGenericMx = 4,
+  kKernDequant = 5,        // FP8 dequant, 16 codes per lane-chunk
+  kKernGenericDequant = 6, // FP8 dequant, one element per thread
 };
+
+// Descriptor and local work unit of this work-group: the single-tensor
+// descriptor (kernel argument) or, for a grouped launch, the one the device
+// map names for the XCD-remapped work-group index.
+__device__ __forceinline__ void pick_desc(const Desc& single, const Desc* descs,
+                                          const uint32_t* map, Desc& d, int64_t& u) {
+  const int64_t wg = xcd_unit(blockIdx.x, gridDim.x);
+  if (map != nullptr) {
+    const uint32_t t = map[wg];
+    d = descs[t];
+    u = wg - d.unit0;
+  } else {
+    d = single;
+    u = wg;
+  }
+}
 
 // Launch parameters common to every tensor of one launch.
 struct LaunchCfg {
@@ -40,6 +60,8 @@ struct LaunchCfg {
   int blk_r, blk_c;
   int mx_fmt;     // 8 or 4
   int scale_bf16; // FP8 kernels: write the float32 scales rounded to bf16
+  int out_dtype;  // dequant: kF32 or kBF16 (in_dtype is then the scale dtype)
+  int rows_dense; // dequant, 1xB: every tensor has cols % blk_c == 0
 };
 
 // Work-groups a tensor needs under `cfg` (filled into d.units and the unit
@@ -51,13 +73,14 @@ bool plan_units(const LaunchCfg& cfg, Desc& d);
 // arrays (map_dev[wg] = descriptor index) and total_units work-groups run.
 hipError_t launch(const LaunchCfg& cfg, const Desc& single, const Desc* descs_dev,
                   const uint32_t* map_dev, int64_t total_units, hipStream_t stream);
+hipError_t launch_fp8(const LaunchCfg&, const Desc&, const Desc*, const uint32_t*, int64_t, hipStream_t);
+hipError_t launch_mx(const LaunchCfg&, const Desc&, const Desc*, const uint32_t*, int64_t, hipStream_t);
+hipError_t launch_dequant(const LaunchCfg&, const Desc&, const Desc*, const uint32_t*, int64_t, hipStream_t);
 
-hipError_t launch_dequant(const uint8_t* codes, const void* scales, int scale_dtype,
-                          int64_t batch, int64_t rows, int64_t cols, int blk_r, int blk_c,
-                          void* out, int out_dtype, hipStream_t stream);
 
 // Diagnostics: element encoders applied to raw inputs.
 hipError_t launch_diag_e4m3_bits(uint32_t start, int64_t n, uint8_t* out, hipStream_t stream);
+hipError_t launch_diag_bf16_bits(uint32_t start, int64_t n, uint16_t* out, hipStream_t stream);
 hipError_t launch_diag_mx(int fmt, const float* in, const uint8_t* e8m0, int64_t n, uint8_t* out,
                           hipStream_t stream);
 

@@ -106,15 +106,7 @@ __global__ __launch_bounds__(256) void k_mx(Desc single, const Desc* __restrict_
   constexpr int kEmax = FMT == 8 ? 8 : 2;
   Desc d;
   int64_t u;
-  const int64_t wg = xcd_unit(blockIdx.x, gridDim.x);
-  if (map != nullptr) {
-    const uint32_t t = map[wg];
-    d = descs[t];
-    u = wg - d.unit0;
-  } else {
-    d = single;
-    u = wg;
-  }
+  pick_desc(single, descs, map, d, u);
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int p = lane & 3;
@@ -165,14 +157,7 @@ __global__ __launch_bounds__(256) void k_mx_generic(Desc single, const Desc* __r
   constexpr int kEmax = FMT == 8 ? 8 : 2;
   Desc d;
   int64_t u;
-  if (map != nullptr) {
-    const uint32_t t = map[blockIdx.x];
-    d = descs[t];
-    u = (int64_t)blockIdx.x - d.unit0;
-  } else {
-    d = single;
-    u = blockIdx.x;
-  }
+  pick_desc(single, descs, map, d, u);
   const int64_t g = u * 256 + threadIdx.x;
   if (g >= d.nblocks) return;
   const int64_t row = g / d.bpr;

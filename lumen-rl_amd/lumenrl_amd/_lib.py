@@ -14,8 +14,8 @@ _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "liblrq.so")
 
 DTYPE_BF16, DTYPE_F16, DTYPE_F32 = 0, 1, 2
-FLAG_POW2_SCALE, FLAG_NATIVE_ARITH, FLAG_SCALE_BF16 = 1, 2, 4
-FMT_FP8_BLOCK, FMT_MXFP8, FMT_MXFP4 = 0, 1, 2
+FLAG_POW2_SCALE, FLAG_NATIVE_ARITH, FLAG_SCALE_BF16, FLAG_OUT_BF16 = 1, 2, 4, 8
+FMT_FP8_BLOCK, FMT_MXFP8, FMT_MXFP4, FMT_FP8_DEQUANT = 0, 1, 2, 3
 ERR_ARG, ERR_ALIGN, ERR_CAPACITY, ERR_TABLE = -1, -2, -3, -4
 
 
@@ -52,6 +52,7 @@ SIGNATURES = {
     "lrq_version": (ctypes.c_char_p, []),
     "lrq_last_error": (ctypes.c_char_p, []),
     "lrq_diag_e4m3_bits": (_CI, [ctypes.c_uint32, _I64, _VP, _VP]),
+    "lrq_diag_bf16_bits": (_CI, [ctypes.c_uint32, _I64, _VP, _VP]),
     "lrq_diag_mx_encode": (_CI, [_CI, _VP, _VP, _VP, _I64, _VP]),
 }
 

@@ -1,5 +1,6 @@
 """Weight quantization for trainer -> rollout weight sync (lumenrl/quantization mirror)."""
 
+from lumenrl_amd.quantization.bucket import QuantizedBucketWriter
 from lumenrl_amd.quantization.fp8_config import (
     FP8Config,
     QuantizationConfig,
@@ -7,6 +8,7 @@ from lumenrl_amd.quantization.fp8_config import (
     TrainingQuantConfig,
 )
 from lumenrl_amd.quantization.ops import (
+    DequantPlan,
     QuantPlan,
     quantize_fp8_blockwise,
     quantize_mxfp4,
@@ -16,9 +18,11 @@ from lumenrl_amd.quantization.ops import fp8_block_dequant, fp8_block_quant
 from lumenrl_amd.quantization.weight_quantizer import WeightQuantizer, fp8_e4m3_max
 
 __all__ = [
+    "DequantPlan",
     "FP8Config",
     "QuantizationConfig",
     "QuantPlan",
+    "QuantizedBucketWriter",
     "RolloutQuantConfig",
     "TrainingQuantConfig",
     "WeightQuantizer",

@@ -1,0 +1,204 @@
+"""Quantize weights straight into a weight-transfer bucket.
+
+Lumen-RL's sync copies bf16 weights into a flat uint8 device bucket, one tensor
+after another, and ships the bucket with per-tensor metadata.  Two transports
+carry it:
+- `BucketedWeightSender` (ZMQ + IPC) uses `{name, shape, dtype, offset, handle}`
+  (lumenrl/engine/inference/bucketed_weight_transfer.py:129-171);
+- the RCCL bucket broadcast uses `{name, shape, dtype, offset, nbytes}` JSON
+  entries (lumenrl/engine/inference/rdma_weight_transfer.py:22-57).
+
+The rollout engine then re-quantizes the bf16 weights to FP8 itself
+(vllm_fp8_utils.py:111-118).
+
+`QuantizedBucketWriter` moves that quantization to the sender.  Each planned bucket is ONE
+kernel launch that reads the bf16 weights and writes e4m3 codes and
+`<name>_scale_inv` scales directly at their offsets in the bucket (no
+intermediate tensors, no copy).  Tensors that are not quantized (norms,
+embeddings, lm_head, anything the predicate rejects) are copied in as-is, as
+the reference sender does.  The bucket then carries about half (FP8) or a
+quarter (MXFP4) of the bf16 bytes, and the receiver gets exactly what a
+vLLM/ATOM FP8 loader takes.
+"""
+
+from __future__ import annotations
+
+from typing import Callable, Iterator, Optional, Sequence
+
+import torch
+from torch import Tensor
+
+from lumenrl_amd.quantization import ops
+
+_ALIGN = 256
+
+
+def default_quantize_if(name: str, t: Tensor) -> bool:
+    """2-D linear weights with a 128-aligned input dim; embeddings and lm_head stay bf16."""
+    lname = name.lower()
+    if "embed" in lname or "lm_head" in lname:
+        return False
+    return t.dim() in (2, 3) and t.shape[-1] % 128 == 0 and t.dtype in (
+        torch.bfloat16, torch.float16, torch.float32)
+
+
+class _Entry:
+    __slots__ = ("name", "shape", "dtype", "offset", "nbytes", "src")
+
+    def __init__(self, name, shape, dtype, offset, nbytes, src=None):
+        self.name, self.shape, self.dtype = name, tuple(shape), dtype
+        self.offset, self.nbytes, self.src = offset, nbytes, src
+
+
+class Bucket:
+    """One planned bucket: a grouped quantize launch plus pass-through copies."""
+
+    def __init__(self, buffer: Tensor, entries: list[_Entry], plan: Optional[ops.QuantPlan],
+                 copies: list[_Entry]) -> None:
+        self.buffer = buffer
+        self.entries = entries
+        self.plan = plan
+        self.copies = copies
+        self.nbytes = max((e.offset + e.nbytes for e in entries), default=0)
+
+    def fill(self) -> "Bucket":
+        """Enqueue the quantize launch and the pass-through copies (current stream)."""
+        if self.plan is not None:
+            self.plan.run()
+        for e in self.copies:
+            self.buffer[e.offset:e.offset + e.nbytes].copy_(
+                e.src.reshape(-1).view(torch.uint8), non_blocking=True)
+        return self
+
+    def bucket_meta(self) -> dict:
+        """BucketedWeightSender metadata (bucketed_weight_transfer.py:155-161)."""
+        return {e.name: {"name": e.name, "shape": torch.Size(e.shape), "dtype": e.dtype,
+                         "offset": e.offset, "handle": None} for e in self.entries}
+
+    def rdma_entries(self) -> list[dict]:
+        """RCCL bucket entries (rdma_weight_transfer.py:36-44)."""
+        return [{"name": e.name, "shape": list(e.shape), "dtype": str(e.dtype).removeprefix("torch."),
+                 "offset": e.offset, "nbytes": e.nbytes} for e in self.entries]
+
+    def views(self) -> list[tuple[str, Tensor]]:
+        """What a receiver rebuilds from the metadata: (name, tensor) views of the buffer."""
+        out = []
+        for e in self.entries:
+            n = 1
+            for d in e.shape:
+                n *= int(d)
+            t = self.buffer[e.offset:e.offset + e.nbytes].view(e.dtype)[:n].view(e.shape)
+            out.append((e.name, t))
+        return out
+
+
+class QuantizedBucketWriter:
+    """Plans buckets over a fixed list of named weights and fills them on demand.
+
+    Plan once (the parameter storage is stable across RL steps), then per sync:
+    ``for bucket in writer: bucket.fill(); send(bucket.buffer, bucket.bucket_meta())``.
+    All buckets share one device buffer of ``bucket_bytes``; the caller must not
+    refill it before the receiver has consumed the previous bucket (the
+    reference's REQ/REP handshake guarantees that).
+    """
+
+    def __init__(self, named_weights: Sequence[tuple[str, Tensor]], bucket_bytes: int,
+                 fmt: str = "fp8_block", block_size: tuple[int, int] = (128, 128),
+                 quantize_if: Callable[[str, Tensor], bool] = default_quantize_if,
+                 scale_suffix: str = "_scale_inv", buffer: Optional[Tensor] = None) -> None:
+        if fmt not in ("fp8_block", "mxfp8", "mxfp4"):
+            raise ValueError(f"fmt must be fp8_block, mxfp8 or mxfp4, got {fmt!r}")
+        if not named_weights:
+            raise ValueError("no weights to plan")
+        dev = named_weights[0][1].device
+        if buffer is None:
+            buffer = torch.empty(int(bucket_bytes), dtype=torch.uint8, device=dev)
+        if buffer.dtype != torch.uint8 or buffer.dim() != 1 or buffer.numel() < bucket_bytes:
+            raise ValueError("buffer must be a flat uint8 tensor of at least bucket_bytes")
+        self.buffer = buffer
+        self.bucket_bytes = int(bucket_bytes)
+        self.scale_suffix = scale_suffix
+        self.fmt = fmt
+        self.block_size = block_size
+        self.buckets: list[Bucket] = []
+
+        cur: list[tuple[str, Tensor, bool]] = []
+        used = 0
+        for name, w in named_weights:
+            q = quantize_if(name, w)
+            need = self._footprint(w, q)
+            if need > self.bucket_bytes:
+                raise ValueError(f"{name} needs {need} bytes, more than the bucket ({self.bucket_bytes})")
+            if used + need > self.bucket_bytes and cur:
+                self.buckets.append(self._plan(cur))
+                cur, used = [], 0
+            cur.append((name, w, q))
+            used += need
+        if cur:
+            self.buckets.append(self._plan(cur))
+
+    # bytes a tensor occupies in a bucket, each entry padded to _ALIGN
+    def _sizes(self, w: Tensor, q: bool) -> list[tuple[tuple, torch.dtype, int]]:
+        if not q:
+            return [(tuple(w.shape), w.dtype, w.numel() * w.element_size())]
+        *lead, rows, cols = w.shape if w.dim() >= 2 else (1,) + tuple(w.shape)
+        lead = tuple(lead)
+        if self.fmt == "fp8_block":
+            br, bc = self.block_size
+            sshape = lead + (-(-rows // br), -(-cols // bc))
+            return [(tuple(w.shape), torch.float8_e4m3fn, w.numel()),
+                    (sshape, torch.float32, 4 * _prod(sshape))]
+        cshape = tuple(w.shape) if self.fmt == "mxfp8" else lead + (rows, cols // 2)
+        ctype = torch.float8_e4m3fn if self.fmt == "mxfp8" else torch.uint8
+        sshape = lead + (rows, cols // 32)
+        return [(cshape, ctype, _prod(cshape)), (sshape, torch.uint8, _prod(sshape))]
+
+    def _footprint(self, w: Tensor, q: bool) -> int:
+        return sum(_align(n) for _, _, n in self._sizes(w, q))
+
+    def _plan(self, items: list[tuple[str, Tensor, bool]]) -> Bucket:
+        entries, copies, qin, qout = [], [], [], []
+        off = 0
+        for name, w, q in items:
+            sizes = self._sizes(w, q)
+            if not w.is_contiguous():
+                raise ValueError(f"{name}: bucket planning needs contiguous weights "
+                                 "(the plan keeps pointers to their storage)")
+            if not q:
+                shape, dt, n = sizes[0]
+                e = _Entry(name, shape, dt, off, n, src=w)
+                entries.append(e)
+                copies.append(e)
+                off += _align(n)
+                continue
+            (cshape, cdt, cn), (sshape, sdt, sn) = sizes
+            ce = _Entry(name, cshape, cdt, off, cn)
+            off += _align(cn)
+            se = _Entry(name + self.scale_suffix, sshape, sdt, off, sn)
+            off += _align(sn)
+            entries += [ce, se]
+            codes = self.buffer[ce.offset:ce.offset + cn].view(cdt).view(cshape)
+            scales = self.buffer[se.offset:se.offset + sn].view(sdt).view(sshape)
+            qin.append(w)
+            qout.append((codes, scales))
+        plan = None
+        if qin:
+            plan = ops.QuantPlan(qin, self.fmt, self.block_size, outputs=qout)
+        return Bucket(self.buffer, entries, plan, copies)
+
+    def __iter__(self) -> Iterator[Bucket]:
+        return iter(self.buckets)
+
+    def __len__(self) -> int:
+        return len(self.buckets)
+
+
+def _align(n: int) -> int:
+    return (n + _ALIGN - 1) // _ALIGN * _ALIGN
+
+
+def _prod(shape) -> int:
+    p = 1
+    for d in shape:
+        p *= int(d)
+    return p

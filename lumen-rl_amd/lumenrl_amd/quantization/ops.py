@@ -206,16 +206,47 @@ def quantize_fp8_blockwise(x: Tensor, block_size: tuple[int, int] = (128, 128), 
 # ---------------------------------------------------------------------------
 # grouped launches
 # ---------------------------------------------------------------------------
-_FMTS = {"fp8_block": _lib.FMT_FP8_BLOCK, "mxfp8": _lib.FMT_MXFP8, "mxfp4": _lib.FMT_MXFP4}
+_FMTS = {"fp8_block": _lib.FMT_FP8_BLOCK, "mxfp8": _lib.FMT_MXFP8, "mxfp4": _lib.FMT_MXFP4,
+         "fp8_dequant": _lib.FMT_FP8_DEQUANT}
+
+
+class _GroupLaunch:
+    """A packed descriptor table (host + device copy) for one grouped launch."""
+
+    def __init__(self, fmt: str, descs, n: int, in_dtype: int, block: tuple[int, int],
+                 flags: int, device: torch.device) -> None:
+        L = _lib.lib()
+        br, bc = int(block[0]), int(block[1])
+        need = L.lrq_group_table_bytes(_FMTS[fmt], descs, n, in_dtype, br, bc, flags)
+        if need < 0:
+            _lib.check(int(need), "lrq_group_table_bytes")
+        self.host = torch.empty(int(need), dtype=torch.uint8)
+        rc = L.lrq_group_pack(_FMTS[fmt], descs, n, in_dtype, br, bc, flags,
+                              self.host.data_ptr(), int(need))
+        _lib.check(rc, "lrq_group_pack")
+        self.dev = self.host.to(device)
+        self.device = device
+        self.units = int(L.lrq_group_units(self.host.data_ptr()))
+
+    def run(self) -> None:
+        with torch.cuda.device(self.device):
+            rc = _lib.lib().lrq_quant_grouped(self.host.data_ptr(), self.dev.data_ptr(),
+                                              _stream(self.device))
+        _lib.check(rc, "lrq_quant_grouped")
+
+
+def _nbytes(t: Tensor) -> int:
+    return t.numel() * t.element_size()
 
 
 class QuantPlan:
     """One kernel launch that quantizes a whole list of weights.
 
-    The plan allocates every output once and uploads a small descriptor table
-    (tensor pointers and shapes plus a work-group -> tensor map).  ``run()``
-    re-quantizes whatever the input tensors currently hold -- the RL weight-sync
-    pattern, where the same parameter storage is refreshed every step.
+    The plan allocates every output once (or takes caller-provided output
+    views, e.g. slices of a transfer bucket) and uploads a small descriptor
+    table (tensor pointers and shapes plus a work-group -> tensor map).
+    ``run()`` re-quantizes whatever the input tensors currently hold -- the RL
+    weight-sync pattern, where the same parameter storage is refreshed every step.
 
     Inputs must be device tensors with 16-byte aligned rows (every torch
     allocation of a [N, K] weight with K % 8 == 0 qualifies).
@@ -223,9 +254,10 @@ class QuantPlan:
 
     def __init__(self, tensors: Sequence[Tensor], fmt: str = "fp8_block",
                  block_size: tuple[int, int] = (128, 128), *, use_pow2_scale: bool = False,
-                 native_arith: bool = False, scale_dtype: torch.dtype = torch.float32) -> None:
-        if fmt not in _FMTS:
-            raise ValueError(f"fmt must be one of {sorted(_FMTS)}, got {fmt!r}")
+                 native_arith: bool = False, scale_dtype: torch.dtype = torch.float32,
+                 outputs: Optional[Sequence[tuple[Tensor, Tensor]]] = None) -> None:
+        if fmt not in ("fp8_block", "mxfp8", "mxfp4"):
+            raise ValueError(f"fmt must be fp8_block, mxfp8 or mxfp4, got {fmt!r}")
         if not tensors:
             raise ValueError("QuantPlan needs at least one tensor")
         dt = tensors[0].dtype
@@ -234,6 +266,8 @@ class QuantPlan:
             _check_input(t, "QuantPlan")
             if t.dtype != dt or t.device != dev:
                 raise ValueError("all tensors of a QuantPlan must share dtype and device")
+        if outputs is not None and len(outputs) != len(tensors):
+            raise ValueError("outputs must pair up with tensors")
         self.fmt = fmt
         self.device = dev
         self.inputs = list(tensors)
@@ -258,43 +292,101 @@ class QuantPlan:
             self._views.append(xm)
             shape = tuple(t.shape) if t.dim() >= 2 else (1,) + tuple(t.shape)
             if fmt == "fp8_block":
-                codes = torch.empty(shape, dtype=torch.float8_e4m3fn, device=dev)
+                cshape, cdt = shape, torch.float8_e4m3fn
                 sdt = dt if native else (torch.bfloat16 if flags & _lib.FLAG_SCALE_BF16 else torch.float32)
-                scales = torch.empty(shape[:-2] + (-(-rows // br), -(-cols // bc)), dtype=sdt, device=dev)
+                sshape = shape[:-2] + (-(-rows // br), -(-cols // bc))
             else:
                 if cols % 32:
                     raise ValueError(f"tensor {i}: last dim {cols} is not a multiple of 32")
                 lead = shape[:-1]
-                if fmt == "mxfp8":
-                    codes = torch.empty(shape, dtype=torch.float8_e4m3fn, device=dev)
-                else:
-                    codes = torch.empty(lead + (cols // 2,), dtype=torch.uint8, device=dev)
-                scales = torch.empty(lead + (cols // 32,), dtype=torch.uint8, device=dev)
+                cshape = shape if fmt == "mxfp8" else lead + (cols // 2,)
+                cdt = torch.float8_e4m3fn if fmt == "mxfp8" else torch.uint8
+                sshape, sdt = lead + (cols // 32,), torch.uint8
+            if outputs is None:
+                codes = torch.empty(cshape, dtype=cdt, device=dev)
+                scales = torch.empty(sshape, dtype=sdt, device=dev)
+            else:
+                codes, scales = outputs[i]
+                if (codes.numel() * codes.element_size() != _prod(cshape)
+                        or scales.numel() * scales.element_size() != _prod(sshape) * _esize(sdt)
+                        or not codes.is_contiguous() or not scales.is_contiguous()
+                        or codes.device != dev or scales.device != dev):
+                    raise ValueError(f"output {i} must be contiguous device views of "
+                                     f"{cshape} codes and {sshape} {sdt} scales")
             self.outputs.append((codes, scales))
             descs[i].in_ = xm.data_ptr()
             descs[i].codes = codes.data_ptr()
             descs[i].scales = scales.data_ptr()
             descs[i].batch, descs[i].rows, descs[i].cols = batch, rows, cols
             descs[i].ld, descs[i].batch_stride = ld, bstride
-            nbytes += t.numel() * t.element_size() + codes.numel() * codes.element_size() + \
-                scales.numel() * scales.element_size()
+            nbytes += _nbytes(t) + _nbytes(codes) + _nbytes(scales)
         self.algorithmic_bytes = nbytes
-        L = _lib.lib()
-        in_dt = _IN_DTYPES[dt]
-        need = L.lrq_group_table_bytes(_FMTS[fmt], descs, len(tensors), in_dt, br, bc, flags)
-        if need < 0:
-            _lib.check(int(need), "lrq_group_table_bytes")
-        self._host_table = torch.empty(int(need), dtype=torch.uint8, pin_memory=False)
-        rc = L.lrq_group_pack(_FMTS[fmt], descs, len(tensors), in_dt, br, bc, flags,
-                              self._host_table.data_ptr(), int(need))
-        _lib.check(rc, "lrq_group_pack")
-        self._dev_table = self._host_table.to(dev)
-        self.units = int(L.lrq_group_units(self._host_table.data_ptr()))
+        self._launch = _GroupLaunch(fmt, descs, len(tensors), _IN_DTYPES[dt], (br, bc), flags, dev)
+        self.units = self._launch.units
 
     def run(self) -> list[tuple[Tensor, Tensor]]:
         """Enqueue the launch on the current stream; returns the (codes, scales) list."""
-        with torch.cuda.device(self.device):
-            rc = _lib.lib().lrq_quant_grouped(self._host_table.data_ptr(),
-                                              self._dev_table.data_ptr(), _stream(self.device))
-        _lib.check(rc, "lrq_quant_grouped")
+        self._launch.run()
         return self.outputs
+
+
+class DequantPlan:
+    """One kernel launch that dequantizes a list of (codes, scales) pairs.
+
+    fp32(code) * fp32(scale) per ``block_size`` block, written as ``out_dtype``
+    (float32: dequantize_tensor; bfloat16: dequantize_state_dict's cast).
+    """
+
+    def __init__(self, pairs: Sequence[tuple[Tensor, Tensor]], block_size: tuple[int, int],
+                 out_dtype: torch.dtype = torch.float32) -> None:
+        if not pairs:
+            raise ValueError("DequantPlan needs at least one (codes, scales) pair")
+        if out_dtype not in (torch.float32, torch.bfloat16):
+            raise ValueError(f"out_dtype must be float32 or bfloat16, got {out_dtype}")
+        sdt = pairs[0][1].dtype
+        dev = pairs[0][0].device
+        br, bc = int(block_size[0]), int(block_size[1])
+        descs = (_lib.LrqTensor * len(pairs))()
+        self.inputs = []
+        self.outputs: list[Tensor] = []
+        nbytes = 0
+        for i, (c, sc) in enumerate(pairs):
+            if c.dtype not in (torch.float8_e4m3fn, torch.uint8) or not c.is_cuda or not c.is_contiguous():
+                raise ValueError(f"pair {i}: codes must be contiguous float8_e4m3fn device tensors")
+            if sc.dtype != sdt or sc.device != dev or not sc.is_contiguous():
+                raise ValueError(f"pair {i}: scales must be contiguous {sdt} on {dev}")
+            shape = tuple(c.shape) if c.dim() >= 2 else (1,) + tuple(c.shape)
+            *lead, rows, cols = shape
+            batch = _prod(lead)
+            need = batch * (-(-rows // br)) * (-(-cols // bc))
+            if sc.numel() != need:
+                raise ValueError(f"pair {i}: scales have {sc.numel()} elements, blocks need {need}")
+            out = torch.empty(c.shape, dtype=out_dtype, device=dev)
+            self.inputs.append((c, sc))
+            self.outputs.append(out)
+            descs[i].in_ = c.data_ptr()
+            descs[i].codes = out.data_ptr()
+            descs[i].scales = sc.data_ptr()
+            descs[i].batch, descs[i].rows, descs[i].cols = batch, rows, cols
+            descs[i].ld, descs[i].batch_stride = cols, rows * cols
+            nbytes += _nbytes(c) + _nbytes(sc) + _nbytes(out)
+        self.algorithmic_bytes = nbytes
+        flags = _lib.FLAG_OUT_BF16 if out_dtype == torch.bfloat16 else 0
+        self._launch = _GroupLaunch("fp8_dequant", descs, len(pairs), _IN_DTYPES[sdt], (br, bc),
+                                    flags, dev)
+        self.units = self._launch.units
+
+    def run(self) -> list[Tensor]:
+        self._launch.run()
+        return self.outputs
+
+
+def _prod(shape) -> int:
+    p = 1
+    for d in shape:
+        p *= int(d)
+    return p
+
+
+def _esize(dtype: torch.dtype) -> int:
+    return torch.empty((), dtype=dtype).element_size()

@@ -169,19 +169,48 @@ class WeightQuantizer:
         return out
 
     def dequantize_state_dict(self, state_dict: dict[str, Tensor]) -> dict[str, Tensor | Any]:
-        """Strip FP8 tensors back to BF16 weights using stored scales (:117-134)."""
+        """Strip FP8 tensors back to BF16 weights using stored scales (:117-134).
+
+        Every (codes, scales) pair goes through ONE grouped kernel launch that
+        writes bf16 directly (fp32 product, then the bf16 cast of :133).
+        """
         consumed_suffixes = {"_fp8_scales", "_fp8_meta"}
+        todo: dict[str, tuple[Tensor, Tensor, torch.device | None]] = {}
+        for key, value in state_dict.items():
+            if any(key.endswith(sfx) for sfx in consumed_suffixes) or not isinstance(value, Tensor):
+                continue
+            scale_key = f"{key}_fp8_scales"
+            if scale_key not in state_dict:
+                continue
+            q, home = _stage(value)
+            s = state_dict[scale_key].to(q.device)
+            if s.dtype == torch.float64:
+                s = s.to(torch.float32)
+            last = value.shape[-1]
+            leading = 1
+            for d in value.shape[:-1]:
+                leading *= int(d)
+            todo[key] = (q.contiguous().reshape(leading, last),
+                         s.contiguous().reshape(leading, last // 128), home)
+        results: dict[str, Tensor] = {}
+        groups: dict[tuple[torch.dtype, torch.device], list[str]] = {}
+        for key, (q, s, _) in todo.items():
+            if q.numel() > 0 and q.data_ptr() % 16 == 0:
+                groups.setdefault((s.dtype, q.device), []).append(key)
+            else:
+                results[key] = ops.fp8_block_dequant(q, s, (1, 128), torch.bfloat16)
+        for keys in groups.values():
+            plan = ops.DequantPlan([todo[k][:2] for k in keys], (1, 128), torch.bfloat16)
+            results.update(zip(keys, plan.run()))
+
         out: dict[str, Tensor | Any] = {}
         for key, value in state_dict.items():
             if any(key.endswith(sfx) for sfx in consumed_suffixes):
                 continue
-            if not isinstance(value, Tensor):
+            if key not in todo:
                 out[key] = value
                 continue
-            scale_key = f"{key}_fp8_scales"
-            if scale_key not in state_dict:
-                out[key] = value
-                continue
-            scales = state_dict[scale_key]
-            out[key] = self._dequant(value, scales.to(value.device), 128, torch.bfloat16)
+            dq = results[key].reshape(value.shape)
+            home = todo[key][2]
+            out[key] = dq.to(home) if home is not None else dq
         return out

@@ -124,6 +124,30 @@ def test_hw_e4m3_encoder_all_float32_patterns():
     assert nan_codes <= {0x7F, 0xFF}
 
 
+@pytest.mark.slow
+def test_hw_bf16_encoder_all_float32_patterns():
+    """v_cvt_pk_bf16_f32 (dequant's bf16 output) vs the oracle's RNE on every
+    non-NaN float32 pattern; NaN results never reach it (the kernel routes NaN
+    codes and NaN/inf/zero scales through the explicit rules)."""
+    chunk = 1 << 28
+    out = torch.empty(chunk, dtype=torch.int16, device=DEV)
+    bad = 0
+    for k in range((1 << 32) // chunk):
+        start = k * chunk
+        _lib.check(_lib.lib().lrq_diag_bf16_bits(start, chunk, out.data_ptr(), None), "diag")
+        torch.cuda.synchronize()
+        got = out.cpu().numpy().view(np.uint16)
+        bits = np.arange(start, start + chunk, dtype=np.uint64).astype(np.uint32)
+        want = O.bf16_from_f32(bits.view(np.float32))
+        isnan = (bits & 0x7FFFFFFF) > 0x7F800000
+        nb = int(((got != want) & ~isnan).sum())
+        if nb:
+            w = np.argwhere((got != want) & ~isnan)[:4].ravel()
+            say("bf16 mismatch", [(hex(start + int(i)), hex(got[i]), hex(want[i])) for i in w])
+        bad += nb
+    assert bad == 0
+
+
 @pytest.mark.parametrize("fmt", [8, 4])
 def test_mx_element_path_every_bf16_and_scale(fmt):
     """The MX kernels' element encoder on every finite bf16 x under every E8M0
@@ -425,3 +449,94 @@ def test_exhaustive_pairs_tile_kernel():
     oc, osc = O.fp8_block_quant(xb, "bf16", "f32", (128, 128))
     assert np.array_equal(u8(c).reshape(oc.shape), oc)
     assert np.array_equal(scale_bits(s).reshape(-1), osc.view(np.uint32).reshape(-1))
+
+
+# ----------------------------------------------------------------------------
+# dequant (weight_quantizer.py:79-89, :133) and quantize-into-bucket
+# ----------------------------------------------------------------------------
+def _codes_and_scales(shape, blk, sdt):
+    rows, cols = shape[-2], shape[-1]
+    lead = shape[:-2]
+    codes = RNG.integers(0, 256, shape, dtype=np.uint8)
+    sshape = lead + (-(-rows // blk[0]), -(-cols // blk[1]))
+    sc = (RNG.normal(0, 1e-3, sshape)).astype(np.float32)
+    flat = sc.reshape(-1)
+    flat[:4] = [0.0, np.inf, np.nan, -np.inf]
+    if sdt == "f32":
+        return codes, flat.reshape(sshape), flat.reshape(sshape)
+    t = torch.from_numpy(flat).to(DT[sdt])
+    bits16 = t.view(torch.int16).numpy().view(np.uint16).reshape(sshape)
+    return codes, bits16, t.reshape(sshape)
+
+
+@pytest.mark.parametrize("blk", [(1, 128), (128, 128), (1, 64), (1, 40), (64, 48)])
+@pytest.mark.parametrize("sdt", ["f32", "bf16", "f16"])
+@pytest.mark.parametrize("odt", ["f32", "bf16"])
+def test_dequant_paths_match_oracle(blk, sdt, odt):
+    shape = (3, 200, 480) if blk[1] % 16 == 0 else (200, 480)
+    codes, sbits, st = _codes_and_scales(shape, blk, sdt)
+    cd = torch.from_numpy(codes).to(DEV).view(torch.float8_e4m3fn)
+    sd = st.to(DEV) if isinstance(st, torch.Tensor) else torch.from_numpy(st).to(DEV)
+    out = ops.fp8_block_dequant(cd, sd, blk, torch.float32 if odt == "f32" else torch.bfloat16)
+    torch.cuda.synchronize()
+    c3 = codes.reshape((-1,) + shape[-2:])
+    want = O.fp8_block_dequant(c3, sbits, sdt, blk, odt)
+    got = out.cpu().contiguous()
+    got = got.numpy().view(np.uint32) if odt == "f32" else got.view(torch.int16).numpy().view(np.uint16)
+    w = want.view(np.uint32) if odt == "f32" else want
+    assert np.array_equal(got.reshape(w.shape), w)
+
+
+def test_grouped_dequant_plan_matches_oracle():
+    pairs, host = [], []
+    for rows, cols in QWEN3_8B_LAYER[:4]:
+        codes, sbits, st = _codes_and_scales((rows, cols), (1, 128), "bf16")
+        pairs.append((torch.from_numpy(codes).to(DEV).view(torch.float8_e4m3fn), st.to(DEV)))
+        host.append((codes, sbits))
+    plan = ops.DequantPlan(pairs, (1, 128), torch.bfloat16)
+    outs = plan.run()
+    torch.cuda.synchronize()
+    for (codes, sbits), o in zip(host, outs):
+        want = O.fp8_block_dequant(codes, sbits, "bf16", (1, 128), "bf16")[0]
+        assert np.array_equal(o.cpu().view(torch.int16).numpy().view(np.uint16), want)
+
+
+@pytest.mark.parametrize("fmt", ["fp8_block", "mxfp4"])
+def test_bucket_writer_matches_oracle(fmt):
+    from lumenrl_amd.quantization import QuantizedBucketWriter
+
+    named = [("model.embed_tokens.weight", weights((512, 256)).to(DEV)),
+             ("layers.0.self_attn.q_proj.weight", weights((512, 512)).to(DEV)),
+             ("layers.0.input_layernorm.weight", torch.ones(512, dtype=torch.bfloat16, device=DEV)),
+             ("layers.0.mlp.down_proj.weight", weights((256, 1024)).to(DEV)),
+             ("layers.0.mlp.experts.w13", weights((4, 256, 384)).to(DEV)),
+             ("lm_head.weight", weights((512, 256)).to(DEV))]
+    writer = QuantizedBucketWriter(named, bucket_bytes=700_000, fmt=fmt)
+    assert len(writer) >= 2
+    src = dict(named)
+    seen = set()
+    for bucket in writer:
+        bucket.fill()
+        torch.cuda.synchronize()
+        meta = bucket.bucket_meta()
+        assert [e["name"] for e in bucket.rdma_entries()] == list(meta)
+        views = dict(bucket.views())
+        for name, t in views.items():
+            seen.add(name)
+            base = name[: -len("_scale_inv")] if name.endswith("_scale_inv") else name
+            w = src[base]
+            if base == name and t.dtype == w.dtype:       # pass-through
+                assert torch.equal(t, w)
+                continue
+            xh = host_bits(w)
+            if fmt == "fp8_block":
+                oc, osc = O.fp8_block_quant(xh.reshape((-1,) + xh.shape[-2:]), "bf16", "f32", (128, 128))
+                want = oc if name == base else osc
+                got = u8(t) if name == base else scale_bits(t)
+                assert np.array_equal(got.reshape(-1), (want if name == base else want.view(np.uint32)).reshape(-1))
+            else:
+                oc, osc = O.mx_quant(xh.reshape(-1, xh.shape[-1]), "bf16", 4)
+                want = oc if name == base else osc
+                assert np.array_equal(u8(t).reshape(-1), want.reshape(-1))
+    assert seen == {n for n, _ in named} | {n + "_scale_inv" for n, _ in named
+                                             if "embed" not in n and "lm_head" not in n and "norm" not in n}
