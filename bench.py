@@ -16,6 +16,10 @@ already resident in HBM:
   c2r: c2 weights with the reference's own 1x128 blocks (scales [N, K/128]).
   c2d: dequantize_state_dict of the c2r result: e4m3 codes + bf16 1x128 scales ->
        bf16 weights, ONE grouped launch.
+  act: the W8A8 rollout linear's activation fake-quant (fp8_rollout.py:53-72)
+       on the seven linear inputs of one Qwen3-8B layer for an 8192-token
+       prefill chunk (bf16 in, float32 out), one launch per linear, every input
+       its own buffer.
 
 Prints ONE JSON line on stdout.  value = algorithmic bytes (bf16 in + codes +
 scales) per step / step time, in GB/s (1e9 B/s).  The roofline object uses the
@@ -46,7 +50,11 @@ QWEN3_8B = [("q_proj", 4096, 4096), ("k_proj", 1024, 4096), ("v_proj", 1024, 409
 
 PROFILE_FOR = {"c2": "k_tile128_qwen3_8b_fp8_128x128", "c2r": "k_row_qwen3_8b_fp8_1x128",
                "c3": "k_tile128_qwen3_30b_a3b_experts", "c4": "k_mx_qwen3_8b_mxfp8",
-               "c5": "k_mx_qwen3_8b_mxfp4"}
+               "c5": "k_mx_qwen3_8b_mxfp4", "c2d": "k_dequant_qwen3_8b_fp8_1x128_to_bf16",
+               "act": "k_act_qdq_qwen3_8b_prefill_8192"}
+KERNEL_FOR = {"c1": "k_tile128", "c2": "k_tile128", "c3": "k_tile128", "c4": "k_mx", "c5": "k_mx",
+              "c2r": "k_row", "c2d": "k_dequant", "act": "k_act_qdq8"}
+PREFILL_TOKENS = 8192
 
 
 def log(*a):
@@ -124,8 +132,23 @@ def cpu_baseline(torch, ws, fmt, fmt_block, seconds):
     n = 0
     t_total = 0.0
     for w in ws:
+        if fmt == "fp8_dequant":
+            c, sc = w[0].cpu(), w[1].cpu()
+            t0 = time.perf_counter()
+            out = torch_ref.dequantize_tensor(c, sc, fmt_block[1]).to(torch.bfloat16)
+            t_total += time.perf_counter() - t0
+            done_bytes += c.numel() + sc.numel() * 2 + out.numel() * 2
+            n += 1
+            if t_total >= seconds:
+                break
+            continue
         x = w.cpu()
-        if fmt == "fp8_block":
+        if fmt == "act":
+            t0 = time.perf_counter()
+            out = torch_ref.act_qdq(x, fmt_block[1])
+            t_total += time.perf_counter() - t0
+            done_bytes += x.numel() * 2 + out.numel() * 4
+        elif fmt == "fp8_block":
             t0 = time.perf_counter()
             if fmt_block == (128, 128):
                 q, s = torch_ref.quantize_tensor_tiles(x.float(), (128, 128))
@@ -142,9 +165,12 @@ def cpu_baseline(torch, ws, fmt, fmt_block, seconds):
         n += 1
         if t_total >= seconds:
             break
-    what = (f"oracle/torch_ref.py (weight_quantizer.py op order on {fmt_block[0]}x{fmt_block[1]} "
-            f"blocks, fp32 upcast first)" if fmt == "fp8_block" else
-            f"the C oracle's {fmt} restatement (the reference has no MX CPU path)")
+    what = {
+        "fp8_block": (f"oracle/torch_ref.py (weight_quantizer.py op order on "
+                      f"{fmt_block[0]}x{fmt_block[1]} blocks, fp32 upcast first)"),
+        "fp8_dequant": "oracle/torch_ref.py (weight_quantizer.py:79-89 then the bf16 cast of :133)",
+        "act": "oracle/torch_ref.py (fp8_rollout.py:53-72 op order)",
+    }.get(fmt, f"the C oracle's {fmt} restatement (the reference has no MX CPU path)")
     return {
         "value": round(done_bytes / t_total / 1e9, 3),
         "unit": "GB/s",
@@ -154,6 +180,18 @@ def cpu_baseline(torch, ws, fmt, fmt_block, seconds):
                    f"algorithmic) through {what}, {threads} threads on {os.cpu_count()} "
                    f"visible cores"),
     }
+
+
+class _ActCall:
+    """One activation fake-quant launch into a preallocated float32 output."""
+
+    def __init__(self, torch, ops, x):
+        self.ops, self.x = ops, x
+        self.out = torch.empty(x.shape, dtype=torch.float32, device=x.device)
+        self.algorithmic_bytes = x.numel() * (x.element_size() + 4)
+
+    def run(self):
+        self.ops.act_qdq(self.x, 128, out=self.out)
 
 
 # ---------------------------------------------------------------------------
@@ -179,7 +217,7 @@ def run(args):
         torch.cuda.synchronize()
         plans = [ops.DequantPlan(pairs, (1, 128), torch.bfloat16)]
         workload = "qwen3-8b-linears-fp8-1x128-dequant-to-bf16"
-        cpu_ws, cpu_blk, cpu_fmt = [], (1, 128), "fp8_dequant"
+        cpu_ws, cpu_blk, cpu_fmt = pairs, (1, 128), "fp8_dequant"
         extra = {"tensors": len(pairs), "layers": 36, "elements": sum(c.numel() for c, _ in pairs),
                  "format": "fp8_dequant", "launches_per_step": 1}
     elif cfg in ("c2", "c4", "c5", "c2r"):
@@ -193,6 +231,22 @@ def run(args):
         cpu_ws, cpu_blk, cpu_fmt = ws, blk, fmt
         extra = {"tensors": len(ws), "layers": 36, "elements": sum(w.numel() for w in ws),
                  "format": fmt, "launches_per_step": 1}
+    elif cfg == "act":
+        g = torch.Generator(device=dev).manual_seed(args.seed)
+        ins = [("q_proj", 4096), ("k_proj", 4096), ("v_proj", 4096), ("o_proj", 4096),
+               ("gate_proj", 4096), ("up_proj", 4096), ("down_proj", 12288)]
+        ws = []
+        for _, k in ins:
+            x = torch.empty(PREFILL_TOKENS, k, device=dev, dtype=torch.float32)
+            x.normal_(0.0, 1.0, generator=g)
+            x[:, :: 97] *= 30.0  # outlier channels
+            ws.append(x.to(torch.bfloat16))
+            del x
+        plans = [_ActCall(torch, ops, x) for x in ws]
+        workload = f"qwen3-8b-layer-act-fake-quant-1x128-prefill-{PREFILL_TOKENS}"
+        cpu_ws, cpu_blk, cpu_fmt = ws, (1, 128), "act"
+        extra = {"tensors": len(ws), "tokens": PREFILL_TOKENS, "elements": sum(x.numel() for x in ws),
+                 "format": "act_qdq_1x128_bf16_to_f32", "launches_per_step": len(ws)}
     elif cfg == "c1":
         g = torch.Generator(device=dev).manual_seed(args.seed)
         ws = [gen_weight(torch, 4096, 4096, g, dev)]
@@ -288,7 +342,7 @@ def run(args):
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
             "traffic": traffic,
-            "kernel": {"c2r": "k_rowquad"}.get(cfg, "k_tile128" if cfg in ("c1", "c2", "c3") else "k_mx"),
+            "kernel": KERNEL_FOR[cfg],
             "launch_ms": round(kern_ms, 5),
         },
     }
@@ -325,7 +379,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--config", default="c2", choices=["c1", "c2", "c3", "c4", "c5", "c2r", "c2d"])
+    ap.add_argument("--config", default="c2", choices=["c1", "c2", "c3", "c4", "c5", "c2r", "c2d", "act"])
     ap.add_argument("--seed", type=int, default=1000)
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")

@@ -104,6 +104,18 @@ int lrq_mxfp4_quant(const void* in, int in_dtype, int64_t rows, int64_t cols, in
                     uint8_t* codes, uint8_t* scales, lrq_stream_t stream);
 
 /*
+ * Activation fake-quant of the FP8 W8A8 rollout linear: per 1 x blk block of
+ * each row (a token's hidden vector), s = clamp(amax/448, FLT_MIN), optional
+ * pow2 (LRQ_FLAG_POW2_SCALE = FP8Config.use_activation_pow2_scale), and
+ * out = float32(x / s) * s.  Replaces the activation ops of
+ * _FP8W8A8Linear.forward (lumenrl/quantization/fp8_rollout.py:53-72).
+ *   in  : [rows, cols] in_dtype, row stride ld (4-element aligned);
+ *   out : [rows, cols] float32, dense, 16-byte aligned;  blk in {32,64,128,256}.
+ */
+int lrq_act_qdq(const void* in, int in_dtype, int64_t rows, int64_t cols, int64_t ld, int64_t blk,
+                unsigned flags, float* out, lrq_stream_t stream);
+
+/*
  * Grouped launch: many tensors (a layer, a whole weight set, or MoE expert
  * stacks) quantized by ONE kernel launch.  Replaces the per-tensor Python loop
  * of WeightQuantizer.quantize_state_dict (weight_quantizer.py:91-115) and the

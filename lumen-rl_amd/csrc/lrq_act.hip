@@ -1,0 +1,212 @@
+// Activation fake-quant of the FP8 W8A8 rollout linear
+// (lumenrl/quantization/fp8_rollout.py:53-72): per 1xB block of each token row,
+// s = clamp(amax/448, FLT_MIN) [pow2], x_dq = float32(x/s) * s.  The reference
+// emulates FP8 activations without rounding them to e4m3, so x_dq is what the
+// GEMM consumes; results match torch on x86 bit for bit (IEEE division per
+// element, x86 NaN/inf rules on blocks whose scale is not finite).
+//
+#include "lrq.h"
+#include "lrq_device.hpp"
+#include "lrq_internal.hpp"
+
+namespace lrq {
+
+// torch's vectorized x86 product x * s: a NaN scale wins (quieted), then a
+// NaN x; 0 * inf is the default NaN.
+__device__ __forceinline__ float x86_mul_scale_first(float q, float s) {
+  const uint32_t aq = f2u(q) & 0x7FFFFFFFu, as = f2u(s) & 0x7FFFFFFFu;
+  if (as > 0x7F800000u) return u2f(f2u(s) | 0x00400000u);
+  if (aq > 0x7F800000u) return u2f(f2u(q) | 0x00400000u);
+  if ((aq == 0u && as == 0x7F800000u) || (as == 0u && aq == 0x7F800000u)) return u2f(0xFFC00000u);
+  return q * s;
+}
+__device__ __forceinline__ float x86_div(float x, float s) {
+  const uint32_t ax = f2u(x) & 0x7FFFFFFFu, as = f2u(s) & 0x7FFFFFFFu;
+  if (ax > 0x7F800000u) return u2f(f2u(x) | 0x00400000u);
+  if (as > 0x7F800000u) return u2f(f2u(s) | 0x00400000u);
+  if ((ax == 0x7F800000u && as == 0x7F800000u) || (ax == 0u && as == 0u)) return u2f(0xFFC00000u);
+  return x / s;
+}
+
+template <int DT>
+__device__ __forceinline__ void load4(const void* base, int64_t off, float (&x)[4]) {
+  if constexpr (DT == kF32) {
+    const v4u v = load_nt(static_cast<const float*>(base) + off);
+    x[0] = u2f(v.x); x[1] = u2f(v.y); x[2] = u2f(v.z); x[3] = u2f(v.w);
+  } else {
+    const v2u v = __builtin_nontemporal_load(reinterpret_cast<const v2u*>(static_cast<const uint16_t*>(base) + off));
+    if constexpr (DT == kBF16) {
+      x[0] = bf16_lo(v.x); x[1] = bf16_hi(v.x); x[2] = bf16_lo(v.y); x[3] = bf16_hi(v.y);
+    } else {
+      x[0] = f16_to_f32(v.x & 0xFFFFu); x[1] = f16_to_f32(v.x >> 16);
+      x[2] = f16_to_f32(v.y & 0xFFFFu); x[3] = f16_to_f32(v.y >> 16);
+    }
+  }
+}
+
+// Shared by both kernels: the [rows, cols] matrix is walked as its row-major
+// element sequence e = row * cols + col (the output is dense), a 1xB block is
+// B/EPL consecutive lanes holding EPL consecutive elements each, and
+// cols % B == 0 keeps every block inside one row and one wave span.
+
+__device__ __forceinline__ int64_t act_offset(int64_t e, int64_t cols, int64_t ld, bool dense) {
+  if (dense) return e;
+  const int64_t row = e / cols;
+  return row * ld + (e - row * cols);
+}
+
+// x_dq for one lane's elements, given the block's |x| maximum bit pattern.
+template <int N>
+__device__ __forceinline__ void act_block(const float (&x)[N], uint32_t amax, int pow2, uint32_t (&o)[N]) {
+  const BlockScale bs = block_scale<kF32>(amax, pow2 != 0);
+  if (bs.kind <= kScaleExact) {
+#pragma unroll
+    for (int i = 0; i < N; ++i) o[i] = f2u((x[i] / bs.s) * bs.s);
+  } else {
+#pragma unroll
+    for (int i = 0; i < N; ++i) o[i] = f2u(x86_mul_scale_first(x86_div(x[i], bs.s), bs.s));
+  }
+}
+
+template <int N>
+__device__ __forceinline__ uint32_t abs_max(const float (&x)[N]) {
+  uint32_t a = 0u;
+#pragma unroll
+  for (int i = 0; i < N; ++i) {
+    const uint32_t m = f2u(x[i]) & 0x7FFFFFFFu;
+    a = m > a ? m : a;
+  }
+  return a;
+}
+
+// 16-bit inputs, 8 elements per lane: one 16-byte load per lane (a wave reads
+// 1 KiB), 2048 elements per work-group.  Lane t of a wave holds elements
+// 8t..8t+7 of the wave's 512-element span; the float32 results are exchanged
+// across the wave so that store h of lane t writes elements 256h + 4t .. +3
+// (owned by lane 32h + t/2, half t&1): each store instruction writes 1 KiB
+// of whole cache lines.
+template <int DT, int LPB, bool DENSE>
+__global__ __launch_bounds__(256) void k_act_qdq8(const uint16_t* __restrict__ in, int64_t rows, int64_t cols,
+                                                  int64_t ld, float* __restrict__ out, int pow2) {
+  const int64_t n = rows * cols;
+  const int lane = threadIdx.x & 63;
+  const int64_t span = xcd_unit(blockIdx.x, gridDim.x) * 2048 + (threadIdx.x >> 6) * 512;
+  const int64_t e = span + 8 * lane;
+  v4u v = {0u, 0u, 0u, 0u};
+  if (e < n) v = __builtin_nontemporal_load(reinterpret_cast<const v4u*>(in + act_offset(e, cols, ld, DENSE)));
+  const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+  float x[8];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    if constexpr (DT == kBF16) {
+      x[2 * i] = bf16_lo(w[i]);
+      x[2 * i + 1] = bf16_hi(w[i]);
+    } else {
+      x[2 * i] = f16_to_f32(w[i] & 0xFFFFu);
+      x[2 * i + 1] = f16_to_f32(w[i] >> 16);
+    }
+  }
+  const uint32_t a = group_max<LPB>(abs_max(x));  // a group is all in or all out of range
+  uint32_t o[8];
+  act_block(x, a, pow2, o);
+  const bool odd = lane & 1;
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const int src = 32 * h + (lane >> 1);
+    uint32_t r[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint32_t lo = (uint32_t)__shfl((int)o[i], src, 64);
+      const uint32_t hi = (uint32_t)__shfl((int)o[4 + i], src, 64);
+      r[i] = odd ? hi : lo;
+    }
+    const int64_t eo = span + 256 * h + 4 * lane;
+    if (eo < n) __builtin_nontemporal_store(v4u{r[0], r[1], r[2], r[3]}, reinterpret_cast<v4u*>(out + eo));
+  }
+}
+
+// Any input dtype, 4 elements per lane, NCH 1024-element chunks per
+// work-group: in chunk j lane t holds elements 1024j + 4t .. +3, so each wave
+// load reads one contiguous span and each store writes 1 KiB.  All NCH loads
+// are issued before the first reduction.
+template <int DT, int LPB, int NCH, bool DENSE>
+__global__ __launch_bounds__(256) void k_act_qdq(const void* __restrict__ in, int64_t rows, int64_t cols,
+                                                 int64_t ld, float* __restrict__ out, int pow2) {
+  const int64_t n = rows * cols;
+  const int64_t base = xcd_unit(blockIdx.x, gridDim.x) * (1024 * NCH) + 4 * (int64_t)threadIdx.x;
+  float x[NCH][4];
+#pragma unroll
+  for (int j = 0; j < NCH; ++j) {
+    const int64_t e = base + 1024 * j;
+    x[j][0] = x[j][1] = x[j][2] = x[j][3] = 0.0f;
+    if (e < n) load4<DT>(in, act_offset(e, cols, ld, DENSE), x[j]);
+  }
+#pragma unroll
+  for (int j = 0; j < NCH; ++j) {
+    const int64_t e = base + 1024 * j;
+    const uint32_t a = group_max<LPB>(abs_max(x[j]));
+    if (e >= n) continue;
+    uint32_t o[4];
+    act_block(x[j], a, pow2, o);
+    __builtin_nontemporal_store(v4u{o[0], o[1], o[2], o[3]}, reinterpret_cast<v4u*>(out + e));
+  }
+}
+
+constexpr int kActChunks = 2;
+
+// True when the 8-per-lane kernel applies: 16-bit input whose rows start on
+// 16-byte boundaries.
+static bool act_wide(const void* in, int dtype, int64_t rows, int64_t ld) {
+  return dtype != kF32 && ((uintptr_t)in % 16u) == 0 && (rows == 1 || ld % 8 == 0);
+}
+
+int64_t act_grid(const void* in, int dtype, int64_t rows, int64_t cols, int64_t ld) {
+  const int64_t per_wg = act_wide(in, dtype, rows, ld) ? 2048 : 1024 * kActChunks;
+  return (rows * cols + per_wg - 1) / per_wg;
+}
+
+template <int DT, bool DENSE>
+static hipError_t launch_act_typed(const void* in, int64_t rows, int64_t cols, int64_t ld, int64_t blk,
+                                   float* out, int pow2, hipStream_t stream) {
+  const dim3 grid((unsigned)act_grid(in, DT, rows, cols, ld)), block(256);
+  const uint16_t* in16 = static_cast<const uint16_t*>(in);
+  if constexpr (DT != kF32) {
+    if (act_wide(in, DT, rows, ld)) {
+      switch (blk) {
+        case 32: hipLaunchKernelGGL((k_act_qdq8<DT, 4, DENSE>), grid, block, 0, stream, in16, rows, cols, ld, out, pow2); break;
+        case 64: hipLaunchKernelGGL((k_act_qdq8<DT, 8, DENSE>), grid, block, 0, stream, in16, rows, cols, ld, out, pow2); break;
+        case 128: hipLaunchKernelGGL((k_act_qdq8<DT, 16, DENSE>), grid, block, 0, stream, in16, rows, cols, ld, out, pow2); break;
+        case 256: hipLaunchKernelGGL((k_act_qdq8<DT, 32, DENSE>), grid, block, 0, stream, in16, rows, cols, ld, out, pow2); break;
+        default: return hipErrorInvalidValue;
+      }
+      return hipGetLastError();
+    }
+  }
+  switch (blk) {
+    case 32: hipLaunchKernelGGL((k_act_qdq<DT, 8, kActChunks, DENSE>), grid, block, 0, stream, in, rows, cols, ld, out, pow2); break;
+    case 64: hipLaunchKernelGGL((k_act_qdq<DT, 16, kActChunks, DENSE>), grid, block, 0, stream, in, rows, cols, ld, out, pow2); break;
+    case 128: hipLaunchKernelGGL((k_act_qdq<DT, 32, kActChunks, DENSE>), grid, block, 0, stream, in, rows, cols, ld, out, pow2); break;
+    case 256: hipLaunchKernelGGL((k_act_qdq<DT, 64, kActChunks, DENSE>), grid, block, 0, stream, in, rows, cols, ld, out, pow2); break;
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
+hipError_t launch_act(const void* in, int dtype, int64_t rows, int64_t cols, int64_t ld, int64_t blk,
+                      float* out, int pow2, hipStream_t stream) {
+  const bool dense = rows == 1 || ld == cols;
+  switch (dtype) {
+    case kBF16:
+      return dense ? launch_act_typed<kBF16, true>(in, rows, cols, ld, blk, out, pow2, stream)
+                   : launch_act_typed<kBF16, false>(in, rows, cols, ld, blk, out, pow2, stream);
+    case kF16:
+      return dense ? launch_act_typed<kF16, true>(in, rows, cols, ld, blk, out, pow2, stream)
+                   : launch_act_typed<kF16, false>(in, rows, cols, ld, blk, out, pow2, stream);
+    case kF32:
+      return dense ? launch_act_typed<kF32, true>(in, rows, cols, ld, blk, out, pow2, stream)
+                   : launch_act_typed<kF32, false>(in, rows, cols, ld, blk, out, pow2, stream);
+  }
+  return hipErrorInvalidValue;
+}
+
+}  // namespace lrq

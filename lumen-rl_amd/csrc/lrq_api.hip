@@ -39,7 +39,8 @@ bool pow2_block(int64_t b) { return b == 32 || b == 64 || b == 128 || b == 256 |
 
 constexpr uint32_t kMagic = 0x4C525154u;  // "LRQT"
 constexpr uint32_t kTableVersion = 1u;
-constexpr int64_t kMaxGrid = 0x7FFFFFFF;
+// HIP takes a launch's thread count (grid x 256 threads) as a 32-bit value
+constexpr int64_t kMaxGrid = 0xFFFFFFFFll / 256;
 
 struct GroupHeader {
   uint32_t magic, version;
@@ -315,6 +316,26 @@ int lrq_mxfp8_quant(const void* in, int in_dtype, int64_t rows, int64_t cols, in
 int lrq_mxfp4_quant(const void* in, int in_dtype, int64_t rows, int64_t cols, int64_t ld,
                     uint8_t* codes, uint8_t* scales, lrq_stream_t stream) {
   return mx_quant(4, in, in_dtype, rows, cols, ld, codes, scales, (hipStream_t)stream);
+}
+
+int lrq_act_qdq(const void* in, int in_dtype, int64_t rows, int64_t cols, int64_t ld, int64_t blk,
+                unsigned flags, float* out, lrq_stream_t stream) {
+  g_err.clear();
+  if (!valid_dtype(in_dtype)) return fail(LRQ_ERR_ARG, "bad input dtype %d", in_dtype);
+  if (blk != 32 && blk != 64 && blk != 128 && blk != 256)
+    return fail(LRQ_ERR_ARG, "activation block must be 32, 64, 128 or 256, got %lld", (long long)blk);
+  if (rows < 0 || cols < 0 || cols % blk != 0)
+    return fail(LRQ_ERR_ARG, "cols (%lld) must be a multiple of the block", (long long)cols);
+  if (rows == 0 || cols == 0) return 0;
+  if (ld < cols) return fail(LRQ_ERR_ARG, "ld < cols");
+  if (!in || !out) return fail(LRQ_ERR_ARG, "null pointer");
+  const int64_t es = esize(in_dtype);
+  if (!aligned(in, (uintptr_t)(4 * es)) || (ld * es) % (4 * es) != 0 || !aligned(out, 16))
+    return fail(LRQ_ERR_ALIGN, "activation rows must be aligned to 4 elements, out to 16 bytes");
+  if (lrq::act_grid(in, in_dtype, rows, cols, ld) > kMaxGrid) return fail(LRQ_ERR_ARG, "tensor too large for one launch");
+  return check_hip(lrq::launch_act(in, in_dtype, rows, cols, ld, blk, out,
+                                   (flags & LRQ_FLAG_POW2_SCALE) ? 1 : 0, (hipStream_t)stream),
+                   "kernel launch");
 }
 
 int64_t lrq_group_table_bytes(int fmt, const lrq_tensor* tensors, int64_t n, int in_dtype,

@@ -292,6 +292,22 @@ __device__ __forceinline__ uint32_t quad_max(uint32_t v) {
   return v > o ? v : o;
 }
 
+// Max over aligned groups of LPB lanes (LPB = 2..64): DPP within 16 lanes,
+// shuffles beyond.
+template <int LPB>
+__device__ __forceinline__ uint32_t group_max(uint32_t v) {
+  uint32_t o;
+  if constexpr (LPB >= 2) { o = (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0xB1, 0xF, 0xF, false); v = v > o ? v : o; }
+  if constexpr (LPB >= 4) { o = (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x4E, 0xF, 0xF, false); v = v > o ? v : o; }
+  // row_half_mirror: lane i <- lane 7-i within its 8-lane half (joins the two
+  // quads of an 8-lane group); row_mirror: lane i <- lane 15-i (joins halves)
+  if constexpr (LPB >= 8) { o = (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x141, 0xF, 0xF, false); v = v > o ? v : o; }
+  if constexpr (LPB >= 16) { o = (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x140, 0xF, 0xF, false); v = v > o ? v : o; }
+  if constexpr (LPB >= 32) { o = (uint32_t)__shfl_xor((int)v, 16, 64); v = v > o ? v : o; }
+  if constexpr (LPB >= 64) { o = (uint32_t)__shfl_xor((int)v, 32, 64); v = v > o ? v : o; }
+  return v;
+}
+
 __device__ __forceinline__ uint32_t wave_max(uint32_t v) {
 #pragma unroll
   for (int off = 32; off >= 1; off >>= 1) {

@@ -193,20 +193,6 @@ __global__ __launch_bounds__(256) void k_tile128(Desc single, const Desc* __rest
 // the four scales are exchanged by shuffles, so the IEEE divisions cost one
 // pair per lane instead of four.  Rows are folded over the batch by the host.
 // ---------------------------------------------------------------------------
-template <int LPB>
-__device__ __forceinline__ uint32_t group_max(uint32_t v) {
-  uint32_t o;
-  if constexpr (LPB >= 2) { o = (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0xB1, 0xF, 0xF, false); v = v > o ? v : o; }
-  if constexpr (LPB >= 4) { o = (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x4E, 0xF, 0xF, false); v = v > o ? v : o; }
-  // row_half_mirror: lane i <- lane 7-i within its 8-lane half (joins the two
-  // quads of an 8-lane group); row_mirror: lane i <- lane 15-i (joins halves)
-  if constexpr (LPB >= 8) { o = (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x141, 0xF, 0xF, false); v = v > o ? v : o; }
-  if constexpr (LPB >= 16) { o = (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x140, 0xF, 0xF, false); v = v > o ? v : o; }
-  if constexpr (LPB >= 32) { o = (uint32_t)__shfl_xor((int)v, 16, 64); v = v > o ? v : o; }
-  if constexpr (LPB >= 64) { o = (uint32_t)__shfl_xor((int)v, 32, 64); v = v > o ? v : o; }
-  return v;
-}
-
 template <int DT, int CDT, int LPB>
 __global__ __launch_bounds__(256) void k_row(Desc single, const Desc* __restrict__ descs,
                                              const uint32_t* __restrict__ map, int pow2,

@@ -79,6 +79,9 @@ hipError_t launch_dequant(const LaunchCfg&, const Desc&, const Desc*, const uint
 
 
 // Diagnostics: element encoders applied to raw inputs.
+int64_t act_grid(const void* in, int dtype, int64_t rows, int64_t cols, int64_t ld);
+hipError_t launch_act(const void* in, int dtype, int64_t rows, int64_t cols, int64_t ld, int64_t blk,
+                      float* out, int pow2, hipStream_t stream);
 hipError_t launch_diag_e4m3_bits(uint32_t start, int64_t n, uint8_t* out, hipStream_t stream);
 hipError_t launch_diag_bf16_bits(uint32_t start, int64_t n, uint16_t* out, hipStream_t stream);
 hipError_t launch_diag_mx(int fmt, const float* in, const uint8_t* e8m0, int64_t n, uint8_t* out,

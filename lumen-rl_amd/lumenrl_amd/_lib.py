@@ -45,6 +45,7 @@ SIGNATURES = {
     "lrq_fp8_block_dequant": (_CI, [_VP, _VP, _CI, _I64, _I64, _I64, _I64, _I64, _VP, _CI, _VP]),
     "lrq_mxfp8_quant": (_CI, [_VP, _CI, _I64, _I64, _I64, _VP, _VP, _VP]),
     "lrq_mxfp4_quant": (_CI, [_VP, _CI, _I64, _I64, _I64, _VP, _VP, _VP]),
+    "lrq_act_qdq": (_CI, [_VP, _CI, _I64, _I64, _I64, _I64, _CU, _VP, _VP]),
     "lrq_group_table_bytes": (_I64, [_CI, ctypes.POINTER(LrqTensor), _I64, _CI, _I64, _I64, _CU]),
     "lrq_group_pack": (_CI, [_CI, ctypes.POINTER(LrqTensor), _I64, _CI, _I64, _I64, _CU, _VP, _I64]),
     "lrq_quant_grouped": (_CI, [_VP, _VP, _VP]),

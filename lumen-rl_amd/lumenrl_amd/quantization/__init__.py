@@ -7,6 +7,7 @@ from lumenrl_amd.quantization.fp8_config import (
     RolloutQuantConfig,
     TrainingQuantConfig,
 )
+from lumenrl_amd.quantization.fp8_rollout import FP8RolloutQuantizer
 from lumenrl_amd.quantization.ops import (
     DequantPlan,
     QuantPlan,
@@ -14,18 +15,20 @@ from lumenrl_amd.quantization.ops import (
     quantize_mxfp4,
     quantize_mxfp8,
 )
-from lumenrl_amd.quantization.ops import fp8_block_dequant, fp8_block_quant
+from lumenrl_amd.quantization.ops import act_qdq, fp8_block_dequant, fp8_block_quant
 from lumenrl_amd.quantization.weight_quantizer import WeightQuantizer, fp8_e4m3_max
 
 __all__ = [
     "DequantPlan",
     "FP8Config",
+    "FP8RolloutQuantizer",
     "QuantizationConfig",
     "QuantPlan",
     "QuantizedBucketWriter",
     "RolloutQuantConfig",
     "TrainingQuantConfig",
     "WeightQuantizer",
+    "act_qdq",
     "fp8_block_dequant",
     "fp8_block_quant",
     "fp8_e4m3_max",

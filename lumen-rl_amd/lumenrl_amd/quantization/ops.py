@@ -156,6 +156,36 @@ def fp8_block_dequant(codes: Tensor, scales: Tensor, block: tuple[int, int],
     return out
 
 
+def act_qdq(x: Tensor, block: int = 128, *, pow2: bool = False,
+            out: Optional[Tensor] = None) -> Tensor:
+    """Activation fake-quant of the FP8 W8A8 rollout linear (fp8_rollout.py:53-72).
+
+    ``x`` [..., K] (bf16/fp16/fp32, K % block == 0) -> float32 [prod(...), K]
+    with x_dq = float32(x / s) * s per 1 x block, s = clamp(amax/448, FLT_MIN).
+    ``out``: optional contiguous float32 [prod(...), K] on x's device to write into.
+    """
+    _check_input(x, "act_qdq")
+    last = x.shape[-1]
+    rows = x.numel() // last if last else 0
+    xm = x.reshape(rows, last)
+    if xm.stride(-1) != 1 or (rows > 1 and xm.stride(0) % 4 != 0) or xm.data_ptr() % (4 * x.element_size()):
+        xm = xm.contiguous()
+    if out is None:
+        out = torch.empty((rows, last), dtype=torch.float32, device=x.device)
+    elif (out.dtype != torch.float32 or tuple(out.shape) != (rows, last) or not out.is_contiguous()
+          or out.device != x.device):
+        raise ValueError(f"act_qdq: out must be a contiguous float32 {(rows, last)} tensor on {x.device}")
+    if out.numel() == 0:
+        return out
+    ld = xm.stride(0) if rows > 1 else last
+    with torch.cuda.device(x.device):
+        rc = _lib.lib().lrq_act_qdq(xm.data_ptr(), _IN_DTYPES[x.dtype], rows, last, ld, int(block),
+                                    _lib.FLAG_POW2_SCALE if pow2 else 0, out.data_ptr(),
+                                    _stream(x.device))
+    _lib.check(rc, "lrq_act_qdq")
+    return out
+
+
 def _mx(x: Tensor, fmt: int) -> tuple[Tensor, Tensor]:
     _check_input(x, "mx quantize")
     if x.dim() < 1 or x.shape[-1] % 32 != 0:

@@ -428,6 +428,42 @@ int lrqo_mx_quant(const void* in, int in_dtype, int64_t rows, int64_t cols, int6
   return 0;
 }
 
+/* Activation fake-quant of _FP8W8A8Linear.forward
+ * (lumenrl/quantization/fp8_rollout.py:53-72): x -> float32, per 1xB block
+ * s = clamp(amax/448, tiny) [pow2], x_dq = float32(x/s) * s -- no e4m3 rounding.
+ * In x * s (torch's vectorized x86 product) a NaN scale wins, then a NaN x;
+ * 0 * inf is the default NaN 0xFFC00000. */
+static inline float x86_mul_scale_first(float q, float s) {
+  if (isnan(s)) return quiet(s);
+  if (isnan(q)) return quiet(q);
+  if ((q == 0.0f && isinf(s)) || (isinf(q) && s == 0.0f)) return u2f(0xFFC00000u);
+  return q * s;
+}
+
+int lrqo_act_qdq(const void* in, int in_dtype, int64_t rows, int64_t cols, int64_t blk, int pow2,
+                 float* out, int nthreads) {
+  if (blk < 1 || cols % blk != 0) return 1;
+  int64_t nb = rows * (cols / blk);
+#ifdef _OPENMP
+  if (nthreads > 0) omp_set_num_threads(nthreads);
+#pragma omp parallel for schedule(static)
+#endif
+  for (int64_t b = 0; b < nb; ++b) {
+    int64_t base = b * blk;
+    uint32_t amax_bits = 0;
+    for (int64_t i = 0; i < blk; ++i) {
+      uint32_t a = f2u(load_in(in, in_dtype, base + i)) & 0x7FFFFFFFu;
+      if (a > amax_bits) amax_bits = a;
+    }
+    float s = block_scale(LRQO_F32, amax_bits, pow2);
+    for (int64_t i = 0; i < blk; ++i) {
+      float x = load_in(in, in_dtype, base + i);
+      out[base + i] = x86_mul_scale_first(lrqo_x86_div(x, s), s);
+    }
+  }
+  return 0;
+}
+
 /* Bulk element converters, for exhaustive checks against torch. */
 void lrqo_f32_to_e4m3_n(const float* in, uint8_t* out, int64_t n) {
 #ifdef _OPENMP

@@ -50,6 +50,7 @@ def lib() -> ctypes.CDLL:
         L.lrqo_pow2_bf16.restype = ctypes.c_uint16
         L.lrqo_pow2_f16.argtypes = [ctypes.c_uint16]
         L.lrqo_pow2_f16.restype = ctypes.c_uint16
+        L.lrqo_act_qdq.argtypes = [vp, ci, i64, i64, i64, ci, vp, ci]
         L.lrqo_e4m3_to_f32.argtypes = [ctypes.c_uint8]
         L.lrqo_e4m3_to_f32.restype = ctypes.c_float
         _LIB = L
@@ -124,6 +125,18 @@ def mx_quant(x: np.ndarray, dtype: str = "bf16", fmt: int = 8,
     if rc:
         raise ValueError("oracle rejected the arguments")
     return codes, scales
+
+
+def act_qdq(x: np.ndarray, dtype: str = "f32", block: int = 128, pow2: bool = False,
+            nthreads: int = 0) -> np.ndarray:
+    """_FP8W8A8Linear activation fake-quant of a 2-D [rows, cols] array -> float32."""
+    x = _as_input(x, dtype)
+    rows, cols = x.shape
+    out = np.zeros((rows, cols), np.float32)
+    rc = lib().lrqo_act_qdq(_ptr(x), DTYPES[dtype], rows, cols, block, int(pow2), _ptr(out), nthreads)
+    if rc:
+        raise ValueError("oracle rejected the arguments")
+    return out
 
 
 def e4m3_from_f32(x: np.ndarray) -> np.ndarray:

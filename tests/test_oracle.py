@@ -266,6 +266,41 @@ def test_fp8_ragged_tiles_vs_torch_reference():
     assert np.array_equal(s.numpy().view(np.uint32), so[0].view(np.uint32))
 
 
+@pytest.mark.parametrize("dt", ["bf16", "f16", "f32"])
+@pytest.mark.parametrize("pow2", [False, True])
+@pytest.mark.parametrize("blk", [32, 128, 256])
+@pytest.mark.parametrize("data", ["acts", "edge"])
+def test_act_qdq_oracle_vs_torch_reference(dt, pow2, blk, data):
+    """Activation fake-quant (fp8_rollout.py:53-72) against the torch op sequence."""
+    if data == "acts":
+        x = (RNG.standard_t(3, (96, 512)) * 0.7).astype(np.float32)
+        x[5, :blk] = 0.0
+        x[7, 3] = 60000.0
+    else:
+        x = _edge()
+    t, xin = _torch_input(x, dt)
+    want = T.act_qdq(t, blk, pow2).numpy()
+    got = O.act_qdq(xin, dt, blk, pow2)
+    wb, gb = want.view(np.uint32), got.view(np.uint32)
+    if pow2:
+        # pow(2, NaN) bits depend on torch's vector-body/scalar-tail position;
+        # elsewhere bit-exact, NaN where torch has NaN
+        nan = np.isnan(want)
+        assert np.array_equal(wb[~nan], gb[~nan])
+        assert np.isnan(got[nan]).all()
+    else:
+        assert np.array_equal(wb, gb)
+    # no e4m3 rounding happens (the reference emulates, it does not cast):
+    # x/s*s is x up to two f32 roundings, plus the subnormal grid of x/s
+    # (spacing 2^-149) scaled back by s, with s <= 2*max(amax/448, FLT_MIN)
+    xf = t.float().numpy()
+    amax = np.abs(xf).reshape(xf.shape[0], -1, blk).max(axis=-1)
+    sblk = np.repeat(np.maximum(amax / 448.0, np.finfo(np.float32).tiny), blk, axis=-1)
+    fin = np.isfinite(got) & np.isfinite(xf) & np.isfinite(sblk)
+    bound = 2 * np.spacing(np.abs(xf)) + 2 * sblk * 2.0 ** -149
+    assert np.all(np.abs(got - xf)[fin] <= bound[fin])
+
+
 def test_dequant_oracle_vs_torch_reference():
     g = load_golden("fp8_dequant.npz")
     out = O.fp8_block_dequant(g["codes"], g["scales"], "f32", (1, 128), "f32")
@@ -294,6 +329,14 @@ def test_oracle_reproduces_fp8_golden(name):
         assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
     else:
         assert np.array_equal(got, want)
+
+
+@pytest.mark.parametrize("name", ["act_bf16.npz", "act_bf16_b32_pow2.npz", "act_f32_pow2.npz"])
+def test_oracle_reproduces_act_golden(name):
+    g = load_golden(name)
+    dt = "f32" if g["x"].dtype == np.float32 else "bf16"
+    out = O.act_qdq(g["x"], dt, int(g["block"][0]), bool(g["pow2"][0]))
+    assert np.array_equal(out.view(np.uint32), g["out"].view(np.uint32))
 
 
 @pytest.mark.parametrize("name", ["mxfp8_bf16.npz", "mxfp4_bf16.npz", "mxfp8_f32.npz", "mxfp4_f32.npz"])
