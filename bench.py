@@ -16,6 +16,9 @@ already resident in HBM:
   c2r: c2 weights with the reference's own 1x128 blocks (scales [N, K/128]).
   c2d: dequantize_state_dict of the c2r result: e4m3 codes + bf16 1x128 scales ->
        bf16 weights, ONE grouped launch.
+  kv:  FP8KVCacheQuantizer scale recalibration: max(|W|.max(), FLT_MIN)/448 over
+       the 108 q/k/v_proj weights of Qwen3-8B (c2's values), one grouped
+       amax launch + one per-tensor finishing launch.
   act: the W8A8 rollout linear's activation fake-quant (fp8_rollout.py:53-72)
        on the seven linear inputs of one Qwen3-8B layer for an 8192-token
        prefill chunk (bf16 in, float32 out), one launch per linear, every input
@@ -51,9 +54,9 @@ QWEN3_8B = [("q_proj", 4096, 4096), ("k_proj", 1024, 4096), ("v_proj", 1024, 409
 PROFILE_FOR = {"c2": "k_tile128_qwen3_8b_fp8_128x128", "c2r": "k_row_qwen3_8b_fp8_1x128",
                "c3": "k_tile128_qwen3_30b_a3b_experts", "c4": "k_mx_qwen3_8b_mxfp8",
                "c5": "k_mx_qwen3_8b_mxfp4", "c2d": "k_dequant_qwen3_8b_fp8_1x128_to_bf16",
-               "act": "k_act_qdq_qwen3_8b_prefill_8192"}
+               "act": "k_act_qdq_qwen3_8b_prefill_8192", "kv": "k_amax_qwen3_8b_qkv_scales"}
 KERNEL_FOR = {"c1": "k_tile128", "c2": "k_tile128", "c3": "k_tile128", "c4": "k_mx", "c5": "k_mx",
-              "c2r": "k_row", "c2d": "k_dequant", "act": "k_act_qdq8"}
+              "c2r": "k_row", "c2d": "k_dequant", "act": "k_act_qdq8", "kv": "k_amax"}
 PREFILL_TOKENS = 8192
 
 
@@ -143,7 +146,12 @@ def cpu_baseline(torch, ws, fmt, fmt_block, seconds):
                 break
             continue
         x = w.cpu()
-        if fmt == "act":
+        if fmt == "kv":
+            t0 = time.perf_counter()
+            torch_ref.kv_scale(x)
+            t_total += time.perf_counter() - t0
+            done_bytes += x.numel() * 2 + 4
+        elif fmt == "act":
             t0 = time.perf_counter()
             out = torch_ref.act_qdq(x, fmt_block[1])
             t_total += time.perf_counter() - t0
@@ -170,6 +178,7 @@ def cpu_baseline(torch, ws, fmt, fmt_block, seconds):
                       f"{fmt_block[0]}x{fmt_block[1]} blocks, fp32 upcast first)"),
         "fp8_dequant": "oracle/torch_ref.py (weight_quantizer.py:79-89 then the bf16 cast of :133)",
         "act": "oracle/torch_ref.py (fp8_rollout.py:53-72 op order)",
+        "kv": "oracle/torch_ref.py (fp8_kv_cache.py:52-54 op order, one tensor at a time)",
     }.get(fmt, f"the C oracle's {fmt} restatement (the reference has no MX CPU path)")
     return {
         "value": round(done_bytes / t_total / 1e9, 3),
@@ -231,6 +240,14 @@ def run(args):
         cpu_ws, cpu_blk, cpu_fmt = ws, blk, fmt
         extra = {"tensors": len(ws), "layers": 36, "elements": sum(w.numel() for w in ws),
                  "format": fmt, "launches_per_step": 1}
+    elif cfg == "kv":
+        ws, names = qwen3_8b_set(torch, dev, args.seed, "normal")
+        ws = [w for w, nm in zip(ws, names) if nm.split(".")[-1] in ("q_proj", "k_proj", "v_proj")]
+        plans = [ops.TensorScalePlan(ws)]
+        workload = "qwen3-8b-qkv-proj-fp8-kv-scales"
+        cpu_ws, cpu_blk, cpu_fmt = ws, (1, 1), "kv"
+        extra = {"tensors": len(ws), "layers": 36, "elements": sum(w.numel() for w in ws),
+                 "format": "per_tensor_e4m3_scale", "launches_per_step": 2}
     elif cfg == "act":
         g = torch.Generator(device=dev).manual_seed(args.seed)
         ins = [("q_proj", 4096), ("k_proj", 4096), ("v_proj", 4096), ("o_proj", 4096),
@@ -379,7 +396,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--config", default="c2", choices=["c1", "c2", "c3", "c4", "c5", "c2r", "c2d", "act"])
+    ap.add_argument("--config", default="c2", choices=["c1", "c2", "c3", "c4", "c5", "c2r", "c2d", "act", "kv"])
     ap.add_argument("--seed", type=int, default=1000)
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")

@@ -51,6 +51,9 @@ typedef struct ihipStream_t* lrq_stream_t; /* == hipStream_t */
 #define LRQ_FMT_MXFP4 2
 #define LRQ_FMT_FP8_DEQUANT 3 /* grouped dequant: lrq_tensor.in = codes, .codes = output,
                                  in_dtype = scale dtype, LRQ_FLAG_OUT_BF16 = bf16 output */
+#define LRQ_FMT_TENSOR_SCALE 4 /* per-tensor FP8 scale (lrq_tensor_scale_grouped):
+                                  lrq_tensor.in = weight, .scales = one float32 out,
+                                  .codes unused (may be NULL) */
 
 /* errors */
 #define LRQ_ERR_ARG (-1)      /* invalid argument (shape, dtype, block size, null) */
@@ -150,6 +153,23 @@ int lrq_group_pack(int fmt, const lrq_tensor* tensors, int64_t n, int in_dtype, 
 int lrq_quant_grouped(const void* host_table, const void* device_table, lrq_stream_t stream);
 /* work-groups of a packed table's launch (for bandwidth accounting) */
 int64_t lrq_group_units(const void* host_table);
+/*
+ * Per-tensor FP8 scales of the KV-cache quantizer, for a table packed with
+ * fmt LRQ_FMT_TENSOR_SCALE (blk_r, blk_c and flags are ignored):
+ *   scale = max(|w|.max(), FLT_MIN) / 448  per tensor (float32),
+ * the clamp applied BEFORE the division as in
+ * FP8KVCacheQuantizer.recalibrate_scales (lumenrl/quantization/fp8_kv_cache.py:52-54),
+ * which this replaces for all q/k/v projections in two launches.  A tensor
+ * holding a NaN gets 0x7FC00000 (torch's multi-threaded x86 reduction);
+ * empty tensors are rejected (torch's max() raises for them).
+ * `workspace` is device memory of at least lrq_group_workspace_bytes(table)
+ * bytes (4 per work-group) that the launch overwrites; launches sharing one
+ * workspace must be stream-ordered.  lrq_group_workspace_bytes() is 0 for
+ * every other format.
+ */
+int64_t lrq_group_workspace_bytes(const void* host_table);
+int lrq_tensor_scale_grouped(const void* host_table, const void* device_table, void* workspace,
+                             int64_t workspace_bytes, lrq_stream_t stream);
 
 /* Library version string ("lrq <semver> gfx950"). */
 const char* lrq_version(void);

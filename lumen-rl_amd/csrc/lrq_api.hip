@@ -51,7 +51,7 @@ struct GroupHeader {
 int64_t align_up(int64_t x, int64_t a) { return (x + a - 1) / a * a; }
 
 // Fill a Desc from a tensor and check its shape.
-int make_desc(const lrq_tensor& t, Desc& d) {
+int make_desc(const lrq_tensor& t, Desc& d, bool need_codes = true) {
   if (t.batch < 0 || t.rows < 0 || t.cols < 0) return fail(LRQ_ERR_ARG, "negative extent");
   if (t.batch == 0 || t.rows == 0 || t.cols == 0) {
     memset(&d, 0, sizeof(d));
@@ -61,7 +61,7 @@ int make_desc(const lrq_tensor& t, Desc& d) {
   if (t.ld < t.cols) return fail(LRQ_ERR_ARG, "ld (%lld) < cols (%lld)", (long long)t.ld, (long long)t.cols);
   if (t.batch > 1 && t.batch_stride < (t.rows - 1) * t.ld + t.cols)
     return fail(LRQ_ERR_ARG, "batch_stride (%lld) overlaps matrices", (long long)t.batch_stride);
-  if (!t.in || !t.codes || !t.scales) return fail(LRQ_ERR_ARG, "null pointer");
+  if (!t.in || (need_codes && !t.codes) || !t.scales) return fail(LRQ_ERR_ARG, "null pointer");
   memset(&d, 0, sizeof(d));
   d.in = t.in;
   d.codes = static_cast<uint8_t*>(t.codes);
@@ -226,6 +226,8 @@ int plan_group(int fmt, const lrq_tensor* ts, int64_t n, int in_dtype, int64_t b
     cfg.blk_r = (int)blk_r;
     cfg.blk_c = (int)blk_c;
     cfg.out_dtype = (flags & LRQ_FLAG_OUT_BF16) ? lrq::kBF16 : lrq::kF32;
+  } else if (fmt == LRQ_FMT_TENSOR_SCALE) {
+    cfg.kernel = lrq::kKernAmax;
   } else {
     return fail(LRQ_ERR_ARG, "bad format %d", fmt);
   }
@@ -233,7 +235,25 @@ int plan_group(int fmt, const lrq_tensor* ts, int64_t n, int in_dtype, int64_t b
   int64_t units = 0;
   for (int64_t i = 0; i < n; ++i) {
     Desc d;
-    if (int rc = make_desc(ts[i], d)) return fail(rc, "tensor %lld: %s", (long long)i, g_err.c_str());
+    if (int rc = make_desc(ts[i], d, fmt != LRQ_FMT_TENSOR_SCALE))
+      return fail(rc, "tensor %lld: %s", (long long)i, g_err.c_str());
+    if (fmt == LRQ_FMT_TENSOR_SCALE) {
+      if (d.batch == 0 || d.rows == 0 || d.cols == 0)
+        return fail(LRQ_ERR_ARG, "tensor %lld is empty: a max over no elements is undefined", (long long)i);
+      if (!aligned(d.scales, 4)) return fail(LRQ_ERR_ALIGN, "tensor %lld: scale not 4-byte aligned", (long long)i);
+      const int64_t es = esize(in_dtype);
+      const bool vec = aligned(d.in, 16) && (d.ld * es) % 16 == 0 && d.cols % (16 / es) == 0 &&
+                       (d.batch == 1 || (d.bstride * es) % 16 == 0);
+      const bool dense = d.ld == d.cols && (d.batch == 1 || d.bstride == d.rows * d.cols);
+      d.units_c = vec ? 1 : 0;
+      d.units_r = dense ? 1 : 0;
+      const int64_t per = lrq::amax_unit_elems(in_dtype, vec);
+      d.units = (d.batch * d.rows * d.cols + per - 1) / per;
+      d.unit0 = units;
+      units += d.units;
+      if (ds) ds[i] = d;
+      continue;
+    }
     if (d.batch == 0 || d.rows == 0 || d.cols == 0) {
       if (ds) { ds[i] = d; ds[i].unit0 = units; ds[i].units = 0; }
       continue;
@@ -260,7 +280,8 @@ int plan_group(int fmt, const lrq_tensor* ts, int64_t n, int in_dtype, int64_t b
     units += d.units;
     if (ds) ds[i] = d;
   }
-  if (kernel < 0) cfg.kernel = fmt == LRQ_FMT_FP8_BLOCK ? lrq::kKernGenericFp8 : lrq::kKernGenericMx;
+  if (kernel < 0 && fmt != LRQ_FMT_TENSOR_SCALE)
+    cfg.kernel = fmt == LRQ_FMT_FP8_BLOCK ? lrq::kKernGenericFp8 : lrq::kKernGenericMx;
   if (fmt == LRQ_FMT_FP8_DEQUANT) {
     cfg.rows_dense = 1;
     for (int64_t i = 0; i < n; ++i)
@@ -385,12 +406,45 @@ int lrq_quant_grouped(const void* host_table, const void* device_table, lrq_stre
   memcpy(&h, host_table, sizeof(h));
   if (h.magic != kMagic || h.version != kTableVersion) return fail(LRQ_ERR_TABLE, "not an lrq table");
   if (h.units == 0) return 0;
+  if (h.cfg.kernel == lrq::kKernAmax)
+    return fail(LRQ_ERR_ARG, "a tensor-scale table needs a workspace: call lrq_tensor_scale_grouped");
   const char* dev = static_cast<const char*>(device_table);
   const Desc* descs = reinterpret_cast<const Desc*>(dev + h.desc_off);
   const uint32_t* map = reinterpret_cast<const uint32_t*>(dev + h.map_off);
   Desc dummy;
   memset(&dummy, 0, sizeof(dummy));
   return check_hip(lrq::launch(h.cfg, dummy, descs, map, h.units, (hipStream_t)stream), "kernel launch");
+}
+
+int64_t lrq_group_workspace_bytes(const void* host_table) {
+  g_err.clear();
+  if (!host_table) return fail(LRQ_ERR_ARG, "null table");
+  GroupHeader h;
+  memcpy(&h, host_table, sizeof(h));
+  if (h.magic != kMagic || h.version != kTableVersion) return fail(LRQ_ERR_TABLE, "not an lrq table");
+  return h.cfg.kernel == lrq::kKernAmax ? h.units * 4 : 0;
+}
+
+int lrq_tensor_scale_grouped(const void* host_table, const void* device_table, void* workspace,
+                             int64_t workspace_bytes, lrq_stream_t stream) {
+  g_err.clear();
+  if (!host_table || !device_table) return fail(LRQ_ERR_ARG, "null table");
+  GroupHeader h;
+  memcpy(&h, host_table, sizeof(h));
+  if (h.magic != kMagic || h.version != kTableVersion) return fail(LRQ_ERR_TABLE, "not an lrq table");
+  if (h.cfg.kernel != lrq::kKernAmax) return fail(LRQ_ERR_ARG, "not a tensor-scale table");
+  if (h.n == 0) return 0;
+  if (!workspace || !aligned(workspace, 4)) return fail(LRQ_ERR_ARG, "workspace must be 4-byte aligned device memory");
+  if (workspace_bytes < h.units * 4)
+    return fail(LRQ_ERR_CAPACITY, "workspace needs %lld bytes, have %lld", (long long)(h.units * 4),
+                (long long)workspace_bytes);
+  if (h.n > kMaxGrid) return fail(LRQ_ERR_ARG, "too many tensors for one launch");
+  const char* dev = static_cast<const char*>(device_table);
+  const Desc* descs = reinterpret_cast<const Desc*>(dev + h.desc_off);
+  const uint32_t* map = reinterpret_cast<const uint32_t*>(dev + h.map_off);
+  return check_hip(lrq::launch_tensor_scale(h.cfg, descs, map, h.n, h.units, static_cast<uint32_t*>(workspace),
+                                            (hipStream_t)stream),
+                   "kernel launch");
 }
 
 int64_t lrq_group_units(const void* host_table) {

@@ -18,8 +18,8 @@ struct Desc {
   int64_t batch, rows, cols, ld, bstride;
   int64_t unit0;
   int64_t units;     // work-groups of this tensor
-  int64_t units_c;   // tile kernel: tiles per row band; row/MX kernels: unused
-  int64_t units_r;   // tile kernel: tile rows per matrix
+  int64_t units_c;   // tile kernel: tiles per row band; amax: 1 = 16-byte loads
+  int64_t units_r;   // tile kernel: tile rows per matrix; amax: 1 = contiguous
   int64_t nblocks;   // row/MX kernels: number of blocks/groups
   int64_t bpr;       // row/MX kernels: blocks (groups) per row
 };
@@ -33,6 +33,7 @@ enum Kernel : int {
   kKernGenericMx = 4,
   kKernDequant = 5,        // FP8 dequant, 16 codes per lane-chunk
   kKernGenericDequant = 6, // FP8 dequant, one element per thread
+  kKernAmax = 7,           // per-tensor max |x| partials + scale (two launches)
 };
 
 // Descriptor and local work unit of this work-group: the single-tensor
@@ -77,11 +78,18 @@ hipError_t launch_fp8(const LaunchCfg&, const Desc&, const Desc*, const uint32_t
 hipError_t launch_mx(const LaunchCfg&, const Desc&, const Desc*, const uint32_t*, int64_t, hipStream_t);
 hipError_t launch_dequant(const LaunchCfg&, const Desc&, const Desc*, const uint32_t*, int64_t, hipStream_t);
 
+// Per-tensor scales: k_amax over `units` work-groups writing partial[unit],
+// then one work-group per tensor (n) reducing them into the tensor's scale.
+int64_t amax_unit_elems(int dtype, bool vec);
+hipError_t launch_tensor_scale(const LaunchCfg& cfg, const Desc* descs, const uint32_t* map, int64_t n,
+                               int64_t units, uint32_t* partial, hipStream_t stream);
 
-// Diagnostics: element encoders applied to raw inputs.
+// Activation fake-quant.
 int64_t act_grid(const void* in, int dtype, int64_t rows, int64_t cols, int64_t ld);
 hipError_t launch_act(const void* in, int dtype, int64_t rows, int64_t cols, int64_t ld, int64_t blk,
                       float* out, int pow2, hipStream_t stream);
+
+// Diagnostics: element encoders applied to raw inputs.
 hipError_t launch_diag_e4m3_bits(uint32_t start, int64_t n, uint8_t* out, hipStream_t stream);
 hipError_t launch_diag_bf16_bits(uint32_t start, int64_t n, uint16_t* out, hipStream_t stream);
 hipError_t launch_diag_mx(int fmt, const float* in, const uint8_t* e8m0, int64_t n, uint8_t* out,

@@ -15,7 +15,7 @@ LIB_PATH = os.path.join(_HERE, "liblrq.so")
 
 DTYPE_BF16, DTYPE_F16, DTYPE_F32 = 0, 1, 2
 FLAG_POW2_SCALE, FLAG_NATIVE_ARITH, FLAG_SCALE_BF16, FLAG_OUT_BF16 = 1, 2, 4, 8
-FMT_FP8_BLOCK, FMT_MXFP8, FMT_MXFP4, FMT_FP8_DEQUANT = 0, 1, 2, 3
+FMT_FP8_BLOCK, FMT_MXFP8, FMT_MXFP4, FMT_FP8_DEQUANT, FMT_TENSOR_SCALE = 0, 1, 2, 3, 4
 ERR_ARG, ERR_ALIGN, ERR_CAPACITY, ERR_TABLE = -1, -2, -3, -4
 
 
@@ -50,6 +50,8 @@ SIGNATURES = {
     "lrq_group_pack": (_CI, [_CI, ctypes.POINTER(LrqTensor), _I64, _CI, _I64, _I64, _CU, _VP, _I64]),
     "lrq_quant_grouped": (_CI, [_VP, _VP, _VP]),
     "lrq_group_units": (_I64, [_VP]),
+    "lrq_group_workspace_bytes": (_I64, [_VP]),
+    "lrq_tensor_scale_grouped": (_CI, [_VP, _VP, _VP, _I64, _VP]),
     "lrq_version": (ctypes.c_char_p, []),
     "lrq_last_error": (ctypes.c_char_p, []),
     "lrq_diag_e4m3_bits": (_CI, [ctypes.c_uint32, _I64, _VP, _VP]),

@@ -7,10 +7,12 @@ from lumenrl_amd.quantization.fp8_config import (
     RolloutQuantConfig,
     TrainingQuantConfig,
 )
+from lumenrl_amd.quantization.fp8_kv_cache import FP8KVCacheQuantizer
 from lumenrl_amd.quantization.fp8_rollout import FP8RolloutQuantizer
 from lumenrl_amd.quantization.ops import (
     DequantPlan,
     QuantPlan,
+    TensorScalePlan,
     quantize_fp8_blockwise,
     quantize_mxfp4,
     quantize_mxfp8,
@@ -21,11 +23,13 @@ from lumenrl_amd.quantization.weight_quantizer import WeightQuantizer, fp8_e4m3_
 __all__ = [
     "DequantPlan",
     "FP8Config",
+    "FP8KVCacheQuantizer",
     "FP8RolloutQuantizer",
     "QuantizationConfig",
     "QuantPlan",
     "QuantizedBucketWriter",
     "RolloutQuantConfig",
+    "TensorScalePlan",
     "TrainingQuantConfig",
     "WeightQuantizer",
     "act_qdq",

@@ -237,7 +237,7 @@ def quantize_fp8_blockwise(x: Tensor, block_size: tuple[int, int] = (128, 128), 
 # grouped launches
 # ---------------------------------------------------------------------------
 _FMTS = {"fp8_block": _lib.FMT_FP8_BLOCK, "mxfp8": _lib.FMT_MXFP8, "mxfp4": _lib.FMT_MXFP4,
-         "fp8_dequant": _lib.FMT_FP8_DEQUANT}
+         "fp8_dequant": _lib.FMT_FP8_DEQUANT, "tensor_scale": _lib.FMT_TENSOR_SCALE}
 
 
 class _GroupLaunch:
@@ -263,6 +263,16 @@ class _GroupLaunch:
             rc = _lib.lib().lrq_quant_grouped(self.host.data_ptr(), self.dev.data_ptr(),
                                               _stream(self.device))
         _lib.check(rc, "lrq_quant_grouped")
+
+    def workspace_bytes(self) -> int:
+        return int(_lib.lib().lrq_group_workspace_bytes(self.host.data_ptr()))
+
+    def run_tensor_scale(self, workspace: Tensor) -> None:
+        with torch.cuda.device(self.device):
+            rc = _lib.lib().lrq_tensor_scale_grouped(self.host.data_ptr(), self.dev.data_ptr(),
+                                                     workspace.data_ptr(), _nbytes(workspace),
+                                                     _stream(self.device))
+        _lib.check(rc, "lrq_tensor_scale_grouped")
 
 
 def _nbytes(t: Tensor) -> int:
@@ -409,6 +419,59 @@ class DequantPlan:
     def run(self) -> list[Tensor]:
         self._launch.run()
         return self.outputs
+
+
+class TensorScalePlan:
+    """Per-tensor FP8 scales of a list of weights in two launches.
+
+    ``scales[i] = max(|w_i|.max(), FLT_MIN) / 448`` (float32), the clamp before
+    the division as in FP8KVCacheQuantizer.recalibrate_scales
+    (lumenrl/quantization/fp8_kv_cache.py:52-54).  The plan owns a float32 [n]
+    device tensor ``scales`` (or writes into ``out``) and a partial-maximum
+    workspace; ``run()`` recomputes the scales from the tensors' current values.
+    """
+
+    def __init__(self, tensors: Sequence[Tensor], out: Optional[Tensor] = None) -> None:
+        if not tensors:
+            raise ValueError("TensorScalePlan needs at least one tensor")
+        dt, dev = tensors[0].dtype, tensors[0].device
+        for t in tensors:
+            _check_input(t, "TensorScalePlan")
+            if t.dtype != dt or t.device != dev:
+                raise ValueError("all tensors of a TensorScalePlan must share dtype and device")
+            if t.numel() == 0:
+                raise RuntimeError("max(): a per-tensor scale of an empty tensor is undefined")
+        n = len(tensors)
+        if out is None:
+            out = torch.empty(n, dtype=torch.float32, device=dev)
+        elif out.dtype != torch.float32 or out.shape != (n,) or not out.is_contiguous() or out.device != dev:
+            raise ValueError(f"out must be a contiguous float32 [{n}] tensor on {dev}")
+        self.device = dev
+        self.inputs = list(tensors)
+        self.scales = out
+        descs = (_lib.LrqTensor * n)()
+        self._views = []
+        nbytes = 0
+        for i, t in enumerate(tensors):
+            xm, batch, rows, cols, ld, bstride = matrix_view(t)
+            if xm.data_ptr() != t.data_ptr():
+                raise ValueError(f"tensor {i} is not a strided matrix view; pass .contiguous()")
+            self._views.append(xm)
+            descs[i].in_ = xm.data_ptr()
+            descs[i].codes = None
+            descs[i].scales = out.data_ptr() + 4 * i
+            descs[i].batch, descs[i].rows, descs[i].cols = batch, rows, cols
+            descs[i].ld, descs[i].batch_stride = ld, bstride
+            nbytes += _nbytes(t)
+        self.algorithmic_bytes = nbytes + 4 * n
+        self._launch = _GroupLaunch("tensor_scale", descs, n, _IN_DTYPES[dt], (1, 1), 0, dev)
+        self.units = self._launch.units
+        self.workspace = torch.empty(self._launch.workspace_bytes(), dtype=torch.uint8, device=dev)
+
+    def run(self) -> Tensor:
+        """Enqueue both launches on the current stream; returns ``scales``."""
+        self._launch.run_tensor_scale(self.workspace)
+        return self.scales
 
 
 def _prod(shape) -> int:

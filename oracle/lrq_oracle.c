@@ -464,6 +464,26 @@ int lrqo_act_qdq(const void* in, int in_dtype, int64_t rows, int64_t cols, int64
   return 0;
 }
 
+/* Per-tensor FP8 scale of FP8KVCacheQuantizer.recalibrate_scales
+ * (lumenrl/quantization/fp8_kv_cache.py:52-54): w.to(float32).abs().max(),
+ * clamp(min=FLT_MIN), then / 448 (division AFTER the clamp, so an all-zero
+ * tensor gives the subnormal FLT_MIN/448).  A NaN anywhere gives the canonical
+ * quiet NaN 0x7FC00000: torch's multi-threaded CPU reduction over more than
+ * 32768 elements, the regime of every q/k/v projection (a single-threaded or
+ * smaller reduction gives all-ones instead).  Returns the scale's bit pattern;
+ * `in` is `n` contiguous elements. */
+uint32_t lrqo_tensor_scale(const void* in, int in_dtype, int64_t n) {
+  uint32_t amax_bits = 0;
+  for (int64_t i = 0; i < n; ++i) {
+    uint32_t a = f2u(load_in(in, in_dtype, i)) & 0x7FFFFFFFu;
+    if (a > amax_bits) amax_bits = a;
+  }
+  if (amax_bits > 0x7F800000u) return 0x7FC00000u;
+  float amax = u2f(amax_bits);
+  if (amax < 0x1p-126f) amax = 0x1p-126f;
+  return f2u(amax / 448.0f);
+}
+
 /* Bulk element converters, for exhaustive checks against torch. */
 void lrqo_f32_to_e4m3_n(const float* in, uint8_t* out, int64_t n) {
 #ifdef _OPENMP

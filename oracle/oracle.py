@@ -51,6 +51,8 @@ def lib() -> ctypes.CDLL:
         L.lrqo_pow2_f16.argtypes = [ctypes.c_uint16]
         L.lrqo_pow2_f16.restype = ctypes.c_uint16
         L.lrqo_act_qdq.argtypes = [vp, ci, i64, i64, i64, ci, vp, ci]
+        L.lrqo_tensor_scale.argtypes = [vp, ci, i64]
+        L.lrqo_tensor_scale.restype = ctypes.c_uint32
         L.lrqo_e4m3_to_f32.argtypes = [ctypes.c_uint8]
         L.lrqo_e4m3_to_f32.restype = ctypes.c_float
         _LIB = L
@@ -137,6 +139,12 @@ def act_qdq(x: np.ndarray, dtype: str = "f32", block: int = 128, pow2: bool = Fa
     if rc:
         raise ValueError("oracle rejected the arguments")
     return out
+
+
+def tensor_scale(x: np.ndarray, dtype: str = "bf16") -> np.uint32:
+    """FP8KVCacheQuantizer per-tensor scale of a whole tensor -> float32 bit pattern."""
+    x = _as_input(x, dtype)
+    return np.uint32(lib().lrqo_tensor_scale(_ptr(x), DTYPES[dtype], x.size))
 
 
 def e4m3_from_f32(x: np.ndarray) -> np.ndarray:

@@ -152,6 +152,42 @@ def test_group_pack_rejects_mixed_kernels_and_small_buffers():
     assert rc == _lib.ERR_CAPACITY
 
 
+def test_tensor_scale_tables():
+    """Per-tensor scale tables: 32 KiB units (16-byte loads) or 8192-element units
+    (element walk) in one table, no codes pointer, workspace of 4 B per unit."""
+    qkv = [(1, 4096, 4096), (1, 1024, 4096), (1, 1024, 4096)]
+    ts = _tensors(qkv + [(1, 300, 100)])
+    for t in ts:
+        t.codes = None
+    ts[3].in_ = ts[3].in_ + 2  # misaligned: element walk
+    fmt = _lib.FMT_TENSOR_SCALE
+    need = L().lrq_group_table_bytes(fmt, ts, 4, 0, 1, 1, 0)
+    assert need > 0, _lib.last_error()
+    buf = np.zeros(need, np.uint8)
+    assert L().lrq_group_pack(fmt, ts, 4, 0, 1, 1, 0, buf.ctypes.data, need) == 0, _lib.last_error()
+    units = [4096 * 4096 // 16384, 1024 * 4096 // 16384, 1024 * 4096 // 16384, -(-300 * 100 // 8192)]
+    assert L().lrq_group_units(buf.ctypes.data) == sum(units)
+    assert L().lrq_group_workspace_bytes(buf.ctypes.data) == 4 * sum(units)
+    wmap = buf[-4 * sum(units):].view(np.uint32)
+    assert np.array_equal(wmap, np.repeat(np.arange(4, dtype=np.uint32), units))
+    # argument errors are reported before any device work
+    assert L().lrq_quant_grouped(buf.ctypes.data, buf.ctypes.data, None) == _lib.ERR_ARG
+    assert "workspace" in _lib.last_error()
+    small = 4 * sum(units) - 4
+    rc = L().lrq_tensor_scale_grouped(buf.ctypes.data, buf.ctypes.data, ctypes.c_void_p(0x1000), small, None)
+    assert rc == _lib.ERR_CAPACITY
+    rc = L().lrq_tensor_scale_grouped(buf.ctypes.data, buf.ctypes.data, None, 1 << 20, None)
+    assert rc == _lib.ERR_ARG
+    fp8 = _pack(_lib.FMT_FP8_BLOCK, qkv)
+    assert L().lrq_group_workspace_bytes(fp8.ctypes.data) == 0
+    rc = L().lrq_tensor_scale_grouped(fp8.ctypes.data, fp8.ctypes.data, ctypes.c_void_p(0x1000), 1 << 20, None)
+    assert rc == _lib.ERR_ARG and "not a tensor-scale table" in _lib.last_error()
+    # an empty tensor has no max (torch's max() raises)
+    ts = _tensors([(1, 0, 128)])
+    assert L().lrq_group_table_bytes(fmt, ts, 1, 0, 1, 1, 0) == _lib.ERR_ARG
+    assert "empty" in _lib.last_error()
+
+
 def test_grouped_rejects_foreign_table():
     junk = np.zeros(4096, np.uint8)
     rc = L().lrq_quant_grouped(junk.ctypes.data, ctypes.c_void_p(0x1000), None)

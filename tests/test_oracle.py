@@ -301,6 +301,45 @@ def test_act_qdq_oracle_vs_torch_reference(dt, pow2, blk, data):
     assert np.all(np.abs(got - xf)[fin] <= bound[fin])
 
 
+@pytest.mark.parametrize("dt", ["bf16", "f16", "f32"])
+@pytest.mark.parametrize("case", ["weights", "zero", "subnormal", "inf", "nan", "huge", "negative"])
+def test_tensor_scale_oracle_vs_torch_reference(dt, case):
+    """FP8KVCacheQuantizer scale (fp8_kv_cache.py:52-54) over a projection-sized
+    tensor (> 32768 elements: torch's multi-threaded reduction)."""
+    x = weights((256, 384))
+    if case == "zero":
+        x[:] = 0.0
+        x[3, 4] = -0.0
+    elif case == "subnormal":
+        x[:] = np.float32(1e-40) if dt != "f16" else np.float32(3e-8)
+    elif case == "inf":
+        x[100, 7] = -np.inf
+    elif case == "nan":
+        x[200, 300] = np.nan
+    elif case == "huge":
+        x[0, 0] = 3.0e38 if dt != "f16" else 65504.0
+    elif case == "negative":
+        x[17, 5] = -9.5
+    t, xin = _torch_input(x, dt)
+    prev = torch.get_num_threads()
+    torch.set_num_threads(max(2, prev))
+    try:
+        want = T.kv_scale(t).reshape(1).view(torch.int32).item() & 0xFFFFFFFF
+    finally:
+        torch.set_num_threads(prev)
+    assert int(O.tensor_scale(xin, dt)) == want
+
+
+def test_tensor_scale_division_every_bf16_amax():
+    """clamp-then-divide over every finite non-negative bf16 amax, against
+    torch's elementwise clamp and division."""
+    b = np.arange(0, 0x7F81, dtype=np.uint32)
+    amax = torch.from_numpy((b << 16).view(np.float32).copy())
+    want = (amax.clamp(min=torch.finfo(torch.float32).tiny) / 448.0).numpy().view(np.uint32)
+    got = np.array([O.tensor_scale(np.array([0, int(v)], np.uint16), "bf16") for v in b], np.uint32)
+    assert np.array_equal(got, want)
+
+
 def test_dequant_oracle_vs_torch_reference():
     g = load_golden("fp8_dequant.npz")
     out = O.fp8_block_dequant(g["codes"], g["scales"], "f32", (1, 128), "f32")
