@@ -1,0 +1,123 @@
+"""BASELINE configs 2-5 at their full sizes on an MI355X.
+
+The inputs are the ones bench.py times, from its generators and seed.
+- C2 (the whole Qwen3-8B linear set, 128x128 FP8), C4 (MXFP8) and C5 (MXFP4)
+  are compared with the CPU oracle bit for bit, tensor by tensor.
+- C3 (Qwen3-30B-A3B experts, 48 layers x 128 experts, one launch per layer)
+  is too large for the oracle in a test's time.  Every layer is checked
+  through exact size-independent properties:
+  - each tile's scale equals max(RN(amax/448), FLT_MIN) computed by numpy
+    from the device's exact tile amax;
+  - each tile's largest |code| is 448 (0x7E) unless the tile is zero or
+    non-finite.
+  Three whole layers, and every layer's planted zero-tile and inf-tile
+  experts, are also compared with the oracle bit for bit.
+"""
+
+from __future__ import annotations
+
+import os
+
+import numpy as np
+import pytest
+import torch
+
+import bench as B
+from oracle import oracle as O
+from lumenrl_amd.quantization import QuantPlan
+
+pytestmark = [pytest.mark.gpu, pytest.mark.slow]
+
+if not torch.cuda.is_available():  # pragma: no cover - CPU container
+    pytest.skip("needs a HIP device", allow_module_level=True)
+
+DEV = torch.device("cuda", 0)
+SEED = 1000  # bench.py's default --seed
+THREADS = max(1, min(os.cpu_count() or 1, 16))
+
+
+def say(*a):
+    print(*a, flush=True)
+
+
+def host16(t: torch.Tensor) -> np.ndarray:
+    return t.detach().cpu().contiguous().view(torch.int16).numpy().view(np.uint16)
+
+
+def host8(t: torch.Tensor) -> np.ndarray:
+    return t.detach().cpu().contiguous().view(torch.uint8).numpy()
+
+
+def _compare_set(kind: str, fmt: str) -> None:
+    ws, names = B.qwen3_8b_set(torch, DEV, SEED, kind)
+    blk = (128, 128) if fmt == "fp8_block" else (1, 32)
+    plan = QuantPlan(ws, fmt, blk)
+    outs = plan.run()
+    torch.cuda.synchronize()
+    say(fmt, kind, len(ws), "tensors quantized; comparing with the oracle")
+    for name, w, (codes, scales) in zip(names, ws, outs):
+        xb = host16(w)
+        if fmt == "fp8_block":
+            oc, osc = O.fp8_block_quant(xb, "bf16", "f32", blk, False, nthreads=THREADS)
+            assert np.array_equal(host8(codes), oc[0]), name
+            sc = scales.detach().cpu().numpy()
+            assert np.array_equal(sc.view(np.uint32), osc[0].view(np.uint32)), name
+        else:
+            oc, osc = O.mx_quant(xb, "bf16", 8 if fmt == "mxfp8" else 4, nthreads=THREADS)
+            assert np.array_equal(host8(codes).reshape(oc.shape), oc), name
+            assert np.array_equal(host8(scales).reshape(osc.shape), osc), name
+
+
+def test_c2_full_qwen3_8b_set_fp8_128x128_bit_exact():
+    _compare_set("normal", "fp8_block")
+
+
+def test_c4_full_qwen3_8b_set_mxfp8_bit_exact():
+    _compare_set("student_t", "mxfp8")
+
+
+def test_c5_full_qwen3_8b_set_mxfp4_bit_exact():
+    _compare_set("rowscale", "mxfp4")
+
+
+def _tile_amax(w: torch.Tensor) -> np.ndarray:
+    """Exact per-128x128-tile max |x| of an [E, R, C] bf16 stack, as float32."""
+    e, r, c = w.shape
+    a = w.view(e, r // 128, 128, c // 128, 128).abs().amax(dim=(2, 4))
+    return a.float().cpu().numpy()
+
+
+def test_c3_all_48_layers_experts():
+    tiny = np.float32(np.finfo(np.float32).tiny)
+    oracle_layers = {0, 23, 47}
+    for layer in range(48):
+        gu, dn = B.moe_layer(torch, DEV, SEED, layer)
+        plan = QuantPlan([gu, dn], "fp8_block", (128, 128))
+        outs = plan.run()
+        torch.cuda.synchronize()
+        for w, (codes, scales) in zip((gu, dn), outs):
+            amax = _tile_amax(w)
+            with np.errstate(over="ignore"):
+                want = np.maximum(amax / np.float32(448.0), tiny).astype(np.float32)
+            got = scales.detach().cpu().numpy()
+            assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), layer
+            e, r, c = w.shape
+            cm = codes.view(torch.uint8).view(e, r // 128, 128, c // 128, 128)
+            top = (cm & 0x7F).amax(dim=(2, 4)).cpu().numpy()
+            finite = np.isfinite(amax) & (amax > 0)
+            assert np.all(top[finite] == 0x7E), layer
+            assert np.all(top[amax == 0] == 0), layer
+            # the planted zero and inf tiles: their experts bit-exact with the oracle
+            special = sorted(set(np.nonzero(~finite)[0].tolist()))
+            for ex in special:
+                oc, osc = O.fp8_block_quant(host16(w[ex]), "bf16", "f32", (128, 128), False,
+                                            nthreads=THREADS)
+                assert np.array_equal(host8(codes[ex]), oc[0]), (layer, ex)
+                assert np.array_equal(got[ex].view(np.uint32), osc[0].view(np.uint32)), (layer, ex)
+            if layer in oracle_layers:
+                say("C3 layer", layer, "whole layer against the oracle")
+                oc, osc = O.fp8_block_quant(host16(w), "bf16", "f32", (128, 128), False,
+                                            nthreads=THREADS)
+                assert np.array_equal(host8(codes), oc), layer
+                assert np.array_equal(got.view(np.uint32), osc.view(np.uint32)), layer
+        del gu, dn, plan, outs
