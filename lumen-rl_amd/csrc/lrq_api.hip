@@ -50,9 +50,28 @@ struct GroupHeader {
 
 int64_t align_up(int64_t x, int64_t a) { return (x + a - 1) / a * a; }
 
+// Largest element offset the kernels' 64-bit index arithmetic is allowed to
+// reach (2^48 elements, far beyond any device's memory): extents whose
+// products pass it are rejected before they can wrap.
+constexpr int64_t kMaxElems = int64_t(1) << 48;
+
+bool span_ok(int64_t batch, int64_t rows, int64_t cols, int64_t ld, int64_t bstride) {
+  int64_t a, b, c;
+  if (batch < 0 || rows < 0 || cols < 0 || ld < 0 || bstride < 0) return false;
+  if (batch > kMaxElems || rows > kMaxElems || cols > kMaxElems || ld > kMaxElems || bstride > kMaxElems)
+    return false;
+  if (__builtin_mul_overflow(batch, rows, &a) || __builtin_mul_overflow(a, cols, &b) || b > kMaxElems)
+    return false;  // elements
+  if (__builtin_mul_overflow(rows, ld, &a) || a > kMaxElems) return false;  // one matrix's extent
+  if (batch > 1 && (__builtin_mul_overflow(batch - 1, bstride, &c) || c > kMaxElems - a)) return false;
+  return true;
+}
+
 // Fill a Desc from a tensor and check its shape.
 int make_desc(const lrq_tensor& t, Desc& d, bool need_codes = true) {
   if (t.batch < 0 || t.rows < 0 || t.cols < 0) return fail(LRQ_ERR_ARG, "negative extent");
+  if (!span_ok(t.batch, t.rows, t.cols, t.ld < t.cols ? t.cols : t.ld, t.batch > 1 ? t.batch_stride : 0))
+    return fail(LRQ_ERR_ARG, "extents exceed 2^48 elements");
   if (t.batch == 0 || t.rows == 0 || t.cols == 0) {
     memset(&d, 0, sizeof(d));
     d.batch = t.batch; d.rows = t.rows; d.cols = t.cols;
@@ -185,7 +204,9 @@ int mx_quant(int fmt, const void* in, int in_dtype, int64_t rows, int64_t cols, 
   g_err.clear();
   if (!valid_dtype(in_dtype)) return fail(LRQ_ERR_ARG, "bad input dtype %d", in_dtype);
   if (cols % 32 != 0) return fail(LRQ_ERR_ARG, "cols (%lld) must be a multiple of 32", (long long)cols);
-  lrq_tensor t{in, codes, scales, 1, rows, cols, ld, rows * ld};
+  int64_t mstride;
+  if (__builtin_mul_overflow(rows, ld, &mstride)) return fail(LRQ_ERR_ARG, "extents exceed 2^48 elements");
+  lrq_tensor t{in, codes, scales, 1, rows, cols, ld, mstride};
   Desc d;
   if (int rc = make_desc(t, d)) return rc;
   LaunchCfg cfg{};
@@ -317,7 +338,9 @@ int lrq_fp8_block_dequant(const uint8_t* codes, const void* scales, int scale_dt
                           int64_t blk_c, void* out, int out_dtype, lrq_stream_t stream) {
   g_err.clear();
   if (out_dtype != lrq::kF32 && out_dtype != lrq::kBF16) return fail(LRQ_ERR_ARG, "bad out dtype %d", out_dtype);
-  lrq_tensor t{codes, out, const_cast<void*>(scales), batch, rows, cols, cols, rows * cols};
+  int64_t mstride;
+  if (__builtin_mul_overflow(rows, cols, &mstride)) return fail(LRQ_ERR_ARG, "extents exceed 2^48 elements");
+  lrq_tensor t{codes, out, const_cast<void*>(scales), batch, rows, cols, cols, mstride};
   LaunchCfg cfg;
   Desc d;
   int64_t units;
@@ -347,6 +370,7 @@ int lrq_act_qdq(const void* in, int in_dtype, int64_t rows, int64_t cols, int64_
     return fail(LRQ_ERR_ARG, "activation block must be 32, 64, 128 or 256, got %lld", (long long)blk);
   if (rows < 0 || cols < 0 || cols % blk != 0)
     return fail(LRQ_ERR_ARG, "cols (%lld) must be a multiple of the block", (long long)cols);
+  if (!span_ok(1, rows, cols, ld < cols ? cols : ld, 0)) return fail(LRQ_ERR_ARG, "extents exceed 2^48 elements");
   if (rows == 0 || cols == 0) return 0;
   if (ld < cols) return fail(LRQ_ERR_ARG, "ld < cols");
   if (!in || !out) return fail(LRQ_ERR_ARG, "null pointer");

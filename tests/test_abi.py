@@ -188,6 +188,20 @@ def test_tensor_scale_tables():
     assert "empty" in _lib.last_error()
 
 
+def test_huge_extents_rejected_before_any_device_work():
+    big = ctypes.c_void_p(0x10000)
+    rc = L().lrq_fp8_block_quant(big, 0, 1, 1 << 40, 1 << 20, 1 << 20, 1 << 60, 128, 128, big, big, 0, None)
+    assert rc == _lib.ERR_ARG and "2^48" in _lib.last_error()
+    rc = L().lrq_fp8_block_quant(big, 0, 1 << 30, 4096, 4096, 4096, 4096 * 4096, 128, 128, big, big, 0, None)
+    assert rc == _lib.ERR_ARG
+    rc = L().lrq_fp8_block_dequant(big, big, 2, 1, 1 << 62, 1 << 4, 1, 128, big, 2, None)
+    assert rc == _lib.ERR_ARG
+    rc = L().lrq_mxfp8_quant(big, 0, 1 << 62, 64, 1 << 3, big, big, None)
+    assert rc == _lib.ERR_ARG
+    rc = L().lrq_act_qdq(big, 0, 1 << 40, 1 << 20, 1 << 20, 128, 0, big, None)
+    assert rc == _lib.ERR_ARG and "2^48" in _lib.last_error()
+
+
 def test_grouped_rejects_foreign_table():
     junk = np.zeros(4096, np.uint8)
     rc = L().lrq_quant_grouped(junk.ctypes.data, ctypes.c_void_p(0x1000), None)
