@@ -16,6 +16,9 @@ already resident in HBM:
   c2r: c2 weights with the reference's own 1x128 blocks (scales [N, K/128]).
   c2d: dequantize_state_dict of the c2r result: e4m3 codes + bf16 1x128 scales ->
        bf16 weights, ONE grouped launch.
+  c2sd: the drop-in WeightQuantizer.quantize_state_dict on the c2 weights held
+       in a device state dict (1x128 blocks, bf16 `_fp8_scales` sidecar, new
+       outputs every call): the API path end to end, host work included.
   kv:  FP8KVCacheQuantizer scale recalibration: max(|W|.max(), FLT_MIN)/448 over
        the 108 q/k/v_proj weights of Qwen3-8B (c2's values), one grouped
        amax launch + one per-tensor finishing launch.
@@ -56,7 +59,7 @@ PROFILE_FOR = {"c2": "k_tile128_qwen3_8b_fp8_128x128", "c2r": "k_row_qwen3_8b_fp
                "c5": "k_mx_qwen3_8b_mxfp4", "c2d": "k_dequant_qwen3_8b_fp8_1x128_to_bf16",
                "act": "k_act_qdq_qwen3_8b_prefill_8192", "kv": "k_amax_qwen3_8b_qkv_scales"}
 KERNEL_FOR = {"c1": "k_tile128", "c2": "k_tile128", "c3": "k_tile128", "c4": "k_mx", "c5": "k_mx",
-              "c2r": "k_row", "c2d": "k_dequant", "act": "k_act_qdq8", "kv": "k_amax"}
+              "c2r": "k_row", "c2d": "k_dequant", "act": "k_act_qdq8", "kv": "k_amax", "c2sd": "k_row"}
 PREFILL_TOKENS = 8192
 
 
@@ -130,7 +133,48 @@ def cpu_baseline(torch, ws, fmt, fmt_block, seconds):
     from oracle import torch_ref
 
     threads = max(1, min(os.cpu_count() or 1, 16))
-    torch.set_num_threads(threads)
+    prev = torch.get_num_threads()
+    try:
+        torch.set_num_threads(threads)
+        done_bytes, t_total, n = _cpu_pass(torch, O, torch_ref, np, ws, fmt, fmt_block, seconds, threads)
+        torch.set_num_threads(1)
+        one_bytes, one_t, one_n = _cpu_pass(torch, O, torch_ref, np, ws, fmt, fmt_block, seconds / 4, 1)
+    finally:
+        torch.set_num_threads(prev)
+    what = {
+        "fp8_block": (f"oracle/torch_ref.py (weight_quantizer.py op order on "
+                      f"{fmt_block[0]}x{fmt_block[1]} blocks, fp32 upcast first)"),
+        "fp8_dequant": "oracle/torch_ref.py (weight_quantizer.py:79-89 then the bf16 cast of :133)",
+        "act": "oracle/torch_ref.py (fp8_rollout.py:53-72 op order)",
+        "kv": "oracle/torch_ref.py (fp8_kv_cache.py:52-54 op order, one tensor at a time)",
+    }.get(fmt, f"the C oracle's {fmt} restatement (the reference has no MX CPU path)")
+    return {
+        "value": round(done_bytes / t_total / 1e9, 3),
+        "unit": "GB/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": (f"first {n} tensors of the same weight set ({done_bytes / 1e9:.2f} GB "
+                   f"algorithmic) through {what}, {threads} threads on {os.cpu_count()} "
+                   f"visible cores"),
+        "value_1thread": round(one_bytes / one_t / 1e9, 3),
+        "sample_1thread": f"first {one_n} tensors, 1 thread",
+        "cpu_model": _cpu_model(),
+    }
+
+
+def _cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def _cpu_pass(torch, O, torch_ref, np, ws, fmt, fmt_block, seconds, threads):
+    """Whole tensors through the CPU path until `seconds` of timed work."""
     done_bytes = 0
     n = 0
     t_total = 0.0
@@ -173,22 +217,19 @@ def cpu_baseline(torch, ws, fmt, fmt_block, seconds):
         n += 1
         if t_total >= seconds:
             break
-    what = {
-        "fp8_block": (f"oracle/torch_ref.py (weight_quantizer.py op order on "
-                      f"{fmt_block[0]}x{fmt_block[1]} blocks, fp32 upcast first)"),
-        "fp8_dequant": "oracle/torch_ref.py (weight_quantizer.py:79-89 then the bf16 cast of :133)",
-        "act": "oracle/torch_ref.py (fp8_rollout.py:53-72 op order)",
-        "kv": "oracle/torch_ref.py (fp8_kv_cache.py:52-54 op order, one tensor at a time)",
-    }.get(fmt, f"the C oracle's {fmt} restatement (the reference has no MX CPU path)")
-    return {
-        "value": round(done_bytes / t_total / 1e9, 3),
-        "unit": "GB/s",
-        "cores": threads,
-        "kind": "port",
-        "sample": (f"first {n} tensors of the same weight set ({done_bytes / 1e9:.2f} GB "
-                   f"algorithmic) through {what}, {threads} threads on {os.cpu_count()} "
-                   f"visible cores"),
-    }
+    return done_bytes, t_total, n
+
+
+class _StateDictCall:
+    """One drop-in quantize_state_dict call (plan, allocations and launch)."""
+
+    def __init__(self, wq, sd):
+        self.wq, self.sd = wq, sd
+        n = sum(w.numel() for w in sd.values())
+        self.algorithmic_bytes = n * 2 + n + (n // 128) * 2
+
+    def run(self):
+        self.out = self.wq.quantize_state_dict(self.sd)
 
 
 class _ActCall:
@@ -240,6 +281,16 @@ def run(args):
         cpu_ws, cpu_blk, cpu_fmt = ws, blk, fmt
         extra = {"tensors": len(ws), "layers": 36, "elements": sum(w.numel() for w in ws),
                  "format": fmt, "launches_per_step": 1}
+    elif cfg == "c2sd":
+        from lumenrl_amd.quantization import FP8Config, WeightQuantizer
+
+        ws, names = qwen3_8b_set(torch, dev, args.seed, "normal")
+        plans = [_StateDictCall(WeightQuantizer(FP8Config()), dict(zip(names, ws)))]
+        workload = "qwen3-8b-state-dict-quantize-fp8-1x128-dropin"
+        cpu_ws, cpu_blk, cpu_fmt = ws, (1, 128), "fp8_block"
+        extra = {"tensors": len(ws), "layers": 36, "elements": sum(w.numel() for w in ws),
+                 "format": "fp8_block_1x128_bf16_scales", "launches_per_step": 1,
+                 "host_work_timed": True}
     elif cfg == "kv":
         ws, names = qwen3_8b_set(torch, dev, args.seed, "normal")
         ws = [w for w, nm in zip(ws, names) if nm.split(".")[-1] in ("q_proj", "k_proj", "v_proj")]
@@ -318,6 +369,10 @@ def run(args):
     wall = time.perf_counter() - w0
     launch_ms = [a.elapsed_time(b) for a, b, _ in evs]
     launch_bytes = [nb for _, _, nb in evs]
+    per = len(plans)
+    step_ev_ms = sorted(sum(launch_ms[i * per:(i + 1) * per]) for i in range(args.steps))
+    median_step_ms = step_ev_ms[len(step_ev_ms) // 2] if len(step_ev_ms) % 2 else \
+        0.5 * (step_ev_ms[len(step_ev_ms) // 2 - 1] + step_ev_ms[len(step_ev_ms) // 2])
     kern_ms = sum(launch_ms) / len(launch_ms)
     achieved = sum(launch_bytes) / len(launch_bytes) / (kern_ms * 1e-3) / 1e9
     if flush is None:
@@ -346,6 +401,7 @@ def run(args):
         "steps": args.steps,
         "warmup": args.warmup,
         "ms_per_step": round(ms_per_step, 5),
+        "median_ms_per_step_events": round(median_step_ms, 5),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
@@ -396,7 +452,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--config", default="c2", choices=["c1", "c2", "c3", "c4", "c5", "c2r", "c2d", "act", "kv"])
+    ap.add_argument("--config", default="c2", choices=["c1", "c2", "c3", "c4", "c5", "c2r", "c2d", "c2sd", "act", "kv"])
     ap.add_argument("--seed", type=int, default=1000)
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
