@@ -461,7 +461,8 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU: the quantize path is per-device with no "
-              "collectives (see DESIGN.md for how it shards); run with --gpus 1", file=sys.stderr)
+              "collectives (each rank would quantize its own shard); run with --gpus 1",
+              file=sys.stderr)
         sys.exit(2)
     if args.mode == "copy":
         run_copy(args)
