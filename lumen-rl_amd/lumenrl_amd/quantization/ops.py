@@ -91,6 +91,8 @@ def fp8_block_quant(x: Tensor, block: tuple[int, int], *, native_arith: bool = F
     ``_fp8_scales`` sidecar, :111).
     """
     _check_input(x, "fp8_block_quant")
+    if x.dim() < 1:
+        raise ValueError("fp8_block_quant expects a tensor with at least one dimension")
     br, bc = int(block[0]), int(block[1])
     if br < 1 or bc < 1:
         raise ValueError(f"block must be positive, got {block}")
@@ -128,8 +130,8 @@ def fp8_block_dequant(codes: Tensor, scales: Tensor, block: tuple[int, int],
     """fp32(code) * fp32(scale) per block; ``out_dtype`` float32 or bfloat16."""
     if codes.dtype not in (torch.float8_e4m3fn, torch.uint8):
         raise TypeError(f"codes must be float8_e4m3fn, got {codes.dtype}")
-    if not codes.is_cuda or not scales.is_cuda:
-        raise ValueError("fp8_block_dequant expects HIP device tensors")
+    if not codes.is_cuda or not scales.is_cuda or codes.device != scales.device:
+        raise ValueError("fp8_block_dequant expects codes and scales on the same HIP device")
     if scales.dtype not in _IN_DTYPES:
         scales = scales.to(torch.float32)
     if out_dtype not in (torch.float32, torch.bfloat16):

@@ -175,7 +175,7 @@ class WeightQuantizer:
         writes bf16 directly (fp32 product, then the bf16 cast of :133).
         """
         consumed_suffixes = {"_fp8_scales", "_fp8_meta"}
-        todo: dict[str, tuple[Tensor, Tensor, torch.device | None]] = {}
+        pending: dict[str, tuple[Tensor, Tensor, torch.device | None]] = {}
         for key, value in state_dict.items():
             if any(key.endswith(sfx) for sfx in consumed_suffixes) or not isinstance(value, Tensor):
                 continue
@@ -190,27 +190,27 @@ class WeightQuantizer:
             leading = 1
             for d in value.shape[:-1]:
                 leading *= int(d)
-            todo[key] = (q.contiguous().reshape(leading, last),
+            pending[key] = (q.contiguous().reshape(leading, last),
                          s.contiguous().reshape(leading, last // 128), home)
         results: dict[str, Tensor] = {}
         groups: dict[tuple[torch.dtype, torch.device], list[str]] = {}
-        for key, (q, s, _) in todo.items():
+        for key, (q, s, _) in pending.items():
             if q.numel() > 0 and q.data_ptr() % 16 == 0:
                 groups.setdefault((s.dtype, q.device), []).append(key)
             else:
                 results[key] = ops.fp8_block_dequant(q, s, (1, 128), torch.bfloat16)
         for keys in groups.values():
-            plan = ops.DequantPlan([todo[k][:2] for k in keys], (1, 128), torch.bfloat16)
+            plan = ops.DequantPlan([pending[k][:2] for k in keys], (1, 128), torch.bfloat16)
             results.update(zip(keys, plan.run()))
 
         out: dict[str, Tensor | Any] = {}
         for key, value in state_dict.items():
             if any(key.endswith(sfx) for sfx in consumed_suffixes):
                 continue
-            if key not in todo:
+            if key not in pending:
                 out[key] = value
                 continue
             dq = results[key].reshape(value.shape)
-            home = todo[key][2]
+            home = pending[key][2]
             out[key] = dq.to(home) if home is not None else dq
         return out
