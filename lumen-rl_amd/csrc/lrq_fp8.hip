@@ -120,14 +120,19 @@ __device__ __forceinline__ void store_scale(void* scales, int64_t idx, float s, 
 }
 
 // ---------------------------------------------------------------------------
-// 128x128 tiles.  Thread t owns column chunk (t & 15) of rows (t >> 4) + 16i,
-// i = 0..7: each load instruction of a wave reads 4 full 256-byte rows.
+// 128x128 tiles, T threads per tile.  Thread t owns column chunk (t & 15) of
+// rows (t >> 4) + (T/16) i: each load instruction of a wave reads 4 full
+// 256-byte rows.  T = 256 (8 loads per thread) for large launches; T = 512 (4
+// loads) when the whole launch fits in one wave of work-groups, where the
+// shorter per-thread chain lowers the latency of a single weight by ~5%.
 // ---------------------------------------------------------------------------
-template <int DT, int CDT>
-__global__ __launch_bounds__(256) void k_tile128(Desc single, const Desc* __restrict__ descs,
-                                                 const uint32_t* __restrict__ map, int pow2,
-                                                 int scale_bf16) {
-  __shared__ uint32_t red[4];
+template <int DT, int CDT, int T>
+__global__ __launch_bounds__(T) void k_tile128(Desc single, const Desc* __restrict__ descs,
+                                               const uint32_t* __restrict__ map, int pow2,
+                                               int scale_bf16) {
+  constexpr int NL = 2048 / T;  // 16-byte chunks per thread
+  constexpr int RS = T / 16;    // rows between a thread's chunks
+  __shared__ uint32_t red[T / 64];
   Desc d;
   int64_t u;
   pick_desc(single, descs, map, d, u);
@@ -146,14 +151,14 @@ __global__ __launch_bounds__(256) void k_tile128(Desc single, const Desc* __rest
   const bool full = (r0 + 128 <= d.rows) && (c0 + 128 <= d.cols);
   const bool col_ok = col < d.cols;
 
-  Chunk<DT> ch[8];
+  Chunk<DT> ch[NL];
   if (full) {
 #pragma unroll
-    for (int i = 0; i < 8; ++i) load_chunk<DT>(ch[i], d.in, in_base + (int64_t)(16 * i) * d.ld);
+    for (int i = 0; i < NL; ++i) load_chunk<DT>(ch[i], d.in, in_base + (int64_t)(RS * i) * d.ld);
   } else {
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      if (col_ok && r0 + rr + 16 * i < d.rows) load_chunk<DT>(ch[i], d.in, in_base + (int64_t)(16 * i) * d.ld);
+    for (int i = 0; i < NL; ++i) {
+      if (col_ok && r0 + rr + RS * i < d.rows) load_chunk<DT>(ch[i], d.in, in_base + (int64_t)(RS * i) * d.ld);
       else zero_chunk<DT>(ch[i]);
     }
   }
@@ -161,26 +166,29 @@ __global__ __launch_bounds__(256) void k_tile128(Desc single, const Desc* __rest
   Amax<DT> am;
   am.init();
 #pragma unroll
-  for (int i = 0; i < 8; ++i) am.add(ch[i]);
+  for (int i = 0; i < NL; ++i) am.add(ch[i]);
   uint32_t a = wave_max(am.bits());
   if ((tid & 63) == 0) red[tid >> 6] = a;
   __syncthreads();
   a = red[0];
-  a = red[1] > a ? red[1] : a;
-  a = red[2] > a ? red[2] : a;
-  a = red[3] > a ? red[3] : a;
+#pragma unroll
+  for (int w = 1; w < T / 64; ++w) a = red[w] > a ? red[w] : a;
   a = __builtin_amdgcn_readfirstlane(a);  // tile-uniform: scalar scale math
 
   const BlockScale bs = block_scale<CDT>(a, pow2 != 0);
   if (tid == 0) store_scale<CDT>(d.scales, u, bs.s, scale_bf16);
 
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
+  for (int i = 0; i < NL; ++i) {
     const v2u q = encode_chunk<DT, CDT>(ch[i], bs);
-    if (full || (col_ok && r0 + rr + 16 * i < d.rows))
-      store_nt(d.codes + out_base + (int64_t)(16 * i) * d.cols, q);
+    if (full || (col_ok && r0 + rr + RS * i < d.rows))
+      store_nt(d.codes + out_base + (int64_t)(RS * i) * d.cols, q);
   }
 }
+
+// Launches of at most this many tiles run one wave of 512-thread work-groups
+// (two per CU on 256 CUs, fewer loads per thread).
+constexpr int64_t kSmallTileLaunch = 2048;
 
 // ---------------------------------------------------------------------------
 // 1xB row blocks (B = 8*LPB, LPB = 4..64 lanes per block).  The 64 lanes of a
@@ -317,8 +325,12 @@ static hipError_t launch_fp8_typed(const LaunchCfg& cfg, const Desc& single, con
   const dim3 grid((unsigned)units), block(256);
   switch (cfg.kernel) {
     case kKernTile128:
-      hipLaunchKernelGGL((k_tile128<DT, CDT>), grid, block, 0, stream, single, descs, map,
-                         cfg.pow2, cfg.scale_bf16);
+      if (units <= kSmallTileLaunch)
+        hipLaunchKernelGGL((k_tile128<DT, CDT, 512>), grid, dim3(512), 0, stream, single, descs, map,
+                           cfg.pow2, cfg.scale_bf16);
+      else
+        hipLaunchKernelGGL((k_tile128<DT, CDT, 256>), grid, block, 0, stream, single, descs, map,
+                           cfg.pow2, cfg.scale_bf16);
       break;
     case kKernRowQuad:
       switch (cfg.blk_c) {
