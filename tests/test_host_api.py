@@ -86,3 +86,59 @@ def test_state_dict_passthrough_rules_without_device():
     assert list(out) == list(sd)
     for k in sd:
         assert out[k] is sd[k]
+
+
+# matrix_view: the stride analysis every launch relies on (CPU tensors, no device)
+from hypothesis import given, settings, strategies as st  # noqa: E402
+
+from lumenrl_amd.quantization.ops import matrix_view  # noqa: E402
+
+
+@st.composite
+def _views(draw):
+    """Random views of a random buffer: slices, steps, transposes, expands, 1-3 dims."""
+    ndim = draw(st.integers(1, 3))
+    shape = [draw(st.integers(1, 9)) for _ in range(ndim)]
+    base = torch.arange(1, 1 + 4 * 9 * 9 * 9, dtype=torch.float32)
+    pads = [draw(st.integers(0, 3)) for _ in range(ndim)]
+    full = [s + p for s, p in zip(shape, pads)]
+    t = base[: int(torch.tensor(full).prod())].view(*full)
+    idx = tuple(slice(draw(st.integers(0, p)), None) for p in pads)
+    t = t[idx]
+    t = t[tuple(slice(0, s) for s in shape)]
+    if ndim >= 2 and draw(st.booleans()):
+        t = t.transpose(-1, -2)
+    if draw(st.booleans()):
+        t = t.unsqueeze(0).expand(draw(st.integers(1, 3)), *t.shape)
+    return t
+
+
+@settings(max_examples=300, deadline=None)
+@given(_views())
+def test_matrix_view_addresses_exactly_the_tensor(t):
+    xb, batch, rows, cols, ld, bstride = matrix_view(t)
+    want = t.reshape(-1, t.shape[-1])
+    lead = 1
+    for d in t.shape[:-2]:
+        lead *= d
+    assert (batch, rows, cols) == (lead, t.shape[-2] if t.dim() >= 2 else 1, t.shape[-1])
+    # rebuild every element from (pointer, batch, rows, cols, ld, bstride) over xb's storage
+    flat = xb.reshape(-1) if xb.data_ptr() != t.data_ptr() else None
+    esz = t.element_size()
+    got = torch.empty(batch, rows, cols)
+    if flat is None:
+        # in place: offsets relative to t's first element inside its storage
+        storage = torch.as_strided(t, (t.untyped_storage().nbytes() // esz - t.storage_offset(),), (1,))
+        assert cols == 1 or xb.stride(-1) == 1
+        for b in range(batch):
+            for r in range(rows):
+                o = b * bstride + r * ld
+                got[b, r] = storage[o:o + cols]
+    else:
+        # a dense copy: ld == cols, bstride == rows * cols
+        assert ld == cols and bstride == rows * cols
+        got = flat.view(batch, rows, cols)
+    assert torch.equal(got.reshape(-1, cols), want.reshape(-1, cols))
+    # matrices never overlap and rows never overlap
+    assert rows == 1 or ld >= cols
+    assert batch == 1 or bstride >= (rows - 1) * ld + cols
