@@ -153,7 +153,7 @@ def test_group_pack_rejects_mixed_kernels_and_small_buffers():
 
 
 def test_tensor_scale_tables():
-    """Per-tensor scale tables: 32 KiB units (16-byte loads) or 8192-element units
+    """Per-tensor scale tables: 16 KiB units (16-byte loads) or 8192-element units
     (element walk) in one table, no codes pointer, workspace of 4 B per unit."""
     qkv = [(1, 4096, 4096), (1, 1024, 4096), (1, 1024, 4096)]
     ts = _tensors(qkv + [(1, 300, 100)])
@@ -165,7 +165,7 @@ def test_tensor_scale_tables():
     assert need > 0, _lib.last_error()
     buf = np.zeros(need, np.uint8)
     assert L().lrq_group_pack(fmt, ts, 4, 0, 1, 1, 0, buf.ctypes.data, need) == 0, _lib.last_error()
-    units = [4096 * 4096 // 16384, 1024 * 4096 // 16384, 1024 * 4096 // 16384, -(-300 * 100 // 8192)]
+    units = [4096 * 4096 // 8192, 1024 * 4096 // 8192, 1024 * 4096 // 8192, -(-300 * 100 // 8192)]
     assert L().lrq_group_units(buf.ctypes.data) == sum(units)
     assert L().lrq_group_workspace_bytes(buf.ctypes.data) == 4 * sum(units)
     wmap = buf[-4 * sum(units):].view(np.uint32)
