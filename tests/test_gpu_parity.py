@@ -501,7 +501,7 @@ def test_grouped_dequant_plan_matches_oracle():
         assert np.array_equal(o.cpu().view(torch.int16).numpy().view(np.uint16), want)
 
 
-@pytest.mark.parametrize("fmt", ["fp8_block", "mxfp4"])
+@pytest.mark.parametrize("fmt", ["fp8_block", "mxfp8", "mxfp4"])
 def test_bucket_writer_matches_oracle(fmt):
     from lumenrl_amd.quantization import QuantizedBucketWriter
 
@@ -535,7 +535,7 @@ def test_bucket_writer_matches_oracle(fmt):
                 got = u8(t) if name == base else scale_bits(t)
                 assert np.array_equal(got.reshape(-1), (want if name == base else want.view(np.uint32)).reshape(-1))
             else:
-                oc, osc = O.mx_quant(xh.reshape(-1, xh.shape[-1]), "bf16", 4)
+                oc, osc = O.mx_quant(xh.reshape(-1, xh.shape[-1]), "bf16", 8 if fmt == "mxfp8" else 4)
                 want = oc if name == base else osc
                 assert np.array_equal(u8(t).reshape(-1), want.reshape(-1))
     assert seen == {n for n, _ in named} | {n + "_scale_inv" for n, _ in named
