@@ -1,0 +1,222 @@
+// A C/C++ caller of liblrq with no torch: device buffers from hipMalloc, the
+// grouped table packed on the host and uploaded by hand, every result compared
+// byte for byte with the CPU oracle (oracle/lrq_oracle.c, test infrastructure).
+// Prints one line per check and "c-abi ok" at the end; exits non-zero on the
+// first mismatch or error.
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+
+#include <vector>
+
+#include "lrq.h"
+
+extern "C" {
+int lrqo_fp8_block_quant(const void* in, int in_dtype, int arith, int64_t batch, int64_t rows,
+                         int64_t cols, int64_t ld, int64_t bstride, int64_t blk_r, int64_t blk_c,
+                         int pow2, uint8_t* codes, void* scales, int nthreads);
+int lrqo_mx_quant(const void* in, int in_dtype, int64_t rows, int64_t cols, int64_t ld, int fmt,
+                  uint8_t* codes, uint8_t* scales, int nthreads);
+int lrqo_act_qdq(const void* in, int in_dtype, int64_t rows, int64_t cols, int64_t blk, int pow2,
+                 float* out, int nthreads);
+uint32_t lrqo_tensor_scale(const void* in, int in_dtype, int64_t n);
+}
+
+#define HIP(x)                                                                  \
+  do {                                                                          \
+    hipError_t e_ = (x);                                                        \
+    if (e_ != hipSuccess) {                                                     \
+      fprintf(stderr, "HIP error %s at line %d\n", hipGetErrorString(e_), __LINE__); \
+      exit(2);                                                                  \
+    }                                                                           \
+  } while (0)
+#define LRQ(x)                                                                  \
+  do {                                                                          \
+    int r_ = (x);                                                               \
+    if (r_ != 0) {                                                              \
+      fprintf(stderr, "lrq error %d at line %d: %s\n", r_, __LINE__, lrq_last_error()); \
+      exit(3);                                                                  \
+    }                                                                           \
+  } while (0)
+
+static void expect(bool ok, const char* what) {
+  printf("%-44s %s\n", what, ok ? "ok" : "MISMATCH");
+  fflush(stdout);
+  if (!ok) exit(1);
+}
+
+// Seeded bf16 weights: N(0, 0.02^2)-like values with a few outliers and one
+// all-zero 128x128 tile.
+static std::vector<uint16_t> make_weights(int64_t rows, int64_t cols, uint32_t seed) {
+  std::vector<uint16_t> w((size_t)(rows * cols));
+  uint32_t s = seed;
+  for (size_t i = 0; i < w.size(); ++i) {
+    float acc = 0.0f;
+    for (int k = 0; k < 4; ++k) {
+      s = s * 1664525u + 1013904223u;
+      acc += (float)(s >> 8) / 16777216.0f - 0.5f;
+    }
+    float f = acc * 0.035f;
+    if ((s & 1023u) == 7u) f *= 80.0f;
+    uint32_t b;
+    memcpy(&b, &f, 4);
+    w[i] = (uint16_t)((b + 0x7FFFu + ((b >> 16) & 1u)) >> 16);
+  }
+  for (int64_t r = 0; r < 128 && r < rows; ++r)
+    for (int64_t c = 0; c < 128 && c < cols; ++c) w[(size_t)(r * cols + c)] = 0;
+  return w;
+}
+
+int main() {
+  int ndev = 0;
+  HIP(hipGetDeviceCount(&ndev));
+  if (ndev < 1) {
+    fprintf(stderr, "no HIP device\n");
+    return 4;
+  }
+  printf("%s\n", lrq_version());
+  hipStream_t st;
+  HIP(hipStreamCreate(&st));
+
+  // two weights of one layer: [512, 1024] and [256, 3072]
+  const int64_t R[2] = {512, 256}, C[2] = {1024, 3072};
+  std::vector<uint16_t> hw[2] = {make_weights(R[0], C[0], 1u), make_weights(R[1], C[1], 2u)};
+  void* dw[2];
+  uint8_t* dcodes[2];
+  float* dscales[2];
+  for (int i = 0; i < 2; ++i) {
+    HIP(hipMalloc(&dw[i], hw[i].size() * 2));
+    HIP(hipMemcpy(dw[i], hw[i].data(), hw[i].size() * 2, hipMemcpyHostToDevice));
+    HIP(hipMalloc(&dcodes[i], (size_t)(R[i] * C[i])));
+    HIP(hipMalloc(&dscales[i], (size_t)(R[i] * C[i] / 128) * 4));
+  }
+
+  // 1. single tensor, 128x128 tiles and 1x128 rows
+  for (int blk_r : {128, 1}) {
+    const int64_t ns = (R[0] / blk_r) * (C[0] / 128);
+    LRQ(lrq_fp8_block_quant(dw[0], LRQ_DTYPE_BF16, 1, R[0], C[0], C[0], R[0] * C[0], blk_r, 128,
+                            dcodes[0], dscales[0], 0, (lrq_stream_t)st));
+    HIP(hipStreamSynchronize(st));
+    std::vector<uint8_t> got((size_t)(R[0] * C[0])), want(got.size());
+    std::vector<float> gs((size_t)ns), ws(gs.size());
+    HIP(hipMemcpy(got.data(), dcodes[0], got.size(), hipMemcpyDeviceToHost));
+    HIP(hipMemcpy(gs.data(), dscales[0], gs.size() * 4, hipMemcpyDeviceToHost));
+    lrqo_fp8_block_quant(hw[0].data(), LRQ_DTYPE_BF16, 0, 1, R[0], C[0], C[0], R[0] * C[0], blk_r, 128,
+                         0, want.data(), ws.data(), 0);
+    expect(got == want && memcmp(gs.data(), ws.data(), gs.size() * 4) == 0,
+           blk_r == 128 ? "lrq_fp8_block_quant 128x128" : "lrq_fp8_block_quant 1x128");
+  }
+
+  // 2. grouped: both tensors in one launch through a hand-uploaded table
+  lrq_tensor ts[2];
+  for (int i = 0; i < 2; ++i) {
+    ts[i].in = dw[i];
+    ts[i].codes = dcodes[i];
+    ts[i].scales = dscales[i];
+    ts[i].batch = 1;
+    ts[i].rows = R[i];
+    ts[i].cols = C[i];
+    ts[i].ld = C[i];
+    ts[i].batch_stride = R[i] * C[i];
+  }
+  const int64_t bytes = lrq_group_table_bytes(LRQ_FMT_FP8_BLOCK, ts, 2, LRQ_DTYPE_BF16, 128, 128, 0);
+  if (bytes <= 0) LRQ((int)bytes);
+  std::vector<uint8_t> host_table((size_t)bytes);
+  LRQ(lrq_group_pack(LRQ_FMT_FP8_BLOCK, ts, 2, LRQ_DTYPE_BF16, 128, 128, 0, host_table.data(), bytes));
+  void* dev_table;
+  HIP(hipMalloc(&dev_table, (size_t)bytes));
+  HIP(hipMemcpy(dev_table, host_table.data(), (size_t)bytes, hipMemcpyHostToDevice));
+  for (int i = 0; i < 2; ++i) HIP(hipMemset(dcodes[i], 0xAB, (size_t)(R[i] * C[i])));
+  LRQ(lrq_quant_grouped(host_table.data(), dev_table, (lrq_stream_t)st));
+  HIP(hipStreamSynchronize(st));
+  bool same = lrq_group_units(host_table.data()) == (R[0] / 128) * (C[0] / 128) + (R[1] / 128) * (C[1] / 128);
+  for (int i = 0; i < 2; ++i) {
+    const int64_t ns = (R[i] / 128) * (C[i] / 128);
+    std::vector<uint8_t> got((size_t)(R[i] * C[i])), want(got.size());
+    std::vector<float> gs((size_t)ns), ws(gs.size());
+    HIP(hipMemcpy(got.data(), dcodes[i], got.size(), hipMemcpyDeviceToHost));
+    HIP(hipMemcpy(gs.data(), dscales[i], gs.size() * 4, hipMemcpyDeviceToHost));
+    lrqo_fp8_block_quant(hw[i].data(), LRQ_DTYPE_BF16, 0, 1, R[i], C[i], C[i], R[i] * C[i], 128, 128, 0,
+                         want.data(), ws.data(), 0);
+    same = same && got == want && memcmp(gs.data(), ws.data(), gs.size() * 4) == 0;
+  }
+  expect(same, "lrq_group_pack + lrq_quant_grouped (2 tensors)");
+
+  // 3. MXFP8 / MXFP4 of tensor 1
+  for (int fmt : {8, 4}) {
+    const int64_t cb = fmt == 8 ? R[1] * C[1] : R[1] * C[1] / 2;
+    uint8_t* dsc;
+    HIP(hipMalloc(&dsc, (size_t)(R[1] * C[1] / 32)));
+    if (fmt == 8) LRQ(lrq_mxfp8_quant(dw[1], LRQ_DTYPE_BF16, R[1], C[1], C[1], dcodes[1], dsc, (lrq_stream_t)st));
+    else LRQ(lrq_mxfp4_quant(dw[1], LRQ_DTYPE_BF16, R[1], C[1], C[1], dcodes[1], dsc, (lrq_stream_t)st));
+    HIP(hipStreamSynchronize(st));
+    std::vector<uint8_t> got((size_t)cb), want(got.size()), gs((size_t)(R[1] * C[1] / 32)), ws(gs.size());
+    HIP(hipMemcpy(got.data(), dcodes[1], got.size(), hipMemcpyDeviceToHost));
+    HIP(hipMemcpy(gs.data(), dsc, gs.size(), hipMemcpyDeviceToHost));
+    lrqo_mx_quant(hw[1].data(), LRQ_DTYPE_BF16, R[1], C[1], C[1], fmt, want.data(), ws.data(), 0);
+    expect(got == want && gs == ws, fmt == 8 ? "lrq_mxfp8_quant" : "lrq_mxfp4_quant");
+    HIP(hipFree(dsc));
+  }
+
+  // 4. activation fake-quant of tensor 0 viewed as 512 tokens x 1024
+  {
+    float* dout;
+    HIP(hipMalloc(&dout, (size_t)(R[0] * C[0]) * 4));
+    LRQ(lrq_act_qdq(dw[0], LRQ_DTYPE_BF16, R[0], C[0], C[0], 128, 0, dout, (lrq_stream_t)st));
+    HIP(hipStreamSynchronize(st));
+    std::vector<float> got((size_t)(R[0] * C[0])), want(got.size());
+    HIP(hipMemcpy(got.data(), dout, got.size() * 4, hipMemcpyDeviceToHost));
+    lrqo_act_qdq(hw[0].data(), LRQ_DTYPE_BF16, R[0], C[0], 128, 0, want.data(), 0);
+    expect(memcmp(got.data(), want.data(), got.size() * 4) == 0, "lrq_act_qdq");
+    HIP(hipFree(dout));
+  }
+
+  // 5. per-tensor scales of both tensors with a caller workspace
+  {
+    float* dsc;
+    HIP(hipMalloc(&dsc, 2 * sizeof(float)));
+    lrq_tensor tt[2] = {ts[0], ts[1]};
+    tt[0].codes = tt[1].codes = nullptr;
+    tt[0].scales = dsc;
+    tt[1].scales = dsc + 1;
+    const int64_t tb = lrq_group_table_bytes(LRQ_FMT_TENSOR_SCALE, tt, 2, LRQ_DTYPE_BF16, 1, 1, 0);
+    if (tb <= 0) LRQ((int)tb);
+    std::vector<uint8_t> ht((size_t)tb);
+    LRQ(lrq_group_pack(LRQ_FMT_TENSOR_SCALE, tt, 2, LRQ_DTYPE_BF16, 1, 1, 0, ht.data(), tb));
+    void* dt;
+    HIP(hipMalloc(&dt, (size_t)tb));
+    HIP(hipMemcpy(dt, ht.data(), (size_t)tb, hipMemcpyHostToDevice));
+    const int64_t wsb = lrq_group_workspace_bytes(ht.data());
+    void* dws;
+    HIP(hipMalloc(&dws, (size_t)wsb));
+    LRQ(lrq_tensor_scale_grouped(ht.data(), dt, dws, wsb, (lrq_stream_t)st));
+    HIP(hipStreamSynchronize(st));
+    uint32_t got[2];
+    HIP(hipMemcpy(got, dsc, sizeof(got), hipMemcpyDeviceToHost));
+    const bool ok = got[0] == lrqo_tensor_scale(hw[0].data(), LRQ_DTYPE_BF16, R[0] * C[0]) &&
+                    got[1] == lrqo_tensor_scale(hw[1].data(), LRQ_DTYPE_BF16, R[1] * C[1]);
+    expect(ok, "lrq_tensor_scale_grouped");
+    HIP(hipFree(dws));
+    HIP(hipFree(dt));
+    HIP(hipFree(dsc));
+  }
+
+  // 6. argument errors come back as codes with a message, not as faults
+  {
+    const int rc = lrq_fp8_block_quant(dw[0], LRQ_DTYPE_BF16, 1, R[0], C[0], C[0] - 1, R[0] * C[0], 128, 128,
+                                       dcodes[0], dscales[0], 0, (lrq_stream_t)st);
+    expect(rc == LRQ_ERR_ARG && strlen(lrq_last_error()) > 0, "ld < cols rejected with LRQ_ERR_ARG");
+  }
+
+  HIP(hipFree(dev_table));
+  for (int i = 0; i < 2; ++i) {
+    HIP(hipFree(dw[i]));
+    HIP(hipFree(dcodes[i]));
+    HIP(hipFree(dscales[i]));
+  }
+  HIP(hipStreamDestroy(st));
+  printf("c-abi ok\n");
+  return 0;
+}

@@ -202,6 +202,19 @@ def test_huge_extents_rejected_before_any_device_work():
     assert rc == _lib.ERR_ARG and "2^48" in _lib.last_error()
 
 
+def test_c_caller_is_built_against_the_in_tree_libraries():
+    import subprocess
+
+    from conftest import ROOT
+
+    binary = os.path.join(ROOT, "tests", "c_abi", "_build", "test_abi_c")
+    if not os.path.exists(binary):
+        pytest.skip("tests/c_abi not built (run __graft_entry__.build())")
+    deps = subprocess.run(["ldd", binary], capture_output=True, text=True).stdout
+    assert "lumen-rl_amd/lumenrl_amd/liblrq.so" in deps
+    assert "oracle/_build/liblrq_oracle.so" in deps
+
+
 def test_grouped_rejects_foreign_table():
     junk = np.zeros(4096, np.uint8)
     rc = L().lrq_quant_grouped(junk.ctypes.data, ctypes.c_void_p(0x1000), None)
