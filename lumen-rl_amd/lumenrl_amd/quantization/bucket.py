@@ -92,6 +92,60 @@ class Bucket:
         return out
 
 
+class BucketLayout:
+    """Where every entry of one bucket goes: (name, shape, dtype, offset, nbytes)
+    per entry, codes and ``<name><scale_suffix>`` scales for quantized weights."""
+
+    def __init__(self) -> None:
+        self.items: list[tuple[str, bool]] = []       # (weight name, quantized)
+        self.entries: list[_Entry] = []
+        self.nbytes = 0
+
+
+def entry_sizes(shape: tuple, dtype: torch.dtype, quantized: bool, fmt: str,
+                block_size: tuple[int, int]) -> list[tuple[tuple, torch.dtype, int]]:
+    """(shape, dtype, bytes) of the entries one weight occupies in a bucket."""
+    if not quantized:
+        return [(tuple(shape), dtype, _prod(shape) * torch.empty((), dtype=dtype).element_size())]
+    shape = tuple(shape)
+    *lead, rows, cols = shape if len(shape) >= 2 else (1,) + shape
+    lead = tuple(lead)
+    if fmt == "fp8_block":
+        br, bc = block_size
+        sshape = lead + (-(-rows // br), -(-cols // bc))
+        return [(shape, torch.float8_e4m3fn, _prod(shape)), (sshape, torch.float32, 4 * _prod(sshape))]
+    cshape = shape if fmt == "mxfp8" else lead + (rows, cols // 2)
+    ctype = torch.float8_e4m3fn if fmt == "mxfp8" else torch.uint8
+    sshape = lead + (rows, cols // 32)
+    return [(cshape, ctype, _prod(cshape)), (sshape, torch.uint8, _prod(sshape))]
+
+
+def plan_layout(weights: Sequence[tuple[str, tuple, torch.dtype, bool]], bucket_bytes: int,
+                fmt: str = "fp8_block", block_size: tuple[int, int] = (128, 128),
+                scale_suffix: str = "_scale_inv") -> list[BucketLayout]:
+    """Split (name, shape, dtype, quantized) weights, in order, into buckets of at
+    most ``bucket_bytes``; every entry starts on a 256-byte boundary.  Pure host
+    arithmetic (no device), shared by :class:`QuantizedBucketWriter`."""
+    layouts: list[BucketLayout] = []
+    cur = BucketLayout()
+    for name, shape, dtype, q in weights:
+        sizes = entry_sizes(shape, dtype, q, fmt, block_size)
+        need = sum(_align(n) for _, _, n in sizes)
+        if need > bucket_bytes:
+            raise ValueError(f"{name} needs {need} bytes, more than the bucket ({bucket_bytes})")
+        if cur.items and cur.nbytes + need > bucket_bytes:
+            layouts.append(cur)
+            cur = BucketLayout()
+        names = [name] if not q else [name, name + scale_suffix]
+        for nm, (eshape, edt, n) in zip(names, sizes):
+            cur.entries.append(_Entry(nm, eshape, edt, cur.nbytes, n))
+            cur.nbytes += _align(n)
+        cur.items.append((name, q))
+    if cur.items:
+        layouts.append(cur)
+    return layouts
+
+
 class QuantizedBucketWriter:
     """Plans buckets over a fixed list of named weights and fills them on demand.
 
@@ -120,71 +174,33 @@ class QuantizedBucketWriter:
         self.scale_suffix = scale_suffix
         self.fmt = fmt
         self.block_size = block_size
-        self.buckets: list[Bucket] = []
-
-        cur: list[tuple[str, Tensor, bool]] = []
-        used = 0
+        src = dict(named_weights)
         for name, w in named_weights:
-            q = quantize_if(name, w)
-            need = self._footprint(w, q)
-            if need > self.bucket_bytes:
-                raise ValueError(f"{name} needs {need} bytes, more than the bucket ({self.bucket_bytes})")
-            if used + need > self.bucket_bytes and cur:
-                self.buckets.append(self._plan(cur))
-                cur, used = [], 0
-            cur.append((name, w, q))
-            used += need
-        if cur:
-            self.buckets.append(self._plan(cur))
-
-    # bytes a tensor occupies in a bucket, each entry padded to _ALIGN
-    def _sizes(self, w: Tensor, q: bool) -> list[tuple[tuple, torch.dtype, int]]:
-        if not q:
-            return [(tuple(w.shape), w.dtype, w.numel() * w.element_size())]
-        *lead, rows, cols = w.shape if w.dim() >= 2 else (1,) + tuple(w.shape)
-        lead = tuple(lead)
-        if self.fmt == "fp8_block":
-            br, bc = self.block_size
-            sshape = lead + (-(-rows // br), -(-cols // bc))
-            return [(tuple(w.shape), torch.float8_e4m3fn, w.numel()),
-                    (sshape, torch.float32, 4 * _prod(sshape))]
-        cshape = tuple(w.shape) if self.fmt == "mxfp8" else lead + (rows, cols // 2)
-        ctype = torch.float8_e4m3fn if self.fmt == "mxfp8" else torch.uint8
-        sshape = lead + (rows, cols // 32)
-        return [(cshape, ctype, _prod(cshape)), (sshape, torch.uint8, _prod(sshape))]
-
-    def _footprint(self, w: Tensor, q: bool) -> int:
-        return sum(_align(n) for _, _, n in self._sizes(w, q))
-
-    def _plan(self, items: list[tuple[str, Tensor, bool]]) -> Bucket:
-        entries, copies, qin, qout = [], [], [], []
-        off = 0
-        for name, w, q in items:
-            sizes = self._sizes(w, q)
             if not w.is_contiguous():
                 raise ValueError(f"{name}: bucket planning needs contiguous weights "
                                  "(the plan keeps pointers to their storage)")
+        layouts = plan_layout([(n, tuple(w.shape), w.dtype, bool(quantize_if(n, w)))
+                               for n, w in named_weights],
+                              self.bucket_bytes, fmt, block_size, scale_suffix)
+        self.buckets = [self._bucket(lay, src) for lay in layouts]
+
+    def _bucket(self, lay: BucketLayout, src: dict) -> Bucket:
+        by_name = {e.name: e for e in lay.entries}
+        copies, qin, qout = [], [], []
+        for name, q in lay.items:
+            w = src[name]
             if not q:
-                shape, dt, n = sizes[0]
-                e = _Entry(name, shape, dt, off, n, src=w)
-                entries.append(e)
+                e = by_name[name]
+                e.src = w
                 copies.append(e)
-                off += _align(n)
                 continue
-            (cshape, cdt, cn), (sshape, sdt, sn) = sizes
-            ce = _Entry(name, cshape, cdt, off, cn)
-            off += _align(cn)
-            se = _Entry(name + self.scale_suffix, sshape, sdt, off, sn)
-            off += _align(sn)
-            entries += [ce, se]
-            codes = self.buffer[ce.offset:ce.offset + cn].view(cdt).view(cshape)
-            scales = self.buffer[se.offset:se.offset + sn].view(sdt).view(sshape)
+            ce, se = by_name[name], by_name[name + self.scale_suffix]
+            codes = self.buffer[ce.offset:ce.offset + ce.nbytes].view(ce.dtype).view(ce.shape)
+            scales = self.buffer[se.offset:se.offset + se.nbytes].view(se.dtype).view(se.shape)
             qin.append(w)
             qout.append((codes, scales))
-        plan = None
-        if qin:
-            plan = ops.QuantPlan(qin, self.fmt, self.block_size, outputs=qout)
-        return Bucket(self.buffer, entries, plan, copies)
+        plan = ops.QuantPlan(qin, self.fmt, self.block_size, outputs=qout) if qin else None
+        return Bucket(self.buffer, lay.entries, plan, copies)
 
     def __iter__(self) -> Iterator[Bucket]:
         return iter(self.buckets)

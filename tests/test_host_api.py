@@ -142,3 +142,65 @@ def test_matrix_view_addresses_exactly_the_tensor(t):
     # matrices never overlap and rows never overlap
     assert rows == 1 or ld >= cols
     assert batch == 1 or bstride >= (rows - 1) * ld + cols
+
+
+# transfer-bucket layout (pure host arithmetic)
+from lumenrl_amd.quantization.bucket import entry_sizes, plan_layout  # noqa: E402
+
+
+@st.composite
+def _weight_lists(draw):
+    fmt = draw(st.sampled_from(["fp8_block", "mxfp8", "mxfp4"]))
+    n = draw(st.integers(1, 12))
+    ws = []
+    for i in range(n):
+        q = draw(st.booleans())
+        if q:
+            lead = tuple(draw(st.lists(st.integers(1, 3), max_size=1)))
+            shape = lead + (draw(st.integers(1, 300)), 32 * draw(st.integers(1, 40)))
+        else:
+            shape = tuple(draw(st.lists(st.integers(1, 300), min_size=1, max_size=2)))
+        ws.append((f"w{i}", shape, draw(st.sampled_from([torch.bfloat16, torch.float32])), q))
+    return fmt, ws
+
+
+@settings(max_examples=300, deadline=None)
+@given(_weight_lists(), st.integers(1 << 12, 1 << 20))
+def test_bucket_layout_properties(fw, bucket_bytes):
+    fmt, ws = fw
+    need = {n: sum((e[2] + 255) // 256 * 256 for e in entry_sizes(s, d, q, fmt, (128, 128)))
+            for n, s, d, q in ws}
+    if max(need.values()) > bucket_bytes:
+        with pytest.raises(ValueError, match="more than the bucket"):
+            plan_layout(ws, bucket_bytes, fmt)
+        return
+    layouts = plan_layout(ws, bucket_bytes, fmt)
+    # every weight once, in order; quantized ones bring their scale entry
+    assert [n for lay in layouts for n, _ in lay.items] == [n for n, *_ in ws]
+    for lay in layouts:
+        assert lay.nbytes <= bucket_bytes
+        end = 0
+        for e in lay.entries:
+            assert e.offset % 256 == 0 and e.offset >= end  # aligned, in order, no overlap
+            end = e.offset + e.nbytes
+        assert end <= lay.nbytes
+        names = [e.name for e in lay.entries]
+        for n, q in lay.items:
+            assert (n + "_scale_inv" in names) == q
+    # greedy: a bucket closes only when the next weight would not fit
+    for a, b in zip(layouts, layouts[1:]):
+        assert a.nbytes + need[b.items[0][0]] > bucket_bytes
+    # codes/scale sizes of each format
+    for n, s, d, q in ws:
+        if not q:
+            continue
+        (cs, cdt, cn), (ss, sdt, sn) = entry_sizes(s, d, True, fmt, (128, 128))
+        rows, cols = s[-2], s[-1]
+        lead = 1
+        for x in s[:-2]:
+            lead *= x
+        if fmt == "fp8_block":
+            assert cn == lead * rows * cols and sn == 4 * lead * -(-rows // 128) * -(-cols // 128)
+        else:
+            assert cn == lead * rows * (cols if fmt == "mxfp8" else cols // 2)
+            assert sn == lead * rows * (cols // 32) and sdt == torch.uint8
