@@ -153,3 +153,50 @@ def test_logprob_parity_small_lm():
         q = F.softmax(twin(ids)[:, :-1].float(), dim=-1)
         kl = F.kl_div(log_p, q, reduction="batchmean", log_target=False)
     assert torch.isfinite(kl) and float(kl) < 0.25
+
+
+# The reference runs these ops on GPU tensors in production: the same op
+# sequence evaluated by torch on this MI355X gives the same bits as the kernels.
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
+def test_matches_reference_ops_run_by_torch_on_the_gpu(dtype):
+    from lumenrl_amd.quantization import TensorScalePlan, act_qdq, ops
+
+    g = torch.Generator().manual_seed(11)
+    x = torch.randn(256, 1024, generator=g) * 0.03
+    x[0, :128] = 0.0
+    x[3, :128] = 1e-39 if dtype != torch.float16 else 1e-6
+    x[5, 7] = 40.0
+    xs = x.to(dtype).to(DEV)
+    special = x.clone()
+    special[7, 5], special[8, 3], special[8, 4], special[9, 130] = float("nan"), float("inf"), -float("inf"), -float("nan")
+    xn = special.to(dtype).to(DEV)  # NaN/inf rows: float32-arithmetic paths only
+    cases = [
+        ("1x128 native", xs, lambda t: T.quantize_tensor(t, 128),
+         lambda t: ops.fp8_block_quant(t, (1, 128), native_arith=True)),
+        ("1x128 f32", xn, lambda t: T.quantize_tensor(t.float(), 128), lambda t: ops.fp8_block_quant(t, (1, 128))),
+        ("128x128 f32", xn, lambda t: T.quantize_tensor_tiles(t.float(), (128, 128)),
+         lambda t: ops.fp8_block_quant(t, (128, 128))),
+        ("1x128 f32 pow2", xs, lambda t: T.quantize_tensor(t.float(), 128, True),
+         lambda t: ops.fp8_block_quant(t, (1, 128), pow2=True)),
+    ]
+    def agree(ours, on_gpu, on_x86, what):
+        """Bit-equal to torch on x86 (the pinned rule); equal to torch on the GPU
+        except for NaN payloads, which torch writes differently there."""
+        ours, on_gpu = ours.cpu().reshape(-1), on_gpu.cpu().reshape(-1)
+        assert np.array_equal(bits(ours), bits(on_x86).reshape(-1)), what
+        if ours.dtype == torch.float8_e4m3fn:
+            assert np.array_equal(bits(ours), bits(on_gpu)), what
+            return
+        nan = torch.isnan(on_gpu.float())
+        assert torch.equal(nan, torch.isnan(ours.float())), what
+        assert np.array_equal(bits(ours[~nan]), bits(on_gpu[~nan])), what
+
+    for name, inp, ref, ours in cases:
+        q, s = ours(inp)
+        rq, rs = ref(inp)
+        xq, xs_ = ref(inp.cpu())
+        agree(q, rq, xq, name + " codes")
+        agree(s, rs, xs_, name + " scales")
+    agree(act_qdq(xs, 128), T.act_qdq(xs, 128), T.act_qdq(xs.cpu(), 128), "act finite")
+    agree(act_qdq(xn, 128), T.act_qdq(xn, 128), T.act_qdq(xn.cpu(), 128), "act NaN/inf rows")
+    agree(TensorScalePlan([xs]).run()[:1], T.kv_scale(xs).reshape(1), T.kv_scale(xs.cpu()).reshape(1), "kv")
