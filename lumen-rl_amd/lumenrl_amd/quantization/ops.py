@@ -15,6 +15,7 @@ without synchronizing.  Formats:
 
 from __future__ import annotations
 
+import contextlib
 import ctypes
 from typing import Optional, Sequence
 
@@ -38,8 +39,21 @@ def require_device() -> torch.device:
     return torch.device("cuda", torch.cuda.current_device())
 
 
+_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
 def _stream(device: torch.device) -> ctypes.c_void_p:
+    """The current torch stream of ``device`` as a hipStream_t."""
+    if _raw_stream is not None:
+        return ctypes.c_void_p(_raw_stream(device.index))
     return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+
+
+def _on(device: torch.device):
+    """Make ``device`` current for a launch; a no-op when it already is."""
+    if device.index == torch.cuda.current_device():
+        return contextlib.nullcontext()
+    return torch.cuda.device(device)
 
 
 def _check_input(x: Tensor, what: str) -> None:
@@ -117,7 +131,7 @@ def fp8_block_quant(x: Tensor, block: tuple[int, int], *, native_arith: bool = F
     scales = torch.empty(sshape, dtype=sdt, device=x.device)
     if codes.numel() == 0:
         return codes.reshape(x.shape), scales
-    with torch.cuda.device(x.device):
+    with _on(x.device):
         rc = _lib.lib().lrq_fp8_block_quant(
             xm.data_ptr(), _IN_DTYPES[x.dtype], batch, rows, cols, ld, bstride, br, bc,
             codes.data_ptr(), scales.data_ptr(), flags, _stream(x.device))
@@ -150,7 +164,7 @@ def fp8_block_dequant(codes: Tensor, scales: Tensor, block: tuple[int, int],
     out = torch.empty(codes.shape, dtype=out_dtype, device=codes.device)
     if out.numel() == 0:
         return out
-    with torch.cuda.device(codes.device):
+    with _on(codes.device):
         rc = _lib.lib().lrq_fp8_block_dequant(
             c.data_ptr(), s.data_ptr(), _IN_DTYPES[s.dtype], batch, rows, cols, br, bc,
             out.data_ptr(), _IN_DTYPES[out_dtype], _stream(codes.device))
@@ -180,7 +194,7 @@ def act_qdq(x: Tensor, block: int = 128, *, pow2: bool = False,
     if out.numel() == 0:
         return out
     ld = xm.stride(0) if rows > 1 else last
-    with torch.cuda.device(x.device):
+    with _on(x.device):
         rc = _lib.lib().lrq_act_qdq(xm.data_ptr(), _IN_DTYPES[x.dtype], rows, last, ld, int(block),
                                     _lib.FLAG_POW2_SCALE if pow2 else 0, out.data_ptr(),
                                     _stream(x.device))
@@ -205,7 +219,7 @@ def _mx(x: Tensor, fmt: int) -> tuple[Tensor, Tensor]:
     if x.numel() == 0:
         return codes, scales
     fn = _lib.lib().lrq_mxfp8_quant if fmt == 8 else _lib.lib().lrq_mxfp4_quant
-    with torch.cuda.device(x.device):
+    with _on(x.device):
         rc = fn(xm.data_ptr(), _IN_DTYPES[x.dtype], rows_all, cols, ld, codes.data_ptr(),
                 scales.data_ptr(), _stream(x.device))
     _lib.check(rc, "lrq_mxfp8_quant" if fmt == 8 else "lrq_mxfp4_quant")
@@ -261,7 +275,7 @@ class _GroupLaunch:
         self.units = int(L.lrq_group_units(self.host.data_ptr()))
 
     def run(self) -> None:
-        with torch.cuda.device(self.device):
+        with _on(self.device):
             rc = _lib.lib().lrq_quant_grouped(self.host.data_ptr(), self.dev.data_ptr(),
                                               _stream(self.device))
         _lib.check(rc, "lrq_quant_grouped")
@@ -270,7 +284,7 @@ class _GroupLaunch:
         return int(_lib.lib().lrq_group_workspace_bytes(self.host.data_ptr()))
 
     def run_tensor_scale(self, workspace: Tensor) -> None:
-        with torch.cuda.device(self.device):
+        with _on(self.device):
             rc = _lib.lib().lrq_tensor_scale_grouped(self.host.data_ptr(), self.dev.data_ptr(),
                                                      workspace.data_ptr(), _nbytes(workspace),
                                                      _stream(self.device))
