@@ -19,6 +19,10 @@ already resident in HBM:
   c2sd: the drop-in WeightQuantizer.quantize_state_dict on the c2 weights held
        in a device state dict (1x128 blocks, bf16 `_fp8_scales` sidecar, new
        outputs every call): the API path end to end, host work included.
+  bucket: one trainer-side weight sync of the whole Qwen3-8B state into 2 GiB
+       transfer buckets (QuantizedBucketWriter): the c2 linears quantized to
+       128x128 FP8 straight into the buckets, and embed_tokens, lm_head and
+       every norm (input/post-attention, q_norm/k_norm, final) copied through.
   kv:  FP8KVCacheQuantizer scale recalibration: max(|W|.max(), FLT_MIN)/448 over
        the 108 q/k/v_proj weights of Qwen3-8B (c2's values), one grouped
        amax launch + one per-tensor finishing launch.
@@ -59,7 +63,7 @@ PROFILE_FOR = {"c2": "k_tile128_qwen3_8b_fp8_128x128", "c2r": "k_row_qwen3_8b_fp
                "c5": "k_mx_qwen3_8b_mxfp4", "c2d": "k_dequant_qwen3_8b_fp8_1x128_to_bf16",
                "act": "k_act_qdq_qwen3_8b_prefill_8192", "kv": "k_amax_qwen3_8b_qkv_scales"}
 KERNEL_FOR = {"c1": "k_tile128", "c2": "k_tile128", "c3": "k_tile128", "c4": "k_mx", "c5": "k_mx",
-              "c2r": "k_row", "c2d": "k_dequant", "act": "k_act_qdq8", "kv": "k_amax", "c2sd": "k_row"}
+              "c2r": "k_row", "c2d": "k_dequant", "act": "k_act_qdq8", "kv": "k_amax", "c2sd": "k_row", "bucket": "k_tile128"}
 PREFILL_TOKENS = 8192
 
 
@@ -105,6 +109,34 @@ def qwen3_8b_set(torch, dev, seed, kind="normal", layers=36):
             ws.append(gen_weight(torch, r, c, gen, dev, kind))
             names.append(f"layers.{layer}.{name}")
     return ws, names
+
+
+def qwen3_8b_state(torch, dev, seed):
+    """The whole Qwen3-8B state in HF key order: embed_tokens, per layer the two
+    RMSNorms, q_norm/k_norm and the seven linears (c2's values), final norm, lm_head."""
+    ws, names = qwen3_8b_set(torch, dev, seed, "normal")
+    g = torch.Generator(device=dev).manual_seed(seed - 1)
+
+    def emb():
+        return (torch.randn(151936, 4096, generator=g, device=dev) * 0.02).to(torch.bfloat16)
+
+    def norm(n):
+        return (1.0 + 0.1 * torch.randn(n, generator=g, device=dev)).to(torch.bfloat16)
+
+    named = [("model.embed_tokens.weight", emb())]
+    lin = iter(zip(names, ws))
+    for layer in range(36):
+        pre = f"model.layers.{layer}"
+        named += [(f"{pre}.input_layernorm.weight", norm(4096)),
+                  (f"{pre}.post_attention_layernorm.weight", norm(4096)),
+                  (f"{pre}.self_attn.q_norm.weight", norm(128)),
+                  (f"{pre}.self_attn.k_norm.weight", norm(128))]
+        for _ in range(7):
+            n, w = next(lin)
+            kind = "self_attn" if n.split(".")[-1] in ("q_proj", "k_proj", "v_proj", "o_proj") else "mlp"
+            named.append((f"{pre}.{kind}.{n.split('.')[-1]}.weight", w))
+    named += [("model.norm.weight", norm(4096)), ("lm_head.weight", emb())]
+    return named
 
 
 def moe_layer(torch, dev, seed, layer, experts=128):
@@ -220,6 +252,18 @@ def _cpu_pass(torch, O, torch_ref, np, ws, fmt, fmt_block, seconds, threads):
     return done_bytes, t_total, n
 
 
+class _BucketFill:
+    """One bucket of a weight sync: the grouped quantize launch plus the copies."""
+
+    def __init__(self, bucket):
+        self.bucket = bucket
+        q = bucket.plan.algorithmic_bytes if bucket.plan is not None else 0
+        self.algorithmic_bytes = q + 2 * sum(e.nbytes for e in bucket.copies)
+
+    def run(self):
+        self.bucket.fill()
+
+
 class _StateDictCall:
     """One drop-in quantize_state_dict call (plan, allocations and launch)."""
 
@@ -291,6 +335,19 @@ def run(args):
         extra = {"tensors": len(ws), "layers": 36, "elements": sum(w.numel() for w in ws),
                  "format": "fp8_block_1x128_bf16_scales", "launches_per_step": 1,
                  "host_work_timed": True}
+    elif cfg == "bucket":
+        from lumenrl_amd.quantization import QuantizedBucketWriter
+
+        named = qwen3_8b_state(torch, dev, args.seed)
+        writer = QuantizedBucketWriter(named, bucket_bytes=2 << 30, fmt="fp8_block")
+        plans = [_BucketFill(b) for b in writer]
+        ws = [w for _, w in named]
+        workload = "qwen3-8b-state-sync-into-fp8-buckets"
+        cpu_ws, cpu_blk, cpu_fmt = [], (128, 128), "fp8_block"
+        extra = {"tensors": len(named), "buckets": len(writer), "layers": 36,
+                 "elements": sum(w.numel() for w in ws),
+                 "passthrough_tensors": sum(len(b.copies) for b in writer),
+                 "format": "fp8_block_128x128 + passthrough copies", "launches_per_step": len(writer)}
     elif cfg == "kv":
         ws, names = qwen3_8b_set(torch, dev, args.seed, "normal")
         ws = [w for w, nm in zip(ws, names) if nm.split(".")[-1] in ("q_proj", "k_proj", "v_proj")]
@@ -452,7 +509,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--config", default="c2", choices=["c1", "c2", "c3", "c4", "c5", "c2r", "c2d", "c2sd", "act", "kv"])
+    ap.add_argument("--config", default="c2", choices=["c1", "c2", "c3", "c4", "c5", "c2r", "c2d", "c2sd", "bucket", "act", "kv"])
     ap.add_argument("--seed", type=int, default=1000)
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")

@@ -54,6 +54,12 @@ typedef struct ihipStream_t* lrq_stream_t; /* == hipStream_t */
 #define LRQ_FMT_TENSOR_SCALE 4 /* per-tensor FP8 scale (lrq_tensor_scale_grouped):
                                   lrq_tensor.in = weight, .scales = one float32 out,
                                   .codes unused (may be NULL) */
+#define LRQ_FMT_COPY 5 /* grouped byte copy through lrq_quant_grouped: lrq_tensor.in =
+                          source, .codes = destination (both 16-byte aligned), .cols =
+                          bytes, batch = rows = 1, .ld = .cols, .scales unused (may be
+                          NULL); in_dtype must be a valid dtype and is otherwise ignored.
+                          The pass-through tensors of a weight-transfer bucket in one
+                          launch (bucketed_weight_transfer.py:137-165 copies each) */
 
 /* errors */
 #define LRQ_ERR_ARG (-1)      /* invalid argument (shape, dtype, block size, null) */

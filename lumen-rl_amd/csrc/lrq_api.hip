@@ -68,7 +68,7 @@ bool span_ok(int64_t batch, int64_t rows, int64_t cols, int64_t ld, int64_t bstr
 }
 
 // Fill a Desc from a tensor and check its shape.
-int make_desc(const lrq_tensor& t, Desc& d, bool need_codes = true) {
+int make_desc(const lrq_tensor& t, Desc& d, bool need_codes = true, bool need_scales = true) {
   if (t.batch < 0 || t.rows < 0 || t.cols < 0) return fail(LRQ_ERR_ARG, "negative extent");
   if (!span_ok(t.batch, t.rows, t.cols, t.ld < t.cols ? t.cols : t.ld, t.batch > 1 ? t.batch_stride : 0))
     return fail(LRQ_ERR_ARG, "extents exceed 2^48 elements");
@@ -80,7 +80,7 @@ int make_desc(const lrq_tensor& t, Desc& d, bool need_codes = true) {
   if (t.ld < t.cols) return fail(LRQ_ERR_ARG, "ld (%lld) < cols (%lld)", (long long)t.ld, (long long)t.cols);
   if (t.batch > 1 && t.batch_stride < (t.rows - 1) * t.ld + t.cols)
     return fail(LRQ_ERR_ARG, "batch_stride (%lld) overlaps matrices", (long long)t.batch_stride);
-  if (!t.in || (need_codes && !t.codes) || !t.scales) return fail(LRQ_ERR_ARG, "null pointer");
+  if (!t.in || (need_codes && !t.codes) || (need_scales && !t.scales)) return fail(LRQ_ERR_ARG, "null pointer");
   memset(&d, 0, sizeof(d));
   d.in = t.in;
   d.codes = static_cast<uint8_t*>(t.codes);
@@ -249,6 +249,8 @@ int plan_group(int fmt, const lrq_tensor* ts, int64_t n, int in_dtype, int64_t b
     cfg.out_dtype = (flags & LRQ_FLAG_OUT_BF16) ? lrq::kBF16 : lrq::kF32;
   } else if (fmt == LRQ_FMT_TENSOR_SCALE) {
     cfg.kernel = lrq::kKernAmax;
+  } else if (fmt == LRQ_FMT_COPY) {
+    cfg.kernel = lrq::kKernCopy;
   } else {
     return fail(LRQ_ERR_ARG, "bad format %d", fmt);
   }
@@ -256,8 +258,19 @@ int plan_group(int fmt, const lrq_tensor* ts, int64_t n, int in_dtype, int64_t b
   int64_t units = 0;
   for (int64_t i = 0; i < n; ++i) {
     Desc d;
-    if (int rc = make_desc(ts[i], d, fmt != LRQ_FMT_TENSOR_SCALE))
+    if (int rc = make_desc(ts[i], d, fmt != LRQ_FMT_TENSOR_SCALE, fmt != LRQ_FMT_COPY))
       return fail(rc, "tensor %lld: %s", (long long)i, g_err.c_str());
+    if (fmt == LRQ_FMT_COPY) {
+      if (d.batch > 1 || d.rows > 1 || (d.cols > 0 && d.ld != d.cols))
+        return fail(LRQ_ERR_ARG, "tensor %lld: a copy entry is one run of bytes (batch = rows = 1)", (long long)i);
+      if (d.cols > 0 && (!aligned(d.in, 16) || !aligned(d.codes, 16)))
+        return fail(LRQ_ERR_ALIGN, "tensor %lld: copy source and destination must be 16-byte aligned", (long long)i);
+      d.units = (d.cols + lrq::kCopyUnit - 1) / lrq::kCopyUnit;
+      d.unit0 = units;
+      units += d.units;
+      if (ds) ds[i] = d;
+      continue;
+    }
     if (fmt == LRQ_FMT_TENSOR_SCALE) {
       if (d.batch == 0 || d.rows == 0 || d.cols == 0)
         return fail(LRQ_ERR_ARG, "tensor %lld is empty: a max over no elements is undefined", (long long)i);
@@ -301,7 +314,7 @@ int plan_group(int fmt, const lrq_tensor* ts, int64_t n, int in_dtype, int64_t b
     units += d.units;
     if (ds) ds[i] = d;
   }
-  if (kernel < 0 && fmt != LRQ_FMT_TENSOR_SCALE)
+  if (kernel < 0 && fmt != LRQ_FMT_TENSOR_SCALE && fmt != LRQ_FMT_COPY)
     cfg.kernel = fmt == LRQ_FMT_FP8_BLOCK ? lrq::kKernGenericFp8 : lrq::kKernGenericMx;
   if (fmt == LRQ_FMT_FP8_DEQUANT) {
     cfg.rows_dense = 1;
@@ -435,6 +448,8 @@ int lrq_quant_grouped(const void* host_table, const void* device_table, lrq_stre
   const char* dev = static_cast<const char*>(device_table);
   const Desc* descs = reinterpret_cast<const Desc*>(dev + h.desc_off);
   const uint32_t* map = reinterpret_cast<const uint32_t*>(dev + h.map_off);
+  if (h.cfg.kernel == lrq::kKernCopy)
+    return check_hip(lrq::launch_copy(descs, map, h.units, (hipStream_t)stream), "kernel launch");
   Desc dummy;
   memset(&dummy, 0, sizeof(dummy));
   return check_hip(lrq::launch(h.cfg, dummy, descs, map, h.units, (hipStream_t)stream), "kernel launch");

@@ -34,7 +34,11 @@ enum Kernel : int {
   kKernDequant = 5,        // FP8 dequant, 16 codes per lane-chunk
   kKernGenericDequant = 6, // FP8 dequant, one element per thread
   kKernAmax = 7,           // per-tensor max |x| partials + scale (two launches)
+  kKernCopy = 8,           // grouped byte copy (bucket pass-through tensors)
 };
+
+// Bytes one work-group of the grouped copy moves.
+constexpr int64_t kCopyUnit = 4096;
 
 // Descriptor and local work unit of this work-group: the single-tensor
 // descriptor (kernel argument) or, for a grouped launch, the one the device
@@ -83,6 +87,9 @@ hipError_t launch_dequant(const LaunchCfg&, const Desc&, const Desc*, const uint
 int64_t amax_unit_elems(int dtype, bool vec);
 hipError_t launch_tensor_scale(const LaunchCfg& cfg, const Desc* descs, const uint32_t* map, int64_t n,
                                int64_t units, uint32_t* partial, hipStream_t stream);
+
+// Grouped byte copy over `units` work-groups.
+hipError_t launch_copy(const Desc* descs, const uint32_t* map, int64_t units, hipStream_t stream);
 
 // Activation fake-quant.
 int64_t act_grid(const void* in, int dtype, int64_t rows, int64_t cols, int64_t ld);

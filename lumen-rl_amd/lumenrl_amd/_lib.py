@@ -15,7 +15,7 @@ LIB_PATH = os.path.join(_HERE, "liblrq.so")
 
 DTYPE_BF16, DTYPE_F16, DTYPE_F32 = 0, 1, 2
 FLAG_POW2_SCALE, FLAG_NATIVE_ARITH, FLAG_SCALE_BF16, FLAG_OUT_BF16 = 1, 2, 4, 8
-FMT_FP8_BLOCK, FMT_MXFP8, FMT_MXFP4, FMT_FP8_DEQUANT, FMT_TENSOR_SCALE = 0, 1, 2, 3, 4
+FMT_FP8_BLOCK, FMT_MXFP8, FMT_MXFP4, FMT_FP8_DEQUANT, FMT_TENSOR_SCALE, FMT_COPY = 0, 1, 2, 3, 4, 5
 ERR_ARG, ERR_ALIGN, ERR_CAPACITY, ERR_TABLE = -1, -2, -3, -4
 
 

@@ -10,6 +10,7 @@ from lumenrl_amd.quantization.fp8_config import (
 from lumenrl_amd.quantization.fp8_kv_cache import FP8KVCacheQuantizer
 from lumenrl_amd.quantization.fp8_rollout import FP8RolloutQuantizer
 from lumenrl_amd.quantization.ops import (
+    CopyPlan,
     DequantPlan,
     QuantPlan,
     TensorScalePlan,
@@ -21,6 +22,7 @@ from lumenrl_amd.quantization.ops import act_qdq, fp8_block_dequant, fp8_block_q
 from lumenrl_amd.quantization.weight_quantizer import WeightQuantizer, fp8_e4m3_max
 
 __all__ = [
+    "CopyPlan",
     "DequantPlan",
     "FP8Config",
     "FP8KVCacheQuantizer",

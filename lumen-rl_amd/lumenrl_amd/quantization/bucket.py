@@ -51,7 +51,8 @@ class _Entry:
 
 
 class Bucket:
-    """One planned bucket: a grouped quantize launch plus pass-through copies."""
+    """One planned bucket: a grouped quantize launch plus the pass-through copies,
+    which (16-byte-aligned sources, the torch norm) go in one grouped copy launch."""
 
     def __init__(self, buffer: Tensor, entries: list[_Entry], plan: Optional[ops.QuantPlan],
                  copies: list[_Entry]) -> None:
@@ -60,14 +61,24 @@ class Bucket:
         self.plan = plan
         self.copies = copies
         self.nbytes = max((e.offset + e.nbytes for e in entries), default=0)
+        pairs, self._loose = [], []
+        for e in copies:
+            dst = buffer[e.offset:e.offset + e.nbytes]
+            src = e.src.reshape(-1).view(torch.uint8)
+            if e.nbytes and src.data_ptr() % 16 == 0 and dst.data_ptr() % 16 == 0:
+                pairs.append((dst, src))
+            elif e.nbytes:
+                self._loose.append((dst, src))
+        self.copy_plan = ops.CopyPlan(pairs) if pairs else None
 
     def fill(self) -> "Bucket":
         """Enqueue the quantize launch and the pass-through copies (current stream)."""
         if self.plan is not None:
             self.plan.run()
-        for e in self.copies:
-            self.buffer[e.offset:e.offset + e.nbytes].copy_(
-                e.src.reshape(-1).view(torch.uint8), non_blocking=True)
+        if self.copy_plan is not None:
+            self.copy_plan.run()
+        for dst, src in self._loose:
+            dst.copy_(src, non_blocking=True)
         return self
 
     def bucket_meta(self) -> dict:

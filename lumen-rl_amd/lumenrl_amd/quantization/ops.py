@@ -253,7 +253,8 @@ def quantize_fp8_blockwise(x: Tensor, block_size: tuple[int, int] = (128, 128), 
 # grouped launches
 # ---------------------------------------------------------------------------
 _FMTS = {"fp8_block": _lib.FMT_FP8_BLOCK, "mxfp8": _lib.FMT_MXFP8, "mxfp4": _lib.FMT_MXFP4,
-         "fp8_dequant": _lib.FMT_FP8_DEQUANT, "tensor_scale": _lib.FMT_TENSOR_SCALE}
+         "fp8_dequant": _lib.FMT_FP8_DEQUANT, "tensor_scale": _lib.FMT_TENSOR_SCALE,
+         "copy": _lib.FMT_COPY}
 
 
 class _GroupLaunch:
@@ -488,6 +489,40 @@ class TensorScalePlan:
         """Enqueue both launches on the current stream; returns ``scales``."""
         self._launch.run_tensor_scale(self.workspace)
         return self.scales
+
+
+class CopyPlan:
+    """One launch that copies many (dst, src) byte ranges on one device.
+
+    ``pairs`` are contiguous tensors of equal byte size, 16-byte aligned (any
+    dtype: the copy is bytewise).  Used for the pass-through tensors of a
+    transfer bucket, which would otherwise take one copy launch each.
+    """
+
+    def __init__(self, pairs: Sequence[tuple[Tensor, Tensor]]) -> None:
+        if not pairs:
+            raise ValueError("CopyPlan needs at least one (dst, src) pair")
+        dev = pairs[0][0].device
+        descs = (_lib.LrqTensor * len(pairs))()
+        self.pairs = list(pairs)
+        nbytes = 0
+        for i, (dst, src) in enumerate(pairs):
+            n = _nbytes(src)
+            if (not dst.is_cuda or not src.is_cuda or dst.device != dev or src.device != dev
+                    or not dst.is_contiguous() or not src.is_contiguous() or _nbytes(dst) != n):
+                raise ValueError(f"pair {i}: contiguous device tensors of equal size on {dev} required")
+            descs[i].in_ = src.data_ptr()
+            descs[i].codes = dst.data_ptr()
+            descs[i].scales = None
+            descs[i].batch, descs[i].rows, descs[i].cols = 1, 1, n
+            descs[i].ld, descs[i].batch_stride = n, n
+            nbytes += 2 * n
+        self.algorithmic_bytes = nbytes
+        self._launch = _GroupLaunch("copy", descs, len(pairs), _lib.DTYPE_BF16, (1, 1), 0, dev)
+        self.units = self._launch.units
+
+    def run(self) -> None:
+        self._launch.run()
 
 
 def _prod(shape) -> int:

@@ -215,6 +215,30 @@ def test_c_caller_is_built_against_the_in_tree_libraries():
     assert "oracle/_build/liblrq_oracle.so" in deps
 
 
+def test_copy_tables():
+    """Grouped byte copies: 4 KiB units, NULL scales allowed, alignment and
+    single-run checks before any device work."""
+    fmt = _lib.FMT_COPY
+    sizes = [16384 * 3, 200, 16384 + 17, 1]
+    ts = (_lib.LrqTensor * len(sizes))()
+    base = 0x100000
+    for i, n in enumerate(sizes):
+        ts[i].in_, ts[i].codes, ts[i].scales = base, base + (1 << 24), None
+        ts[i].batch, ts[i].rows, ts[i].cols, ts[i].ld, ts[i].batch_stride = 1, 1, n, n, n
+        base += 1 << 20
+    need = L().lrq_group_table_bytes(fmt, ts, len(sizes), 0, 1, 1, 0)
+    assert need > 0, _lib.last_error()
+    buf = np.zeros(need, np.uint8)
+    assert L().lrq_group_pack(fmt, ts, len(sizes), 0, 1, 1, 0, buf.ctypes.data, need) == 0
+    assert L().lrq_group_units(buf.ctypes.data) == sum(-(-n // 4096) for n in sizes)
+    assert L().lrq_group_workspace_bytes(buf.ctypes.data) == 0
+    ts[1].in_ = ts[1].in_ + 8
+    assert L().lrq_group_table_bytes(fmt, ts, len(sizes), 0, 1, 1, 0) == _lib.ERR_ALIGN
+    ts[1].in_ = ts[1].in_ - 8
+    ts[2].rows = 2
+    assert L().lrq_group_table_bytes(fmt, ts, len(sizes), 0, 1, 1, 0) == _lib.ERR_ARG
+
+
 def test_grouped_rejects_foreign_table():
     junk = np.zeros(4096, np.uint8)
     rc = L().lrq_quant_grouped(junk.ctypes.data, ctypes.c_void_p(0x1000), None)

@@ -540,3 +540,24 @@ def test_bucket_writer_matches_oracle(fmt):
                 assert np.array_equal(u8(t).reshape(-1), want.reshape(-1))
     assert seen == {n for n, _ in named} | {n + "_scale_inv" for n, _ in named
                                              if "embed" not in n and "lm_head" not in n and "norm" not in n}
+
+
+def test_grouped_copy_plan_odd_sizes():
+    """Grouped byte copies of sizes around the 4 KiB unit and 16-byte tails."""
+    from lumenrl_amd.quantization import CopyPlan
+
+    g = torch.Generator(device=DEV).manual_seed(8)
+    sizes = [1, 15, 16, 200, 4095, 4096, 4097, 4096 * 7 + 9, 16385, 3 << 20]
+    srcs = [torch.randint(0, 256, (n,), generator=g, device=DEV, dtype=torch.uint8) for n in sizes]
+    dsts = [torch.full((n,), 0xAB, device=DEV, dtype=torch.uint8) for n in sizes]
+    plan = CopyPlan(list(zip(dsts, srcs)))
+    plan.run()
+    torch.cuda.synchronize()
+    for n, d, s in zip(sizes, dsts, srcs):
+        assert torch.equal(d, s), n
+    # any dtype: bf16 weights copied bytewise into uint8 views
+    w = torch.randn(300, 130, generator=g, device=DEV).to(torch.bfloat16)
+    out = torch.empty(300 * 130 * 2, dtype=torch.uint8, device=DEV)
+    CopyPlan([(out, w.reshape(-1).view(torch.uint8))]).run()
+    torch.cuda.synchronize()
+    assert torch.equal(out.view(torch.bfloat16).view(300, 130), w)
