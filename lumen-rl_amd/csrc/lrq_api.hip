@@ -156,7 +156,7 @@ bool plan_units(const LaunchCfg& cfg, Desc& d) {
       if (cfg.kernel == kKernDequant) {
         const int64_t cpc = cfg.out_dtype == kBF16 ? 8 : 4;  // codes per lane-chunk
         d.nblocks = d.batch * d.rows * d.cols / cpc;
-        d.units = (d.nblocks + 2047) / 2048;                  // 256 lanes x 8 chunks
+        d.units = (d.nblocks + 256 * kDequantChunks - 1) / (256 * kDequantChunks);
       } else {
         d.nblocks = d.batch * d.rows * d.cols;
         d.units = (d.nblocks + 255) / 256;
@@ -171,7 +171,8 @@ bool plan_units(const LaunchCfg& cfg, Desc& d) {
       }
       d.bpr = d.cols / 32;
       d.nblocks = d.rows * d.bpr;
-      d.units = (d.nblocks + 255) / 256;
+      if (cfg.kernel == kKernMx) d.units = (d.nblocks + 64 * kMxLoads - 1) / (64 * kMxLoads);
+      else d.units = (d.nblocks + 255) / 256;
       return true;
   }
   return false;

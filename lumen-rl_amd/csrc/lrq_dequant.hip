@@ -59,7 +59,7 @@ __global__ __launch_bounds__(256) void k_dequant_generic(Desc single, const Desc
 // Vectorized: a lane-chunk is CPC codes (8 for bf16 output, 4 for fp32) whose
 // output is exactly one 16-byte store, so every wave load and store
 // instruction covers one contiguous span (512 B / 256 B of codes, 1 KiB out);
-// eight chunks per lane keep enough loads in flight.  A chunk lies inside one
+// kDequantChunks chunks per lane, all loaded before the first store.  A chunk lies inside one
 // block (blk_c % 16 == 0), so its scale is uniform: when the scale is finite
 // and non-zero and no code is NaN the chunk takes the hardware path
 // (v_cvt_pk_f32_fp8 -> multiply -> v_cvt_pk_bf16_f32); anything else takes the
@@ -74,7 +74,7 @@ __global__ __launch_bounds__(256) void k_dequant(Desc single, const Desc* __rest
                                                  const uint32_t* __restrict__ map, int blk_r, int blk_c) {
   constexpr int CPC = ODT == kBF16 ? 8 : 4;  // codes per lane-chunk
   constexpr int NW = CPC / 4;                // code words per chunk
-  constexpr int NCH = 8;                     // chunks per lane
+  constexpr int NCH = kDequantChunks;        // chunks per lane
   Desc d;
   int64_t u;
   pick_desc(single, descs, map, d, u);

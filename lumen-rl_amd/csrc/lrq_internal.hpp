@@ -37,8 +37,12 @@ enum Kernel : int {
   kKernCopy = 8,           // grouped byte copy (bucket pass-through tensors)
 };
 
-// Bytes one work-group of the grouped copy moves.
-constexpr int64_t kCopyUnit = 4096;
+// Work per lane of the streaming kernels, shared by the kernels and the
+// work-group planner (values chosen by sweeps on an MI355X).
+constexpr int64_t kCopyUnit = 4096;  // k_copy: bytes per work-group (one 16 B load per lane)
+constexpr int kDequantChunks = 2;    // k_dequant: 16-byte output chunks per lane (2 beat 1, 4 and 8)
+constexpr int kMxLoads = 2;          // k_mx: 32-element groups per quad of lanes (2 beat 1, 3 and 4)
+constexpr int kAmaxLoads = 2;        // k_amax: 16-byte loads per lane (2 beat 1, 3, 4 and 8)
 
 // Descriptor and local work unit of this work-group: the single-tensor
 // descriptor (kernel argument) or, for a grouped launch, the one the device

@@ -110,12 +110,12 @@ __global__ __launch_bounds__(256) void k_mx(Desc single, const Desc* __restrict_
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int p = lane & 3;
-  const int64_t g0 = u * 256 + (tid >> 6) * 64 + (lane >> 2);
+  const int64_t g0 = u * (64 * kMxLoads) + (tid >> 6) * (16 * kMxLoads) + (lane >> 2);
 
-  uint32_t w[4][8];
-  bool ok[4];
+  uint32_t w[kMxLoads][8];
+  bool ok[kMxLoads];
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
+  for (int j = 0; j < kMxLoads; ++j) {
     const int64_t g = g0 + 16 * j;
     ok[j] = g < d.nblocks;
     if (ok[j]) {
@@ -134,7 +134,7 @@ __global__ __launch_bounds__(256) void k_mx(Desc single, const Desc* __restrict_
   }
 
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
+  for (int j = 0; j < kMxLoads; ++j) {
     // quads are either wholly in range or wholly out: the DPP stays in-quad
     const uint32_t a = quad_max(mx_amax8<DT>(w[j]));
     const uint32_t e = mx_e8m0<kEmax>(a);

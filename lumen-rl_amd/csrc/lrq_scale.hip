@@ -4,9 +4,9 @@
 // NaN anywhere -> 0x7FC00000 (torch's multi-threaded x86 reduction).
 //
 // Two launches over a grouped table:
-//   k_amax          every work-group streams one 16 KiB unit of one tensor with
-//                   four 16-byte nontemporal loads per lane (all issued before
-//                   the reduction) and writes the unit's max |x| bit pattern to
+//   k_amax          every work-group streams one 8 KiB unit of one tensor with
+//                   kAmaxLoads (two) 16-byte nontemporal loads per lane, all
+//                   issued before the reduction, and writes the unit's max |x| bit pattern to
 //                   workspace[global unit];
 //   k_tensor_scale  one work-group per tensor reduces its units' partials and
 //                   writes the float32 scale.
@@ -20,9 +20,8 @@
 
 namespace lrq {
 
-constexpr int kAmaxLoads = 4;  // 16-byte loads per lane per unit (4 measured 1.5% faster than 8)
 
-// Elements per unit of the vector kernel (256 lanes x 4 loads x 16 bytes).
+// Elements per unit of the vector kernel (256 lanes x kAmaxLoads x 16 bytes).
 int64_t amax_unit_elems(int dtype, bool vec) {
   return vec ? 256 * kAmaxLoads * (16 / (dtype == kF32 ? 4 : 2)) : 256 * 32;
 }

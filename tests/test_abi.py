@@ -131,7 +131,8 @@ def test_group_pack_rows_and_mx_units():
     # 1x128 rows: 16 lanes per block, 4 blocks per wave instruction, 64 blocks per work-group
     assert L().lrq_group_units(buf.ctypes.data) == -(-256 * 32 // 64) + -(-64 * 96 // 64)
     buf = _pack(_lib.FMT_MXFP4, shapes, (1, 32))
-    assert L().lrq_group_units(buf.ctypes.data) == -(-256 * 128 // 256) + -(-64 * 384 // 256)
+    # MX: 64 lanes of a wave, a quad per group, 2 groups per quad -> 128 groups per work-group
+    assert L().lrq_group_units(buf.ctypes.data) == -(-256 * 128 // 128) + -(-64 * 384 // 128)
     del blocks
 
 
@@ -153,7 +154,7 @@ def test_group_pack_rejects_mixed_kernels_and_small_buffers():
 
 
 def test_tensor_scale_tables():
-    """Per-tensor scale tables: 16 KiB units (16-byte loads) or 8192-element units
+    """Per-tensor scale tables: 8 KiB units (16-byte loads) or 8192-element units
     (element walk) in one table, no codes pointer, workspace of 4 B per unit."""
     qkv = [(1, 4096, 4096), (1, 1024, 4096), (1, 1024, 4096)]
     ts = _tensors(qkv + [(1, 300, 100)])
@@ -165,7 +166,7 @@ def test_tensor_scale_tables():
     assert need > 0, _lib.last_error()
     buf = np.zeros(need, np.uint8)
     assert L().lrq_group_pack(fmt, ts, 4, 0, 1, 1, 0, buf.ctypes.data, need) == 0, _lib.last_error()
-    units = [4096 * 4096 // 8192, 1024 * 4096 // 8192, 1024 * 4096 // 8192, -(-300 * 100 // 8192)]
+    units = [4096 * 4096 // 4096, 1024 * 4096 // 4096, 1024 * 4096 // 4096, -(-300 * 100 // 8192)]
     assert L().lrq_group_units(buf.ctypes.data) == sum(units)
     assert L().lrq_group_workspace_bytes(buf.ctypes.data) == 4 * sum(units)
     wmap = buf[-4 * sum(units):].view(np.uint32)
