@@ -145,7 +145,7 @@ bool plan_units(const LaunchCfg& cfg, Desc& d) {
       if (!fold_batch(d)) return false;
       d.bpr = d.cols / cfg.blk_c;
       d.nblocks = d.rows * d.bpr;
-      const int64_t per_wg = 16 * (512 / cfg.blk_c);  // 4 waves x 4 instructions x blocks each
+      const int64_t per_wg = 4 * kRowBlocks * (512 / cfg.blk_c);  // 4 waves x kRowBlocks instructions
       d.units = (d.nblocks + per_wg - 1) / per_wg;
       return true;
     }

@@ -195,11 +195,12 @@ constexpr int64_t kSmallTileLaunch = 2048;
 // wave cover 64 consecutive 8-element chunks, so each load instruction reads
 // one contiguous span (1 KiB of bf16) and each store writes whole 128-byte
 // code lines; lane c of a block holds chunk c of it.  Instruction j of wave w
-// covers blocks (4w + j) * (64 / LPB) + lane / LPB of the work-group.
+// covers blocks (NJ w + j) * (64 / LPB) + lane / LPB of the work-group, with
+// NJ = kRowBlocks blocks per lane.
 // The block amax is reduced over its LPB lanes (DPP within 16 lanes, shuffles
-// beyond).  Each lane then computes the scale of ONE of its four blocks and
-// the four scales are exchanged by shuffles, so the IEEE divisions cost one
-// pair per lane instead of four.  Rows are folded over the batch by the host.
+// beyond).  Each lane then computes the scale of ONE of its NJ blocks and
+// the NJ scales are exchanged by shuffles, so the IEEE divisions cost one
+// pair per lane instead of NJ.  Rows are folded over the batch by the host.
 // ---------------------------------------------------------------------------
 template <int DT, int CDT, int LPB>
 __global__ __launch_bounds__(256) void k_row(Desc single, const Desc* __restrict__ descs,
@@ -212,13 +213,14 @@ __global__ __launch_bounds__(256) void k_row(Desc single, const Desc* __restrict
   pick_desc(single, descs, map, d, u);
   const int tid = threadIdx.x, lane = tid & 63;
   const int c = lane & (LPB - 1);     // chunk of the block held by this lane
-  const int64_t wb = u * (16 * BPI) + (tid >> 6) * (4 * BPI) + lane / LPB;  // block at j = 0
+  constexpr int NJ = kRowBlocks;      // blocks per lane
+  const int64_t wb = u * (4 * NJ * BPI) + (tid >> 6) * (NJ * BPI) + lane / LPB;  // block at j = 0
 
-  Chunk<DT> ch[4];
-  bool ok[4];
-  uint32_t am[4];
+  Chunk<DT> ch[NJ];
+  bool ok[NJ];
+  uint32_t am[NJ];
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
+  for (int j = 0; j < NJ; ++j) {
     const int64_t gb = wb + j * BPI;
     ok[j] = gb < d.nblocks;
     if (ok[j]) {
@@ -235,25 +237,27 @@ __global__ __launch_bounds__(256) void k_row(Desc single, const Desc* __restrict
     }
   }
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
+  for (int j = 0; j < NJ; ++j) {
     Amax<DT> a;
     a.init();
     a.add(ch[j]);
     am[j] = group_max<LPB>(a.bits());  // every lane takes part: groups never straddle
   }
-  // lane c computes the scale of block j = c & 3 of its group; gather all four
-  const uint32_t mine = (c & 3) == 0 ? am[0] : ((c & 3) == 1 ? am[1] : ((c & 3) == 2 ? am[2] : am[3]));
-  const BlockScale own = block_scale<CDT>(mine, pow2 != 0);
-  BlockScale bs[4];
+  // lane c computes the scale of block j = c % NJ of its group; gather all NJ
+  uint32_t mine = am[0];
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
+  for (int j = 1; j < NJ; ++j) mine = (c % NJ) == j ? am[j] : mine;
+  const BlockScale own = block_scale<CDT>(mine, pow2 != 0);
+  BlockScale bs[NJ];
+#pragma unroll
+  for (int j = 0; j < NJ; ++j) {
     const int src = (lane & ~(LPB - 1)) | j;
     bs[j].s = __shfl(own.s, src, 64);
     bs[j].y = __shfl(own.y, src, 64);
     bs[j].kind = __shfl(own.kind, src, 64);
   }
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
+  for (int j = 0; j < NJ; ++j) {
     if (!ok[j]) continue;
     const int64_t gb = wb + j * BPI;
     if (c == 0) store_scale<CDT>(d.scales, gb, bs[j].s, scale_bf16);
