@@ -267,11 +267,21 @@ class _GroupLaunch:
         need = L.lrq_group_table_bytes(_FMTS[fmt], descs, n, in_dtype, br, bc, flags)
         if need < 0:
             _lib.check(int(need), "lrq_group_table_bytes")
-        self.host = torch.empty(int(need), dtype=torch.uint8)
+        self.host = torch.empty(int(need), dtype=torch.uint8, pin_memory=True)
         rc = L.lrq_group_pack(_FMTS[fmt], descs, n, in_dtype, br, bc, flags,
                               self.host.data_ptr(), int(need))
         _lib.check(rc, "lrq_group_pack")
-        self.dev = self.host.to(device)
+        # The device table is allocated and written on the caller's current
+        # stream: stream-ordered like any torch op, so a recycled allocation
+        # is never overwritten while an earlier launch may still read it.  The
+        # copy is from pinned memory and does not block the host (a pageable
+        # copy would wait for the stream to drain, serializing plan building,
+        # e.g. every quantize_state_dict call, with the device).  As for any
+        # tensor produced on a stream, a launch on another stream must first
+        # wait for this one.
+        self.dev = torch.empty(int(need), dtype=torch.uint8, device=device)
+        with _on(device):
+            self.dev.copy_(self.host, non_blocking=True)
         self.device = device
         self.units = int(L.lrq_group_units(self.host.data_ptr()))
 

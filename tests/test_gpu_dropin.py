@@ -200,3 +200,28 @@ def test_matches_reference_ops_run_by_torch_on_the_gpu(dtype):
     agree(act_qdq(xs, 128), T.act_qdq(xs, 128), T.act_qdq(xs.cpu(), 128), "act finite")
     agree(act_qdq(xn, 128), T.act_qdq(xn, 128), T.act_qdq(xn.cpu(), 128), "act NaN/inf rows")
     agree(TensorScalePlan([xs]).run()[:1], T.kv_scale(xs).reshape(1), T.kv_scale(xs.cpu()).reshape(1), "kv")
+
+
+def test_back_to_back_state_dict_calls_keep_every_result():
+    """quantize_state_dict builds and drops a grouped plan per call; calls queued
+    back to back (no synchronization) must each keep their own results while the
+    descriptor tables of earlier calls are recycled by the allocator."""
+    from oracle import oracle as O
+
+    g = torch.Generator(device=DEV).manual_seed(21)
+    sd = {f"l{i}.weight": (torch.randn(1024, 2048, generator=g, device=DEV) * 0.02).to(torch.bfloat16)
+          for i in range(6)}
+    wq = WeightQuantizer(FP8Config())
+    outs = []
+    for k in range(5):
+        for v in sd.values():  # new values each round, written on the same stream
+            v.mul_(1.5)
+        outs.append((wq.quantize_state_dict(sd), {n: v.clone() for n, v in sd.items()}))
+    torch.cuda.synchronize()
+    for out, src in outs:
+        for n, v in src.items():
+            xb = v.cpu().view(torch.int16).numpy().view(np.uint16)
+            oc, osc = O.fp8_block_quant(xb, "bf16", "f32", (1, 128))
+            assert np.array_equal(bits(out[n]), oc[0]), n
+            want_s = torch.from_numpy(osc[0]).to(torch.bfloat16)
+            assert np.array_equal(bits(out[f"{n}_fp8_scales"]), bits(want_s)), n
