@@ -39,8 +39,13 @@ bool pow2_block(int64_t b) { return b == 32 || b == 64 || b == 128 || b == 256 |
 
 constexpr uint32_t kMagic = 0x4C525154u;  // "LRQT"
 constexpr uint32_t kTableVersion = 1u;
-// HIP takes a launch's thread count (grid x 256 threads) as a 32-bit value
+// HIP takes a launch's thread count (work-groups x threads per work-group) as
+// a 32-bit value.  kMaxGrid is the limit for 256-thread work-groups;
+// max_units() gives it per kernel.
 constexpr int64_t kMaxGrid = 0xFFFFFFFFll / 256;
+int64_t max_units(int kernel) {
+  return 0xFFFFFFFFll / (kernel == lrq::kKernTile128 ? lrq::kTileThreads : 256);
+}
 
 struct GroupHeader {
   uint32_t magic, version;
@@ -195,7 +200,7 @@ int run_single(const LaunchCfg& cfg, Desc& d, hipStream_t stream) {
   if (!lrq::plan_units(cfg, d))
     return fail(LRQ_ERR_ARG, "batch stride must equal rows*ld for this format");
   if (d.units == 0) return 0;
-  if (d.units > kMaxGrid) return fail(LRQ_ERR_ARG, "tensor too large for one launch");
+  if (d.units > max_units(cfg.kernel)) return fail(LRQ_ERR_ARG, "tensor too large for one launch");
   d.unit0 = 0;
   return check_hip(lrq::launch(cfg, d, nullptr, nullptr, d.units, stream), "kernel launch");
 }
@@ -322,7 +327,7 @@ int plan_group(int fmt, const lrq_tensor* ts, int64_t n, int in_dtype, int64_t b
     for (int64_t i = 0; i < n; ++i)
       if (ts[i].cols % blk_c != 0) cfg.rows_dense = 0;
   }
-  if (units > kMaxGrid) return fail(LRQ_ERR_ARG, "group too large for one launch");
+  if (units > max_units(cfg.kernel)) return fail(LRQ_ERR_ARG, "group too large for one launch");
   *cfg_out = cfg;
   *units_out = units;
   return 0;

@@ -120,11 +120,11 @@ __device__ __forceinline__ void store_scale(void* scales, int64_t idx, float s, 
 }
 
 // ---------------------------------------------------------------------------
-// 128x128 tiles, T threads per tile.  Thread t owns column chunk (t & 15) of
-// rows (t >> 4) + (T/16) i: each load instruction of a wave reads 4 full
-// 256-byte rows.  T = 256 (8 loads per thread) for large launches; T = 512 (4
-// loads) when the whole launch fits in one wave of work-groups, where the
-// shorter per-thread chain lowers the latency of a single weight by ~5%.
+// 128x128 tiles, T = kTileThreads threads per tile.  Thread t owns column
+// chunk (t & 15) of rows (t >> 4) + (T/16) i: each load instruction of a wave
+// reads 4 full 256-byte rows.  T = 512 (4 loads per thread) beats 256 (8
+// loads) by 1-4% on large launches and by 5% on a single 4096^2 weight; 1024
+// (2 loads) loses 15% to its 16-wave reduction.
 // ---------------------------------------------------------------------------
 template <int DT, int CDT, int T>
 __global__ __launch_bounds__(T) void k_tile128(Desc single, const Desc* __restrict__ descs,
@@ -185,10 +185,6 @@ __global__ __launch_bounds__(T) void k_tile128(Desc single, const Desc* __restri
       store_nt(d.codes + out_base + (int64_t)(RS * i) * d.cols, q);
   }
 }
-
-// Launches of at most this many tiles run one wave of 512-thread work-groups
-// (two per CU on 256 CUs, fewer loads per thread).
-constexpr int64_t kSmallTileLaunch = 2048;
 
 // ---------------------------------------------------------------------------
 // 1xB row blocks (B = 8*LPB, LPB = 4..64 lanes per block).  The 64 lanes of a
@@ -329,12 +325,8 @@ static hipError_t launch_fp8_typed(const LaunchCfg& cfg, const Desc& single, con
   const dim3 grid((unsigned)units), block(256);
   switch (cfg.kernel) {
     case kKernTile128:
-      if (units <= kSmallTileLaunch)
-        hipLaunchKernelGGL((k_tile128<DT, CDT, 512>), grid, dim3(512), 0, stream, single, descs, map,
-                           cfg.pow2, cfg.scale_bf16);
-      else
-        hipLaunchKernelGGL((k_tile128<DT, CDT, 256>), grid, block, 0, stream, single, descs, map,
-                           cfg.pow2, cfg.scale_bf16);
+      hipLaunchKernelGGL((k_tile128<DT, CDT, kTileThreads>), grid, dim3(kTileThreads), 0, stream, single, descs,
+                         map, cfg.pow2, cfg.scale_bf16);
       break;
     case kKernRowQuad:
       switch (cfg.blk_c) {

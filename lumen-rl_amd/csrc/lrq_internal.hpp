@@ -42,6 +42,7 @@ enum Kernel : int {
 constexpr int64_t kCopyUnit = 4096;  // k_copy: bytes per work-group (one 16 B load per lane)
 constexpr int kDequantChunks = 2;    // k_dequant: 16-byte output chunks per lane (2 beat 1, 4 and 8)
 constexpr int kMxLoads = 2;          // k_mx: 32-element groups per quad of lanes (2 beat 1, 3 and 4)
+constexpr int kTileThreads = 512;    // k_tile128: threads per 128x128 tile (512 beat 256 and 1024)
 constexpr int kRowBlocks = 4;        // k_row: 1xB blocks per lane, sharing one scale computation (4: 2 is 7% slower with bf16 scales, 3 slower with both)
 constexpr int kAmaxLoads = 2;        // k_amax: 16-byte loads per lane (2 beat 1, 3, 4 and 8)
 
