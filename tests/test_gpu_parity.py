@@ -283,6 +283,29 @@ def test_ragged_tiles_and_strided_views():
     assert torch.equal(u8t(c1), u8t(c2)) and torch.equal(s1, s2)
 
 
+def test_tiles_across_tensors_batches_and_edges():
+    """128x128 tiles of a strided batch and of grouped launches whose tensors
+    end in ragged edge tiles (rows or columns short of 128) and hold an inf
+    and a zero row: every tile must match the oracle."""
+    say("tiles: strided batch with ragged tiles")
+    base = weights((3, 256, 272)).to(DEV)
+    assert_fp8_matches_oracle(base[:, :200, :264], (128, 128))    # batch stride != rows * ld
+    say("tiles: grouped ragged tensors")
+    shapes = [(1000, 8), (130, 136), (2, 128, 128), (257, 384), (3, 136, 264), (129, 1032)]
+    ws = [weights(s).to(DEV) for s in shapes]
+    ws[1][129, 135] = float("inf")
+    ws[3][256, :] = 0.0
+    for n in (1, 2, 3, len(ws)):                                   # 8 .. 60 tiles per launch
+        plan = ops.QuantPlan(ws[:n], "fp8_block", (128, 128))
+        plan.run()
+        torch.cuda.synchronize()
+        for w, (c, s) in zip(ws[:n], plan.outputs):
+            xh = host_bits(w)
+            oc, osc = O.fp8_block_quant(xh.reshape((-1,) + xh.shape[-2:]), "bf16", "f32", (128, 128))
+            assert np.array_equal(u8(c).reshape(oc.shape), oc)
+            assert np.array_equal(scale_bits(s).reshape(-1), osc.view(np.uint32).reshape(-1))
+
+
 def u8t(c):
     return c.view(torch.uint8)
 
