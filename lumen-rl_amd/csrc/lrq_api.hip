@@ -320,8 +320,10 @@ int plan_group(int fmt, const lrq_tensor* ts, int64_t n, int in_dtype, int64_t b
     units += d.units;
     if (ds) ds[i] = d;
   }
-  if (kernel < 0 && fmt != LRQ_FMT_TENSOR_SCALE && fmt != LRQ_FMT_COPY)
-    cfg.kernel = fmt == LRQ_FMT_FP8_BLOCK ? lrq::kKernGenericFp8 : lrq::kKernGenericMx;
+  if (kernel < 0 && fmt != LRQ_FMT_TENSOR_SCALE && fmt != LRQ_FMT_COPY)  // only empty tensors
+    cfg.kernel = fmt == LRQ_FMT_FP8_BLOCK     ? lrq::kKernGenericFp8
+                 : fmt == LRQ_FMT_FP8_DEQUANT ? lrq::kKernGenericDequant
+                                              : lrq::kKernGenericMx;
   if (fmt == LRQ_FMT_FP8_DEQUANT) {
     cfg.rows_dense = 1;
     for (int64_t i = 0; i < n; ++i)
@@ -493,6 +495,8 @@ int lrq_tensor_scale_grouped(const void* host_table, const void* device_table, v
 }
 
 int64_t lrq_group_units(const void* host_table) {
+  g_err.clear();
+  if (!host_table) return fail(LRQ_ERR_ARG, "null table");
   GroupHeader h;
   memcpy(&h, host_table, sizeof(h));
   if (h.magic != kMagic || h.version != kTableVersion) return fail(LRQ_ERR_TABLE, "not an lrq table");

@@ -5,7 +5,7 @@
 // clamp(tiny) -> [pow2] -> x/s -> float8_e4m3fn, in one HBM pass (bf16 in,
 // e4m3 + scale out).  Three kernels:
 //   k_tile128  : 128x128 tiles (the vLLM/ATOM `weight_scale_inv` layout), one
-//                256-thread work-group per tile, the tile held in VGPRs;
+//                512-thread work-group per tile, the tile held in VGPRs;
 //                tiles handed to XCDs in runs of kXcdRun (xcd_unit).
 //   k_row      : 1xB row blocks (the reference's own layout), B/8 consecutive
 //                lanes per block so every wave instruction is one contiguous

@@ -240,6 +240,12 @@ def test_copy_tables():
     assert L().lrq_group_table_bytes(fmt, ts, len(sizes), 0, 1, 1, 0) == _lib.ERR_ARG
 
 
+def test_group_units_rejects_null_and_foreign_tables():
+    assert L().lrq_group_units(None) == _lib.ERR_ARG and "null" in _lib.last_error()
+    junk = np.zeros(4096, np.uint8)
+    assert L().lrq_group_units(junk.ctypes.data) == _lib.ERR_TABLE
+
+
 def test_grouped_rejects_foreign_table():
     junk = np.zeros(4096, np.uint8)
     rc = L().lrq_quant_grouped(junk.ctypes.data, ctypes.c_void_p(0x1000), None)
