@@ -276,17 +276,33 @@ class _GroupLaunch:
         # is never overwritten while an earlier launch may still read it.  The
         # copy is from pinned memory and does not block the host (a pageable
         # copy would wait for the stream to drain, serializing plan building,
-        # e.g. every quantize_state_dict call, with the device).  As for any
-        # tensor produced on a stream, a launch on another stream must first
-        # wait for this one.
+        # e.g. every quantize_state_dict call, with the device).
         self.dev = torch.empty(int(need), dtype=torch.uint8, device=device)
         with _on(device):
+            self.home = torch.cuda.current_stream(device)
             self.dev.copy_(self.host, non_blocking=True)
+            self.ready = torch.cuda.Event()
+            self.ready.record(self.home)
         self.device = device
         self.units = int(L.lrq_group_units(self.host.data_ptr()))
+        self.buffers: list[Tensor] = [self.dev]  # device memory the launches touch
+
+    def _enter(self) -> None:
+        """Order a launch on another stream after the table upload, and tell the
+        allocator that stream uses the plan's buffers (so freeing the plan
+        cannot recycle them under a running launch).  Inside a graph capture
+        this is skipped: the upload was ordered by the uncaptured warm-up run
+        that capture requires anyway."""
+        cur = torch.cuda.current_stream(self.device)
+        if cur == self.home or torch.cuda.is_current_stream_capturing():
+            return
+        cur.wait_event(self.ready)
+        for b in self.buffers:
+            b.record_stream(cur)
 
     def run(self) -> None:
         with _on(self.device):
+            self._enter()
             rc = _lib.lib().lrq_quant_grouped(self.host.data_ptr(), self.dev.data_ptr(),
                                               _stream(self.device))
         _lib.check(rc, "lrq_quant_grouped")
@@ -296,6 +312,7 @@ class _GroupLaunch:
 
     def run_tensor_scale(self, workspace: Tensor) -> None:
         with _on(self.device):
+            self._enter()
             rc = _lib.lib().lrq_tensor_scale_grouped(self.host.data_ptr(), self.dev.data_ptr(),
                                                      workspace.data_ptr(), _nbytes(workspace),
                                                      _stream(self.device))
@@ -389,6 +406,8 @@ class QuantPlan:
             nbytes += _nbytes(t) + _nbytes(codes) + _nbytes(scales)
         self.algorithmic_bytes = nbytes
         self._launch = _GroupLaunch(fmt, descs, len(tensors), _IN_DTYPES[dt], (br, bc), flags, dev)
+        if outputs is None:
+            self._launch.buffers += [t for pair in self.outputs for t in pair]
         self.units = self._launch.units
 
     def run(self) -> list[tuple[Tensor, Tensor]]:
@@ -441,6 +460,7 @@ class DequantPlan:
         flags = _lib.FLAG_OUT_BF16 if out_dtype == torch.bfloat16 else 0
         self._launch = _GroupLaunch("fp8_dequant", descs, len(pairs), _IN_DTYPES[sdt], (br, bc),
                                     flags, dev)
+        self._launch.buffers += self.outputs
         self.units = self._launch.units
 
     def run(self) -> list[Tensor]:
@@ -469,7 +489,8 @@ class TensorScalePlan:
             if t.numel() == 0:
                 raise RuntimeError("max(): a per-tensor scale of an empty tensor is undefined")
         n = len(tensors)
-        if out is None:
+        owned = out is None
+        if owned:
             out = torch.empty(n, dtype=torch.float32, device=dev)
         elif out.dtype != torch.float32 or out.shape != (n,) or not out.is_contiguous() or out.device != dev:
             raise ValueError(f"out must be a contiguous float32 [{n}] tensor on {dev}")
@@ -494,6 +515,9 @@ class TensorScalePlan:
         self._launch = _GroupLaunch("tensor_scale", descs, n, _IN_DTYPES[dt], (1, 1), 0, dev)
         self.units = self._launch.units
         self.workspace = torch.empty(self._launch.workspace_bytes(), dtype=torch.uint8, device=dev)
+        self._launch.buffers.append(self.workspace)
+        if owned:
+            self._launch.buffers.append(out)
 
     def run(self) -> Tensor:
         """Enqueue both launches on the current stream; returns ``scales``."""
