@@ -61,9 +61,11 @@ QWEN3_8B = [("q_proj", 4096, 4096), ("k_proj", 1024, 4096), ("v_proj", 1024, 409
 PROFILE_FOR = {"c2": "k_tile128_qwen3_8b_fp8_128x128", "c2r": "k_row_qwen3_8b_fp8_1x128",
                "c3": "k_tile128_qwen3_30b_a3b_experts", "c4": "k_mx_qwen3_8b_mxfp8",
                "c5": "k_mx_qwen3_8b_mxfp4", "c2d": "k_dequant_qwen3_8b_fp8_1x128_to_bf16",
-               "act": "k_act_qdq_qwen3_8b_prefill_8192", "kv": "k_amax_qwen3_8b_qkv_scales"}
+               "act": "k_act_qdq_qwen3_8b_prefill_8192", "kv": "k_amax_qwen3_8b_qkv_scales",
+               "cast": "k_cast_e4m3_qwen3_8b_state_dynamic_weight_loader"}
 KERNEL_FOR = {"c1": "k_tile128", "c2": "k_tile128", "c3": "k_tile128", "c4": "k_mx", "c5": "k_mx",
-              "c2r": "k_row", "c2d": "k_dequant", "act": "k_act_qdq8", "kv": "k_amax", "c2sd": "k_row", "bucket": "k_tile128"}
+              "c2r": "k_row", "c2d": "k_dequant", "act": "k_act_qdq8", "kv": "k_amax", "c2sd": "k_row", "bucket": "k_tile128",
+              "cast": "k_cast_e4m3"}
 PREFILL_TOKENS = 8192
 
 
@@ -179,6 +181,7 @@ def cpu_baseline(torch, ws, fmt, fmt_block, seconds):
         "fp8_dequant": "oracle/torch_ref.py (weight_quantizer.py:79-89 then the bf16 cast of :133)",
         "act": "oracle/torch_ref.py (fp8_rollout.py:53-72 op order)",
         "kv": "oracle/torch_ref.py (fp8_kv_cache.py:52-54 op order, one tensor at a time)",
+        "cast": "torch's own tensor.to(float8_e4m3fn) per tensor, as weight_loader.py:19-43 runs it",
     }.get(fmt, f"the C oracle's {fmt} restatement (the reference has no MX CPU path)")
     return {
         "value": round(done_bytes / t_total / 1e9, 3),
@@ -227,6 +230,11 @@ def _cpu_pass(torch, O, torch_ref, np, ws, fmt, fmt_block, seconds, threads):
             torch_ref.kv_scale(x)
             t_total += time.perf_counter() - t0
             done_bytes += x.numel() * 2 + 4
+        elif fmt == "cast":
+            t0 = time.perf_counter()
+            q = x.to(torch.float8_e4m3fn)  # weight_loader.py:33, the reference's own op
+            t_total += time.perf_counter() - t0
+            done_bytes += x.numel() * 2 + q.numel()
         elif fmt == "act":
             t0 = time.perf_counter()
             out = torch_ref.act_qdq(x, fmt_block[1])
@@ -274,6 +282,23 @@ class _StateDictCall:
 
     def run(self):
         self.out = self.wq.quantize_state_dict(self.sd)
+
+
+class _LoaderCall:
+    """One drop-in DynamicWeightLoader.load_weights call with FP8 on: the whole
+    state's unscaled e4m3 cast (plan, allocations and one grouped launch)."""
+
+    def __init__(self, sd):
+        from lumenrl_amd.engine.inference import DynamicWeightLoader
+
+        self.loader, self.sd = DynamicWeightLoader, sd
+        self.algorithmic_bytes = sum(w.numel() * (w.element_size() + 1) for w in sd.values())
+
+    def update_weights(self, sd):
+        self.out = sd
+
+    def run(self):
+        self.loader.load_weights(self, self.sd, fp8_config={"enabled": True})
 
 
 class _ActCall:
@@ -348,6 +373,15 @@ def run(args):
                  "elements": sum(w.numel() for w in ws),
                  "passthrough_tensors": sum(len(b.copies) for b in writer),
                  "format": "fp8_block_128x128 + passthrough copies", "launches_per_step": len(writer)}
+    elif cfg == "cast":
+        named = qwen3_8b_state(torch, dev, args.seed)
+        plans = [_LoaderCall(dict(named))]
+        ws = [w for _, w in named]
+        workload = "qwen3-8b-state-unscaled-e4m3-cast-dynamic-weight-loader"
+        cpu_ws, cpu_blk, cpu_fmt = ws, (1, 1), "cast"
+        extra = {"tensors": len(named), "layers": 36, "elements": sum(w.numel() for w in ws),
+                 "format": "float8_e4m3fn_unscaled_cast", "launches_per_step": 1,
+                 "host_work_timed": True}
     elif cfg == "kv":
         ws, names = qwen3_8b_set(torch, dev, args.seed, "normal")
         ws = [w for w, nm in zip(ws, names) if nm.split(".")[-1] in ("q_proj", "k_proj", "v_proj")]
@@ -509,7 +543,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--config", default="c2", choices=["c1", "c2", "c3", "c4", "c5", "c2r", "c2d", "c2sd", "bucket", "act", "kv"])
+    ap.add_argument("--config", default="c2", choices=["c1", "c2", "c3", "c4", "c5", "c2r", "c2d", "c2sd", "bucket", "act", "kv", "cast"])
     ap.add_argument("--seed", type=int, default=1000)
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")

@@ -60,6 +60,10 @@ typedef struct ihipStream_t* lrq_stream_t; /* == hipStream_t */
                           NULL); in_dtype must be a valid dtype and is otherwise ignored.
                           The pass-through tensors of a weight-transfer bucket in one
                           launch (bucketed_weight_transfer.py:137-165 copies each) */
+#define LRQ_FMT_CAST_E4M3 6 /* grouped unscaled cast through lrq_quant_grouped (see
+                               lrq_cast_e4m3): lrq_tensor.in = source (in_dtype),
+                               .codes = e4m3fn output, .cols = elements, batch = rows
+                               = 1, .ld = .cols, .scales unused (may be NULL) */
 
 /* errors */
 #define LRQ_ERR_ARG (-1)      /* invalid argument (shape, dtype, block size, null) */
@@ -123,6 +127,17 @@ int lrq_mxfp4_quant(const void* in, int in_dtype, int64_t rows, int64_t cols, in
  */
 int lrq_act_qdq(const void* in, int in_dtype, int64_t rows, int64_t cols, int64_t ld, int64_t blk,
                 unsigned flags, float* out, lrq_stream_t stream);
+
+/*
+ * Unscaled cast of n contiguous elements to float8_e4m3fn, as torch's
+ * `tensor.to(torch.float8_e4m3fn)`: round to nearest even, |x| rounding past
+ * 448, +-inf and NaN -> NaN (0x7F | sign).  Replaces the FP8 path of
+ * DynamicWeightLoader (lumenrl/engine/inference/weight_loader.py:19-43,
+ * `_maybe_fp8_quantize_tensor`); a whole state dict goes through one grouped
+ * launch with LRQ_FMT_CAST_E4M3.  Any alignment; a 16-byte aligned input with
+ * codes aligned to 8 bytes (4 for float32 input) takes the vector path.
+ */
+int lrq_cast_e4m3(const void* in, int in_dtype, int64_t n, uint8_t* out, lrq_stream_t stream);
 
 /*
  * Grouped launch: many tensors (a layer, a whole weight set, or MoE expert

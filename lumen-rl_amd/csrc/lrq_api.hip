@@ -257,6 +257,8 @@ int plan_group(int fmt, const lrq_tensor* ts, int64_t n, int in_dtype, int64_t b
     cfg.kernel = lrq::kKernAmax;
   } else if (fmt == LRQ_FMT_COPY) {
     cfg.kernel = lrq::kKernCopy;
+  } else if (fmt == LRQ_FMT_CAST_E4M3) {
+    cfg.kernel = lrq::kKernCast;
   } else {
     return fail(LRQ_ERR_ARG, "bad format %d", fmt);
   }
@@ -264,8 +266,20 @@ int plan_group(int fmt, const lrq_tensor* ts, int64_t n, int in_dtype, int64_t b
   int64_t units = 0;
   for (int64_t i = 0; i < n; ++i) {
     Desc d;
-    if (int rc = make_desc(ts[i], d, fmt != LRQ_FMT_TENSOR_SCALE, fmt != LRQ_FMT_COPY))
+    if (int rc = make_desc(ts[i], d, fmt != LRQ_FMT_TENSOR_SCALE,
+                           fmt != LRQ_FMT_COPY && fmt != LRQ_FMT_CAST_E4M3))
       return fail(rc, "tensor %lld: %s", (long long)i, g_err.c_str());
+    if (fmt == LRQ_FMT_CAST_E4M3) {
+      if (d.batch > 1 || d.rows > 1 || (d.cols > 0 && d.ld != d.cols))
+        return fail(LRQ_ERR_ARG, "tensor %lld: a cast entry is one contiguous run (batch = rows = 1)", (long long)i);
+      const int64_t es = esize(in_dtype);
+      d.units_c = aligned(d.in, 16) && aligned(d.codes, es == 4 ? 4 : 8) ? 1 : 0;
+      d.units = (d.cols + lrq::kCastUnit - 1) / lrq::kCastUnit;
+      d.unit0 = units;
+      units += d.units;
+      if (ds) ds[i] = d;
+      continue;
+    }
     if (fmt == LRQ_FMT_COPY) {
       if (d.batch > 1 || d.rows > 1 || (d.cols > 0 && d.ld != d.cols))
         return fail(LRQ_ERR_ARG, "tensor %lld: a copy entry is one run of bytes (batch = rows = 1)", (long long)i);
@@ -320,7 +334,8 @@ int plan_group(int fmt, const lrq_tensor* ts, int64_t n, int in_dtype, int64_t b
     units += d.units;
     if (ds) ds[i] = d;
   }
-  if (kernel < 0 && fmt != LRQ_FMT_TENSOR_SCALE && fmt != LRQ_FMT_COPY)  // only empty tensors
+  if (kernel < 0 && fmt != LRQ_FMT_TENSOR_SCALE && fmt != LRQ_FMT_COPY &&
+      fmt != LRQ_FMT_CAST_E4M3)  // only empty tensors
     cfg.kernel = fmt == LRQ_FMT_FP8_BLOCK     ? lrq::kKernGenericFp8
                  : fmt == LRQ_FMT_FP8_DEQUANT ? lrq::kKernGenericDequant
                                               : lrq::kKernGenericMx;
@@ -404,6 +419,20 @@ int lrq_act_qdq(const void* in, int in_dtype, int64_t rows, int64_t cols, int64_
                    "kernel launch");
 }
 
+int lrq_cast_e4m3(const void* in, int in_dtype, int64_t n, uint8_t* out, lrq_stream_t stream) {
+  g_err.clear();
+  lrq_tensor t{in, out, nullptr, 1, 1, n, n, n};
+  LaunchCfg cfg;
+  Desc d;
+  int64_t units;
+  if (n < 0) return fail(LRQ_ERR_ARG, "negative element count");
+  if (int rc = plan_group(LRQ_FMT_CAST_E4M3, &t, 1, in_dtype, 1, 1, 0, &cfg, &d, &units)) return rc;
+  if (units == 0) return 0;
+  d.unit0 = 0;
+  return check_hip(lrq::launch_cast(in_dtype, d, nullptr, nullptr, units, (hipStream_t)stream),
+                   "kernel launch");
+}
+
 int64_t lrq_group_table_bytes(int fmt, const lrq_tensor* tensors, int64_t n, int in_dtype,
                               int64_t blk_r, int64_t blk_c, unsigned flags) {
   g_err.clear();
@@ -460,6 +489,9 @@ int lrq_quant_grouped(const void* host_table, const void* device_table, lrq_stre
     return check_hip(lrq::launch_copy(descs, map, h.units, (hipStream_t)stream), "kernel launch");
   Desc dummy;
   memset(&dummy, 0, sizeof(dummy));
+  if (h.cfg.kernel == lrq::kKernCast)
+    return check_hip(lrq::launch_cast(h.cfg.in_dtype, dummy, descs, map, h.units, (hipStream_t)stream),
+                     "kernel launch");
   return check_hip(lrq::launch(h.cfg, dummy, descs, map, h.units, (hipStream_t)stream), "kernel launch");
 }
 

@@ -35,6 +35,7 @@ enum Kernel : int {
   kKernGenericDequant = 6, // FP8 dequant, one element per thread
   kKernAmax = 7,           // per-tensor max |x| partials + scale (two launches)
   kKernCopy = 8,           // grouped byte copy (bucket pass-through tensors)
+  kKernCast = 9,           // grouped unscaled cast to float8_e4m3fn
 };
 
 // Work per lane of the streaming kernels, shared by the kernels and the
@@ -44,6 +45,8 @@ constexpr int kDequantChunks = 2;    // k_dequant: 16-byte output chunks per lan
 constexpr int kMxLoads = 2;          // k_mx: 32-element groups per quad of lanes (2 beat 1, 3 and 4)
 constexpr int kTileThreads = 512;    // k_tile128: threads per 128x128 tile (512 beat 256 and 1024)
 constexpr int kRowBlocks = 4;        // k_row: 1xB blocks per lane, sharing one scale computation (4: 2 is 7% slower with bf16 scales, 3 slower with both)
+constexpr int kCastLaneElems = 16;   // k_cast_e4m3: elements per lane
+constexpr int64_t kCastUnit = 256 * kCastLaneElems;  // k_cast_e4m3: elements per work-group
 constexpr int kAmaxLoads = 2;        // k_amax: 16-byte loads per lane (2 beat 1, 3, 4 and 8)
 
 // Descriptor and local work unit of this work-group: the single-tensor
@@ -96,6 +99,8 @@ hipError_t launch_tensor_scale(const LaunchCfg& cfg, const Desc* descs, const ui
 
 // Grouped byte copy over `units` work-groups.
 hipError_t launch_copy(const Desc* descs, const uint32_t* map, int64_t units, hipStream_t stream);
+hipError_t launch_cast(int dtype, const Desc& single, const Desc* descs, const uint32_t* map,
+                       int64_t units, hipStream_t stream);
 
 // Activation fake-quant.
 int64_t act_grid(const void* in, int dtype, int64_t rows, int64_t cols, int64_t ld);

@@ -202,6 +202,21 @@ def act_qdq(x: Tensor, block: int = 128, *, pow2: bool = False,
     return out
 
 
+def cast_e4m3(x: Tensor) -> Tensor:
+    """``x.to(torch.float8_e4m3fn)`` on the device, unscaled (weight_loader.py:19-43):
+    round to nearest even; |x| rounding past 448, +-inf and NaN give NaN."""
+    _check_input(x, "cast_e4m3")
+    xc = x.contiguous()
+    out = torch.empty(x.shape, dtype=torch.float8_e4m3fn, device=x.device)
+    if x.numel() == 0:
+        return out
+    with _on(x.device):
+        rc = _lib.lib().lrq_cast_e4m3(xc.data_ptr(), _IN_DTYPES[x.dtype], xc.numel(),
+                                      out.data_ptr(), _stream(x.device))
+    _lib.check(rc, "lrq_cast_e4m3")
+    return out
+
+
 def _mx(x: Tensor, fmt: int) -> tuple[Tensor, Tensor]:
     _check_input(x, "mx quantize")
     if x.dim() < 1 or x.shape[-1] % 32 != 0:
@@ -254,7 +269,7 @@ def quantize_fp8_blockwise(x: Tensor, block_size: tuple[int, int] = (128, 128), 
 # ---------------------------------------------------------------------------
 _FMTS = {"fp8_block": _lib.FMT_FP8_BLOCK, "mxfp8": _lib.FMT_MXFP8, "mxfp4": _lib.FMT_MXFP4,
          "fp8_dequant": _lib.FMT_FP8_DEQUANT, "tensor_scale": _lib.FMT_TENSOR_SCALE,
-         "copy": _lib.FMT_COPY}
+         "copy": _lib.FMT_COPY, "cast_e4m3": _lib.FMT_CAST_E4M3}
 
 
 class _GroupLaunch:
@@ -557,6 +572,44 @@ class CopyPlan:
 
     def run(self) -> None:
         self._launch.run()
+
+
+class CastPlan:
+    """One launch that casts many tensors to float8_e4m3fn, unscaled.
+
+    ``tensors`` are contiguous device tensors of one dtype (bf16, fp16 or
+    float32); ``outputs`` are float8_e4m3fn tensors of the same shapes, made
+    by the plan.  ``run()`` recasts whatever the inputs currently hold.
+    """
+
+    def __init__(self, tensors: Sequence[Tensor]) -> None:
+        if not tensors:
+            raise ValueError("CastPlan needs at least one tensor")
+        dt, dev = tensors[0].dtype, tensors[0].device
+        descs = (_lib.LrqTensor * len(tensors))()
+        self.inputs = list(tensors)
+        self.outputs: list[Tensor] = []
+        nbytes = 0
+        for i, t in enumerate(tensors):
+            _check_input(t, "CastPlan")
+            if t.dtype != dt or t.device != dev or not t.is_contiguous():
+                raise ValueError(f"tensor {i}: CastPlan needs contiguous {dt} tensors on {dev}")
+            out = torch.empty(t.shape, dtype=torch.float8_e4m3fn, device=dev)
+            self.outputs.append(out)
+            descs[i].in_ = t.data_ptr()
+            descs[i].codes = out.data_ptr()
+            descs[i].scales = None
+            descs[i].batch, descs[i].rows, descs[i].cols = 1, 1, t.numel()
+            descs[i].ld, descs[i].batch_stride = t.numel(), t.numel()
+            nbytes += _nbytes(t) + _nbytes(out)
+        self.algorithmic_bytes = nbytes
+        self._launch = _GroupLaunch("cast_e4m3", descs, len(tensors), _IN_DTYPES[dt], (1, 1), 0, dev)
+        self._launch.buffers += self.outputs
+        self.units = self._launch.units
+
+    def run(self) -> list[Tensor]:
+        self._launch.run()
+        return self.outputs
 
 
 def _prod(shape) -> int:

@@ -154,6 +154,20 @@ def e4m3_from_f32(x: np.ndarray) -> np.ndarray:
     return out
 
 
+def cast_e4m3(x: np.ndarray, dtype: str = "bf16") -> np.ndarray:
+    """Unscaled ``tensor.to(torch.float8_e4m3fn)`` of DynamicWeightLoader
+    (lumenrl/engine/inference/weight_loader.py:19-43): widen to float32 (exact
+    for bf16/fp16), then the e4m3fn encoder (RNE; past 448, inf, NaN -> 0x7F|sign)."""
+    x = _as_input(x, dtype)
+    if dtype == "bf16":
+        f = bf16_bits_to_f32(x)
+    elif dtype == "f16":
+        f = x.view(np.float16).astype(np.float32)
+    else:
+        f = x
+    return e4m3_from_f32(f)
+
+
 def e4m3_from_f32_bits_range(start: int, n: int) -> np.ndarray:
     out = np.empty(n, np.uint8)
     lib().lrqo_f32_to_e4m3_bits_range(start, n, _ptr(out))

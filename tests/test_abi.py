@@ -246,6 +246,38 @@ def test_group_units_rejects_null_and_foreign_tables():
     assert L().lrq_group_units(junk.ctypes.data) == _lib.ERR_TABLE
 
 
+def test_cast_tables():
+    """Unscaled e4m3 cast tables: one contiguous run per tensor, 4096 elements
+    per work-group; the vector path needs a 16-byte aligned input and codes
+    aligned to one chunk (8 bytes for 16-bit input, 4 for float32)."""
+    fmt = _lib.FMT_CAST_E4M3
+    ts = _tensors([(1, 1, 10000), (1, 1, 4096), (1, 1, 7), (1, 1, 0)])
+    for i, t in enumerate(ts):
+        t.in_, t.codes, t.scales = 0x200000000 + i * 0x100000, 0x300000000 + i * 0x100000, None
+    ts[1].codes = ts[1].codes + 4  # codes only 4-byte aligned: element walk for bf16
+    need = L().lrq_group_table_bytes(fmt, ts, 4, 0, 1, 1, 0)
+    assert need > 0, _lib.last_error()
+    buf = np.zeros(need, np.uint8)
+    assert L().lrq_group_pack(fmt, ts, 4, 0, 1, 1, 0, buf.ctypes.data, need) == 0, _lib.last_error()
+    assert L().lrq_group_units(buf.ctypes.data) == 3 + 1 + 1 + 0
+    descs = buf[256:256 + 4 * 112].view(np.int64).reshape(4, 14)  # 112-byte descriptors
+    assert descs[:3, 10].tolist() == [1, 0, 1]  # vector-path flag (units_c)
+    assert descs[:, 9].tolist() == [3, 1, 1, 0]   # work-groups per tensor
+    # float32 input: 4-byte aligned codes are enough
+    need32 = L().lrq_group_table_bytes(fmt, ts, 2, _lib.DTYPE_F32, 1, 1, 0)
+    buf32 = np.zeros(need32, np.uint8)
+    assert L().lrq_group_pack(fmt, ts, 2, _lib.DTYPE_F32, 1, 1, 0, buf32.ctypes.data, need32) == 0
+    assert buf32[256:256 + 2 * 112].view(np.int64).reshape(2, 14)[:, 10].tolist() == [1, 1]
+    # a cast entry is one run; the single-tensor call checks its arguments first
+    ts2 = _tensors([(1, 4, 64)])
+    assert L().lrq_group_table_bytes(fmt, ts2, 1, 0, 1, 1, 0) == _lib.ERR_ARG
+    fake = ctypes.c_void_p(0x10000)
+    assert L().lrq_cast_e4m3(fake, 0, -1, fake, None) == _lib.ERR_ARG
+    assert L().lrq_cast_e4m3(None, 0, 16, fake, None) == _lib.ERR_ARG
+    assert L().lrq_cast_e4m3(fake, 5, 16, fake, None) == _lib.ERR_ARG
+    assert L().lrq_cast_e4m3(None, 0, 0, None, None) == 0  # nothing to do, no launch
+
+
 def test_grouped_rejects_foreign_table():
     junk = np.zeros(4096, np.uint8)
     rc = L().lrq_quant_grouped(junk.ctypes.data, ctypes.c_void_p(0x1000), None)

@@ -68,6 +68,23 @@ def test_encoders_exhaustive_vs_torch_casts():
     assert bad == {"e4m3": 0, "bf16": 0, "f16": 0}
 
 
+def test_cast_e4m3_every_16bit_pattern_vs_torch():
+    """DynamicWeightLoader's unscaled cast: every bf16 and every fp16 bit
+    pattern (NaN, inf, subnormal, overflow past 448 included) and random
+    float32 patterns against torch's own .to(float8_e4m3fn)."""
+    b = np.arange(1 << 16, dtype=np.uint32).astype(np.uint16)
+    for dt, tdt in (("bf16", torch.bfloat16), ("f16", torch.float16)):
+        t = torch.from_numpy(b.view(np.int16)).view(tdt)
+        want = t.to(torch.float8_e4m3fn).view(torch.uint8).numpy()
+        assert np.array_equal(O.cast_e4m3(b, dt), want), dt
+    f = RNG.integers(0, 1 << 32, 1 << 20, dtype=np.uint64).astype(np.uint32).view(np.float32)
+    f[:6] = [464.0, 464.00003, -480.0, 0.0009765625, np.inf, np.nan]
+    want = torch.from_numpy(f).to(torch.float8_e4m3fn).view(torch.uint8).numpy()
+    assert np.array_equal(O.cast_e4m3(f, "f32"), want)
+    # the rounding boundary past the largest code: 464 ties to 448, above is NaN
+    assert O.cast_e4m3(np.float32([464.0, 464.00003]), "f32").tolist() == [0x7E, 0x7F]
+
+
 def test_e4m3_decode_all_codes_vs_torch():
     codes = np.arange(256, dtype=np.uint8)
     want = torch.from_numpy(codes).view(torch.float8_e4m3fn).float().numpy().view(np.uint32)
