@@ -22,6 +22,7 @@ int lrqo_mx_quant(const void* in, int in_dtype, int64_t rows, int64_t cols, int6
 int lrqo_act_qdq(const void* in, int in_dtype, int64_t rows, int64_t cols, int64_t blk, int pow2,
                  float* out, int nthreads);
 uint32_t lrqo_tensor_scale(const void* in, int in_dtype, int64_t n);
+void lrqo_f32_to_e4m3_n(const float* in, uint8_t* out, int64_t n);
 }
 
 #define HIP(x)                                                                  \
@@ -203,7 +204,43 @@ int main() {
     HIP(hipFree(dsc));
   }
 
-  // 6. argument errors come back as codes with a message, not as faults
+  // 6. unscaled e4m3 cast of tensor 1 (x 300, so values pass 448 -> NaN) and of an
+  //    odd-length, 2-byte-offset slice of it (element-wise path and tail)
+  {
+    const int64_t n = R[1] * C[1];
+    std::vector<uint16_t> hx((size_t)n);
+    std::vector<float> fx((size_t)n);
+    for (int64_t i = 0; i < n; ++i) {
+      uint32_t b = (uint32_t)hw[1][(size_t)i] << 16;
+      float f;
+      memcpy(&f, &b, 4);
+      f *= 300.0f;
+      memcpy(&b, &f, 4);
+      hx[(size_t)i] = (uint16_t)((b + 0x7FFFu + ((b >> 16) & 1u)) >> 16);
+      b = (uint32_t)hx[(size_t)i] << 16;
+      memcpy(&fx[(size_t)i], &b, 4);
+    }
+    void* dx;
+    uint8_t* dq;
+    HIP(hipMalloc(&dx, (size_t)n * 2));
+    HIP(hipMalloc(&dq, (size_t)n));
+    HIP(hipMemcpy(dx, hx.data(), (size_t)n * 2, hipMemcpyHostToDevice));
+    std::vector<uint8_t> want((size_t)n), got((size_t)n);
+    lrqo_f32_to_e4m3_n(fx.data(), want.data(), n);
+    LRQ(lrq_cast_e4m3(dx, LRQ_DTYPE_BF16, n, dq, (lrq_stream_t)st));
+    HIP(hipStreamSynchronize(st));
+    HIP(hipMemcpy(got.data(), dq, (size_t)n, hipMemcpyDeviceToHost));
+    expect(memcmp(got.data(), want.data(), (size_t)n) == 0, "lrq_cast_e4m3 (vector path)");
+    const int64_t m = n - 1001;
+    LRQ(lrq_cast_e4m3(static_cast<uint16_t*>(dx) + 1, LRQ_DTYPE_BF16, m, dq, (lrq_stream_t)st));
+    HIP(hipStreamSynchronize(st));
+    HIP(hipMemcpy(got.data(), dq, (size_t)m, hipMemcpyDeviceToHost));
+    expect(memcmp(got.data(), want.data() + 1, (size_t)m) == 0, "lrq_cast_e4m3 (offset, odd length)");
+    HIP(hipFree(dq));
+    HIP(hipFree(dx));
+  }
+
+  // 7. argument errors come back as codes with a message, not as faults
   {
     const int rc = lrq_fp8_block_quant(dw[0], LRQ_DTYPE_BF16, 1, R[0], C[0], C[0] - 1, R[0] * C[0], 128, 128,
                                        dcodes[0], dscales[0], 0, (lrq_stream_t)st);
