@@ -62,10 +62,11 @@ PROFILE_FOR = {"c2": "k_tile128_qwen3_8b_fp8_128x128", "c2r": "k_row_qwen3_8b_fp
                "c3": "k_tile128_qwen3_30b_a3b_experts", "c4": "k_mx_qwen3_8b_mxfp8",
                "c5": "k_mx_qwen3_8b_mxfp4", "c2d": "k_dequant_qwen3_8b_fp8_1x128_to_bf16",
                "act": "k_act_qdq_qwen3_8b_prefill_8192", "kv": "k_amax_qwen3_8b_qkv_scales",
-               "cast": "k_cast_e4m3_qwen3_8b_state_dynamic_weight_loader"}
+               "cast": "k_cast_e4m3_qwen3_8b_state_dynamic_weight_loader",
+               "c4d": "k_mx_dequant_qwen3_8b_mxfp8_to_bf16"}
 KERNEL_FOR = {"c1": "k_tile128", "c2": "k_tile128", "c3": "k_tile128", "c4": "k_mx", "c5": "k_mx",
               "c2r": "k_row", "c2d": "k_dequant", "act": "k_act_qdq8", "kv": "k_amax", "c2sd": "k_row", "bucket": "k_tile128",
-              "cast": "k_cast_e4m3"}
+              "cast": "k_cast_e4m3", "c4d": "k_mx_dequant"}
 PREFILL_TOKENS = 8192
 
 
@@ -182,6 +183,7 @@ def cpu_baseline(torch, ws, fmt, fmt_block, seconds):
         "act": "oracle/torch_ref.py (fp8_rollout.py:53-72 op order)",
         "kv": "oracle/torch_ref.py (fp8_kv_cache.py:52-54 op order, one tensor at a time)",
         "cast": "torch's own tensor.to(float8_e4m3fn) per tensor, as weight_loader.py:19-43 runs it",
+        "mx_dequant": "oracle/torch_ref.py mx_dequant (torch decode, E8M0 widen, product, bf16 cast)",
     }.get(fmt, f"the C oracle's {fmt} restatement (the reference has no MX CPU path)")
     return {
         "value": round(done_bytes / t_total / 1e9, 3),
@@ -214,6 +216,16 @@ def _cpu_pass(torch, O, torch_ref, np, ws, fmt, fmt_block, seconds, threads):
     n = 0
     t_total = 0.0
     for w in ws:
+        if fmt == "mx_dequant":
+            c, sc = w[0].cpu(), w[1].cpu()
+            t0 = time.perf_counter()
+            out = torch_ref.mx_dequant(c, sc, 8, torch.bfloat16)
+            t_total += time.perf_counter() - t0
+            done_bytes += c.numel() + sc.numel() + out.numel() * 2
+            n += 1
+            if t_total >= seconds:
+                break
+            continue
         if fmt == "fp8_dequant":
             c, sc = w[0].cpu(), w[1].cpu()
             t0 = time.perf_counter()
@@ -339,6 +351,18 @@ def run(args):
         cpu_ws, cpu_blk, cpu_fmt = pairs, (1, 128), "fp8_dequant"
         extra = {"tensors": len(pairs), "layers": 36, "elements": sum(c.numel() for c, _ in pairs),
                  "format": "fp8_dequant", "launches_per_step": 1}
+    elif cfg == "c4d":
+        ws, _ = qwen3_8b_set(torch, dev, args.seed, "student_t")
+        qp = ops.QuantPlan(ws, "mxfp8", (1, 32))
+        pairs = qp.run()
+        torch.cuda.synchronize()
+        del ws
+        plans = [ops.DequantPlan(pairs, (1, 32), torch.bfloat16, fmt="mxfp8")]
+        ws = [c for c, _ in pairs]
+        workload = "qwen3-8b-linears-mxfp8-dequant-to-bf16"
+        cpu_ws, cpu_blk, cpu_fmt = pairs, (1, 32), "mx_dequant"
+        extra = {"tensors": len(pairs), "layers": 36, "elements": sum(c.numel() for c, _ in pairs),
+                 "format": "mxfp8_dequant", "launches_per_step": 1}
     elif cfg in ("c2", "c4", "c5", "c2r"):
         kind = {"c2": "normal", "c4": "student_t", "c5": "rowscale", "c2r": "normal"}[cfg]
         fmt = {"c2": "fp8_block", "c4": "mxfp8", "c5": "mxfp4", "c2r": "fp8_block"}[cfg]
@@ -543,7 +567,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--config", default="c2", choices=["c1", "c2", "c3", "c4", "c5", "c2r", "c2d", "c2sd", "bucket", "act", "kv", "cast"])
+    ap.add_argument("--config", default="c2", choices=["c1", "c2", "c3", "c4", "c5", "c2r", "c2d", "c2sd", "bucket", "act", "kv", "cast", "c4d"])
     ap.add_argument("--seed", type=int, default=1000)
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")

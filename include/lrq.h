@@ -60,6 +60,12 @@ typedef struct ihipStream_t* lrq_stream_t; /* == hipStream_t */
                           NULL); in_dtype must be a valid dtype and is otherwise ignored.
                           The pass-through tensors of a weight-transfer bucket in one
                           launch (bucketed_weight_transfer.py:137-165 copies each) */
+#define LRQ_FMT_MXFP8_DEQUANT 7 /* grouped MX dequant through lrq_quant_grouped (see
+                                   lrq_mx_dequant): lrq_tensor.in = codes, .codes =
+                                   output, .scales = E8M0 bytes; dense [batch, rows,
+                                   cols] with cols % 32 == 0; LRQ_FLAG_OUT_BF16 = bf16
+                                   output; in_dtype must be a valid dtype, else unused */
+#define LRQ_FMT_MXFP4_DEQUANT 8
 #define LRQ_FMT_CAST_E4M3 6 /* grouped unscaled cast through lrq_quant_grouped (see
                                lrq_cast_e4m3): lrq_tensor.in = source (in_dtype),
                                .codes = e4m3fn output, .cols = elements, batch = rows
@@ -138,6 +144,24 @@ int lrq_act_qdq(const void* in, int in_dtype, int64_t rows, int64_t cols, int64_
  * codes aligned to 8 bytes (4 for float32 input) takes the vector path.
  */
 int lrq_cast_e4m3(const void* in, int in_dtype, int64_t n, uint8_t* out, lrq_stream_t stream);
+
+/*
+ * MX dequantization, the inverse of lrq_mxfp8_quant / lrq_mxfp4_quant:
+ * out = element * 2^(E-127) per 1x32 group (OCP MX v1.0), evaluated as torch's
+ * codes.float() * scales.view(float8_e8m0fnu).float() on x86 (E8M0 0xFF is
+ * NaN and propagates; a NaN e4m3 code keeps its sign), then out_dtype
+ * (LRQ_DTYPE_F32, or LRQ_DTYPE_BF16 rounded to nearest even).  No reference
+ * function (the reference hands MX weights to absent vLLM/aiter loaders:
+ * examples/Qwen3_8B_SDDD_MI350_vLLM/configs/opd_qwen3_8b.yaml:43); the
+ * receiving side's view of what the quantizer sent.
+ *   fmt   : LRQ_FMT_MXFP8 (codes [rows, cols]) or LRQ_FMT_MXFP4 (codes
+ *           [rows, cols/2], element 2i in the low nibble);
+ *   scales: [rows, cols/32] E8M0;  out: dense [rows, cols], 16-byte aligned;
+ *   codes aligned to one lane-chunk of codes (MXFP8: 8 bytes for bf16 output,
+ *   4 for fp32; MXFP4: 4 and 2).
+ */
+int lrq_mx_dequant(int fmt, const uint8_t* codes, const uint8_t* scales, int64_t rows,
+                   int64_t cols, void* out, int out_dtype, lrq_stream_t stream);
 
 /*
  * Grouped launch: many tensors (a layer, a whole weight set, or MoE expert

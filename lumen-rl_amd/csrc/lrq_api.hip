@@ -185,6 +185,8 @@ bool plan_units(const LaunchCfg& cfg, Desc& d) {
 
 hipError_t launch(const LaunchCfg& cfg, const Desc& single, const Desc* descs_dev,
                   const uint32_t* map_dev, int64_t total_units, hipStream_t stream) {
+  if (cfg.kernel == kKernMxDequant)
+    return launch_mx_dequant(cfg, single, descs_dev, map_dev, total_units, stream);
   if (cfg.kernel == kKernMx || cfg.kernel == kKernGenericMx)
     return launch_mx(cfg, single, descs_dev, map_dev, total_units, stream);
   if (cfg.kernel == kKernDequant || cfg.kernel == kKernGenericDequant)
@@ -259,6 +261,10 @@ int plan_group(int fmt, const lrq_tensor* ts, int64_t n, int in_dtype, int64_t b
     cfg.kernel = lrq::kKernCopy;
   } else if (fmt == LRQ_FMT_CAST_E4M3) {
     cfg.kernel = lrq::kKernCast;
+  } else if (fmt == LRQ_FMT_MXFP8_DEQUANT || fmt == LRQ_FMT_MXFP4_DEQUANT) {
+    cfg.kernel = lrq::kKernMxDequant;
+    cfg.mx_fmt = fmt == LRQ_FMT_MXFP8_DEQUANT ? 8 : 4;
+    cfg.out_dtype = (flags & LRQ_FLAG_OUT_BF16) ? lrq::kBF16 : lrq::kF32;
   } else {
     return fail(LRQ_ERR_ARG, "bad format %d", fmt);
   }
@@ -269,6 +275,28 @@ int plan_group(int fmt, const lrq_tensor* ts, int64_t n, int in_dtype, int64_t b
     if (int rc = make_desc(ts[i], d, fmt != LRQ_FMT_TENSOR_SCALE,
                            fmt != LRQ_FMT_COPY && fmt != LRQ_FMT_CAST_E4M3))
       return fail(rc, "tensor %lld: %s", (long long)i, g_err.c_str());
+    if (cfg.kernel == lrq::kKernMxDequant) {
+      if (d.batch == 0 || d.rows == 0 || d.cols == 0) {
+        d.unit0 = units;
+        d.units = 0;
+        if (ds) ds[i] = d;
+        continue;
+      }
+      if (d.ld != d.cols || d.bstride != d.rows * d.cols)
+        return fail(LRQ_ERR_ARG, "tensor %lld: MX dequant needs dense codes (ld == cols)", (long long)i);
+      if (d.cols % 32 != 0) return fail(LRQ_ERR_ARG, "tensor %lld: cols %% 32 != 0", (long long)i);
+      const int64_t cpc = cfg.out_dtype == lrq::kBF16 ? 8 : 4;  // elements per lane-chunk
+      const int64_t cb = cfg.mx_fmt == 8 ? cpc : cpc / 2;       // code bytes per lane-chunk
+      if (!aligned(d.in, (uintptr_t)cb) || !aligned(d.codes, 16))
+        return fail(LRQ_ERR_ALIGN, "tensor %lld: MX dequant needs codes aligned to %lld bytes and a "
+                    "16-byte aligned output", (long long)i, (long long)cb);
+      d.nblocks = d.batch * d.rows * d.cols / cpc;
+      d.units = (d.nblocks + 256 * lrq::kDequantChunks - 1) / (256 * lrq::kDequantChunks);
+      d.unit0 = units;
+      units += d.units;
+      if (ds) ds[i] = d;
+      continue;
+    }
     if (fmt == LRQ_FMT_CAST_E4M3) {
       if (d.batch > 1 || d.rows > 1 || (d.cols > 0 && d.ld != d.cols))
         return fail(LRQ_ERR_ARG, "tensor %lld: a cast entry is one contiguous run (batch = rows = 1)", (long long)i);
@@ -335,7 +363,7 @@ int plan_group(int fmt, const lrq_tensor* ts, int64_t n, int in_dtype, int64_t b
     if (ds) ds[i] = d;
   }
   if (kernel < 0 && fmt != LRQ_FMT_TENSOR_SCALE && fmt != LRQ_FMT_COPY &&
-      fmt != LRQ_FMT_CAST_E4M3)  // only empty tensors
+      fmt != LRQ_FMT_CAST_E4M3 && cfg.kernel != lrq::kKernMxDequant)  // only empty tensors
     cfg.kernel = fmt == LRQ_FMT_FP8_BLOCK     ? lrq::kKernGenericFp8
                  : fmt == LRQ_FMT_FP8_DEQUANT ? lrq::kKernGenericDequant
                                               : lrq::kKernGenericMx;
@@ -431,6 +459,25 @@ int lrq_cast_e4m3(const void* in, int in_dtype, int64_t n, uint8_t* out, lrq_str
   d.unit0 = 0;
   return check_hip(lrq::launch_cast(in_dtype, d, nullptr, nullptr, units, (hipStream_t)stream),
                    "kernel launch");
+}
+
+int lrq_mx_dequant(int fmt, const uint8_t* codes, const uint8_t* scales, int64_t rows,
+                   int64_t cols, void* out, int out_dtype, lrq_stream_t stream) {
+  g_err.clear();
+  if (fmt != LRQ_FMT_MXFP8 && fmt != LRQ_FMT_MXFP4) return fail(LRQ_ERR_ARG, "bad MX format %d", fmt);
+  if (out_dtype != lrq::kF32 && out_dtype != lrq::kBF16) return fail(LRQ_ERR_ARG, "bad out dtype %d", out_dtype);
+  int64_t mstride;
+  if (__builtin_mul_overflow(rows, cols, &mstride)) return fail(LRQ_ERR_ARG, "extents exceed 2^48 elements");
+  lrq_tensor t{codes, out, const_cast<uint8_t*>(scales), 1, rows, cols, cols, mstride};
+  LaunchCfg cfg;
+  Desc d;
+  int64_t units;
+  const int gfmt = fmt == LRQ_FMT_MXFP8 ? LRQ_FMT_MXFP8_DEQUANT : LRQ_FMT_MXFP4_DEQUANT;
+  const unsigned flags = out_dtype == lrq::kBF16 ? LRQ_FLAG_OUT_BF16 : 0u;
+  if (int rc = plan_group(gfmt, &t, 1, lrq::kBF16, 1, 32, flags, &cfg, &d, &units)) return rc;
+  if (units == 0) return 0;
+  d.unit0 = 0;
+  return check_hip(lrq::launch(cfg, d, nullptr, nullptr, units, (hipStream_t)stream), "kernel launch");
 }
 
 int64_t lrq_group_table_bytes(int fmt, const lrq_tensor* tensors, int64_t n, int in_dtype,

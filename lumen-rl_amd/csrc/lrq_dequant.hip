@@ -169,6 +169,129 @@ hipError_t launch_dequant(const LaunchCfg& cfg, const Desc& single, const Desc* 
 }
 
 // ---------------------------------------------------------------------------
+// MX dequantization (OCP MX v1.0): element * 2^(E-127) per 1x32 group, E8M0
+// 0xFF = NaN, in float32 as torch evaluates codes.float() * scales.float()
+// (float8_e8m0fnu: E = 0 is the subnormal 2^-127, 0xFF the signalling NaN
+// 0x7F800001).  Vectorized x86 body, code first: a NaN e4m3 code keeps its
+// 0x7FF00000 | sign; otherwise a NaN scale propagates quieted.  Every other
+// product is exact -- four significant bits times a power of two, 2^-136 at
+// the smallest -- except 448 * 2^127 and above, which overflow to inf.
+// A lane-chunk is CPC elements (8 for bf16 output, 4 for fp32) whose output is
+// one 16-byte store; cols % 32 == 0 puts every chunk inside one group.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ float e8m0_to_f32(uint32_t e) {
+  return e == 0xFFu ? u2f(0x7F800001u) : e == 0u ? u2f(0x00400000u) : u2f(e << 23);
+}
+
+__device__ __forceinline__ float mx_mul(float v, float s) {
+  if ((f2u(v) & 0x7FFFFFFFu) > 0x7F800000u) return v;
+  if ((f2u(s) & 0x7FFFFFFFu) > 0x7F800000u) return u2f(f2u(s) | 0x00400000u);
+  return v * s;
+}
+
+// E2M1 nibble -> float: {0, 0.5, 1, 1.5, 2, 3, 4, 6} with the sign bit.
+__device__ __forceinline__ float e2m1_decode(uint32_t n) {
+  const uint32_t e = (n >> 1) & 3u, m = n & 1u;
+  const uint32_t b = e ? ((126u + e) << 23) | (m << 22) : (m ? 0x3F000000u : 0u);
+  return u2f(b | ((n & 8u) << 28));
+}
+
+template <int FMT, int ODT>
+__global__ __launch_bounds__(256) void k_mx_dequant(Desc single, const Desc* __restrict__ descs,
+                                                    const uint32_t* __restrict__ map) {
+  constexpr int CPC = ODT == kBF16 ? 8 : 4;      // elements per lane-chunk
+  constexpr int CB = FMT == 8 ? CPC : CPC / 2;   // code bytes per lane-chunk
+  constexpr int NCH = kDequantChunks;
+  Desc d;
+  int64_t u;
+  pick_desc(single, descs, map, d, u);
+  const int tid = threadIdx.x;
+  const uint8_t* codes = static_cast<const uint8_t*>(d.in);
+  const uint8_t* sc = static_cast<const uint8_t*>(d.scales);
+  uint32_t cw[NCH][2];
+  uint32_t ex[NCH];
+  bool ok[NCH];
+#pragma unroll
+  for (int j = 0; j < NCH; ++j) {
+    const int64_t ch = u * (256 * NCH) + j * 256 + tid;
+    ok[j] = ch < d.nblocks;
+    if (!ok[j]) continue;
+    const uint8_t* p = codes + ch * CB;
+    if constexpr (CB == 8) {
+      const v2u v = __builtin_nontemporal_load(reinterpret_cast<const v2u*>(p));
+      cw[j][0] = v.x;
+      cw[j][1] = v.y;
+    } else if constexpr (CB == 4) {
+      cw[j][0] = __builtin_nontemporal_load(reinterpret_cast<const uint32_t*>(p));
+    } else {
+      cw[j][0] = __builtin_nontemporal_load(reinterpret_cast<const uint16_t*>(p));
+    }
+    ex[j] = sc[(ch * CPC) >> 5];
+  }
+#pragma unroll
+  for (int j = 0; j < NCH; ++j) {
+    if (!ok[j]) continue;
+    const int64_t ch = u * (256 * NCH) + j * 256 + tid;
+    const float s = e8m0_to_f32(ex[j]);
+    float o[CPC];
+    bool fast = ex[j] != 0xFFu;
+    if constexpr (FMT == 8) {
+#pragma unroll
+      for (int q = 0; q < CPC / 4; ++q) fast = fast && !word_has_nan_code(cw[j][q]);
+      if (fast) {
+#pragma unroll
+        for (int q = 0; q < CPC / 4; ++q) {
+          const f32x2 lo = e4m3x2_to_f32<false>(cw[j][q]), hi = e4m3x2_to_f32<true>(cw[j][q]);
+          o[4 * q + 0] = lo.x * s;
+          o[4 * q + 1] = lo.y * s;
+          o[4 * q + 2] = hi.x * s;
+          o[4 * q + 3] = hi.y * s;
+        }
+      } else {
+#pragma unroll
+        for (int k = 0; k < CPC; ++k) o[k] = mx_mul(e4m3_decode((cw[j][k >> 2] >> (8 * (k & 3))) & 0xFFu), s);
+      }
+    } else {
+#pragma unroll
+      for (int k = 0; k < CPC; ++k) {
+        const float v = e2m1_decode((cw[j][0] >> (4 * k)) & 0xFu);  // element 2i: low nibble
+        o[k] = fast ? v * s : mx_mul(v, s);
+      }
+    }
+    v4u val;
+    if constexpr (ODT == kBF16) {
+      if (fast) {
+        val = {bf16x2_bits(o[0], o[1]), bf16x2_bits(o[2], o[3]), bf16x2_bits(o[4], o[5]),
+               bf16x2_bits(o[6], o[7])};
+      } else {
+        val = {bf16_bits(o[0]) | (bf16_bits(o[1]) << 16), bf16_bits(o[2]) | (bf16_bits(o[3]) << 16),
+               bf16_bits(o[4]) | (bf16_bits(o[5]) << 16), bf16_bits(o[6]) | (bf16_bits(o[7]) << 16)};
+      }
+      __builtin_nontemporal_store(val, reinterpret_cast<v4u*>(reinterpret_cast<uint16_t*>(d.codes) + ch * CPC));
+    } else {
+      val = {f2u(o[0]), f2u(o[1]), f2u(o[2]), f2u(o[3])};
+      __builtin_nontemporal_store(val, reinterpret_cast<v4u*>(reinterpret_cast<float*>(d.codes) + ch * CPC));
+    }
+  }
+}
+
+hipError_t launch_mx_dequant(const LaunchCfg& cfg, const Desc& single, const Desc* descs,
+                             const uint32_t* map, int64_t units, hipStream_t stream) {
+  const dim3 grid((unsigned)units), block(256);
+  const bool f32 = cfg.out_dtype == kF32;
+  if (cfg.mx_fmt == 8) {
+    if (f32) hipLaunchKernelGGL((k_mx_dequant<8, kF32>), grid, block, 0, stream, single, descs, map);
+    else hipLaunchKernelGGL((k_mx_dequant<8, kBF16>), grid, block, 0, stream, single, descs, map);
+  } else if (cfg.mx_fmt == 4) {
+    if (f32) hipLaunchKernelGGL((k_mx_dequant<4, kF32>), grid, block, 0, stream, single, descs, map);
+    else hipLaunchKernelGGL((k_mx_dequant<4, kBF16>), grid, block, 0, stream, single, descs, map);
+  } else {
+    return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
 // diagnostics: the element encoders on raw inputs, for exhaustive checks
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(256) void k_diag_e4m3_bits(uint32_t start, int64_t n, uint8_t* out) {

@@ -36,6 +36,7 @@ enum Kernel : int {
   kKernAmax = 7,           // per-tensor max |x| partials + scale (two launches)
   kKernCopy = 8,           // grouped byte copy (bucket pass-through tensors)
   kKernCast = 9,           // grouped unscaled cast to float8_e4m3fn
+  kKernMxDequant = 10,     // MXFP8 / MXFP4 dequant, 8 (bf16 out) or 4 (fp32) elements per lane-chunk
 };
 
 // Work per lane of the streaming kernels, shared by the kernels and the
@@ -99,6 +100,8 @@ hipError_t launch_tensor_scale(const LaunchCfg& cfg, const Desc* descs, const ui
 
 // Grouped byte copy over `units` work-groups.
 hipError_t launch_copy(const Desc* descs, const uint32_t* map, int64_t units, hipStream_t stream);
+hipError_t launch_mx_dequant(const LaunchCfg& cfg, const Desc& single, const Desc* descs,
+                             const uint32_t* map, int64_t units, hipStream_t stream);
 hipError_t launch_cast(int dtype, const Desc& single, const Desc* descs, const uint32_t* map,
                        int64_t units, hipStream_t stream);
 

@@ -16,7 +16,7 @@ LIB_PATH = os.path.join(_HERE, "liblrq.so")
 DTYPE_BF16, DTYPE_F16, DTYPE_F32 = 0, 1, 2
 FLAG_POW2_SCALE, FLAG_NATIVE_ARITH, FLAG_SCALE_BF16, FLAG_OUT_BF16 = 1, 2, 4, 8
 FMT_FP8_BLOCK, FMT_MXFP8, FMT_MXFP4, FMT_FP8_DEQUANT, FMT_TENSOR_SCALE, FMT_COPY = 0, 1, 2, 3, 4, 5
-FMT_CAST_E4M3 = 6
+FMT_CAST_E4M3, FMT_MXFP8_DEQUANT, FMT_MXFP4_DEQUANT = 6, 7, 8
 ERR_ARG, ERR_ALIGN, ERR_CAPACITY, ERR_TABLE = -1, -2, -3, -4
 
 
@@ -48,6 +48,7 @@ SIGNATURES = {
     "lrq_mxfp4_quant": (_CI, [_VP, _CI, _I64, _I64, _I64, _VP, _VP, _VP]),
     "lrq_act_qdq": (_CI, [_VP, _CI, _I64, _I64, _I64, _I64, _CU, _VP, _VP]),
     "lrq_cast_e4m3": (_CI, [_VP, _CI, _I64, _VP, _VP]),
+    "lrq_mx_dequant": (_CI, [_CI, _VP, _VP, _I64, _I64, _VP, _CI, _VP]),
     "lrq_group_table_bytes": (_I64, [_CI, ctypes.POINTER(LrqTensor), _I64, _CI, _I64, _I64, _CU]),
     "lrq_group_pack": (_CI, [_CI, ctypes.POINTER(LrqTensor), _I64, _CI, _I64, _I64, _CU, _VP, _I64]),
     "lrq_quant_grouped": (_CI, [_VP, _VP, _VP]),

@@ -241,6 +241,45 @@ def _mx(x: Tensor, fmt: int) -> tuple[Tensor, Tensor]:
     return codes, scales
 
 
+def _mx_dequant(codes: Tensor, scales: Tensor, fmt: int, out_dtype: torch.dtype) -> Tensor:
+    if codes.dtype not in (torch.float8_e4m3fn, torch.uint8) or scales.dtype not in (torch.uint8,
+                                                                                     torch.float8_e8m0fnu):
+        raise TypeError("MX dequant takes uint8/float8_e4m3fn codes and uint8/float8_e8m0fnu scales")
+    if not codes.is_cuda or codes.device != scales.device:
+        raise ValueError("MX dequant expects codes and scales on the same HIP device")
+    if out_dtype not in (torch.float32, torch.bfloat16):
+        raise ValueError(f"out_dtype must be float32 or bfloat16, got {out_dtype}")
+    *lead, kc = codes.shape if codes.dim() else (1,)
+    cols = kc if fmt == 8 else 2 * kc
+    if cols % 32 or tuple(scales.shape) != (*lead, cols // 32):
+        raise ValueError(f"codes {tuple(codes.shape)} and scales {tuple(scales.shape)} are not an "
+                         f"MXFP{fmt} pair")
+    c = codes.contiguous().view(torch.uint8)
+    cb = (8 if out_dtype == torch.bfloat16 else 4) // (1 if fmt == 8 else 2)
+    if c.data_ptr() % cb:
+        c = c.clone()
+    s = scales.contiguous().view(torch.uint8)
+    out = torch.empty((*lead, cols), dtype=out_dtype, device=codes.device)
+    if out.numel() == 0:
+        return out
+    with _on(codes.device):
+        rc = _lib.lib().lrq_mx_dequant(_lib.FMT_MXFP8 if fmt == 8 else _lib.FMT_MXFP4, c.data_ptr(),
+                                       s.data_ptr(), out.numel() // cols, cols, out.data_ptr(),
+                                       _IN_DTYPES[out_dtype], _stream(codes.device))
+    _lib.check(rc, "lrq_mx_dequant")
+    return out
+
+
+def dequantize_mxfp8(codes: Tensor, scales: Tensor, out_dtype: torch.dtype = torch.bfloat16) -> Tensor:
+    """Inverse of :func:`quantize_mxfp8`: code * 2^(E-127) per 1x32 group -> ``out_dtype``."""
+    return _mx_dequant(codes, scales, 8, out_dtype)
+
+
+def dequantize_mxfp4(codes: Tensor, scales: Tensor, out_dtype: torch.dtype = torch.bfloat16) -> Tensor:
+    """Inverse of :func:`quantize_mxfp4` (codes [..., K/2], low nibble first)."""
+    return _mx_dequant(codes, scales, 4, out_dtype)
+
+
 def quantize_mxfp8(x: Tensor) -> tuple[Tensor, Tensor]:
     """MXFP8: (e4m3fn codes, E8M0 uint8 scales [..., K/32])."""
     return _mx(x, 8)
@@ -269,7 +308,8 @@ def quantize_fp8_blockwise(x: Tensor, block_size: tuple[int, int] = (128, 128), 
 # ---------------------------------------------------------------------------
 _FMTS = {"fp8_block": _lib.FMT_FP8_BLOCK, "mxfp8": _lib.FMT_MXFP8, "mxfp4": _lib.FMT_MXFP4,
          "fp8_dequant": _lib.FMT_FP8_DEQUANT, "tensor_scale": _lib.FMT_TENSOR_SCALE,
-         "copy": _lib.FMT_COPY, "cast_e4m3": _lib.FMT_CAST_E4M3}
+         "copy": _lib.FMT_COPY, "cast_e4m3": _lib.FMT_CAST_E4M3,
+         "mxfp8_dequant": _lib.FMT_MXFP8_DEQUANT, "mxfp4_dequant": _lib.FMT_MXFP4_DEQUANT}
 
 
 class _GroupLaunch:
@@ -436,14 +476,21 @@ class DequantPlan:
 
     fp32(code) * fp32(scale) per ``block_size`` block, written as ``out_dtype``
     (float32: dequantize_tensor; bfloat16: dequantize_state_dict's cast).
+    ``fmt="mxfp8"`` / ``"mxfp4"`` takes MX pairs instead (E8M0 scales per 1x32
+    group; ``block_size`` is then ignored).
     """
 
     def __init__(self, pairs: Sequence[tuple[Tensor, Tensor]], block_size: tuple[int, int],
-                 out_dtype: torch.dtype = torch.float32) -> None:
+                 out_dtype: torch.dtype = torch.float32, *, fmt: str = "fp8_block") -> None:
         if not pairs:
             raise ValueError("DequantPlan needs at least one (codes, scales) pair")
         if out_dtype not in (torch.float32, torch.bfloat16):
             raise ValueError(f"out_dtype must be float32 or bfloat16, got {out_dtype}")
+        if fmt in ("mxfp8", "mxfp4"):
+            self._init_mx(pairs, fmt, out_dtype)
+            return
+        if fmt != "fp8_block":
+            raise ValueError(f"fmt must be fp8_block, mxfp8 or mxfp4, got {fmt!r}")
         sdt = pairs[0][1].dtype
         dev = pairs[0][0].device
         br, bc = int(block_size[0]), int(block_size[1])
@@ -474,6 +521,37 @@ class DequantPlan:
         self.algorithmic_bytes = nbytes
         flags = _lib.FLAG_OUT_BF16 if out_dtype == torch.bfloat16 else 0
         self._launch = _GroupLaunch("fp8_dequant", descs, len(pairs), _IN_DTYPES[sdt], (br, bc),
+                                    flags, dev)
+        self._launch.buffers += self.outputs
+        self.units = self._launch.units
+
+    def _init_mx(self, pairs, fmt: str, out_dtype: torch.dtype) -> None:
+        """(codes, E8M0 scales) pairs of ``fmt``: contiguous, on one device."""
+        dev = pairs[0][0].device
+        descs = (_lib.LrqTensor * len(pairs))()
+        self.inputs, self.outputs = [], []
+        nbytes = 0
+        for i, (c, sc) in enumerate(pairs):
+            if (c.dtype not in (torch.float8_e4m3fn, torch.uint8) or sc.dtype not in (torch.uint8, torch.float8_e8m0fnu)
+                    or not c.is_cuda or c.device != dev or sc.device != dev
+                    or not c.is_contiguous() or not sc.is_contiguous()):
+                raise ValueError(f"pair {i}: contiguous {fmt} codes and uint8 E8M0 scales on {dev} required")
+            *lead, kc = c.shape
+            cols = kc if fmt == "mxfp8" else 2 * kc
+            if cols % 32 or tuple(sc.shape) != (*lead, cols // 32):
+                raise ValueError(f"pair {i}: codes {tuple(c.shape)} and scales {tuple(sc.shape)} are not a pair")
+            out = torch.empty((*lead, cols), dtype=out_dtype, device=dev)
+            self.inputs.append((c, sc))
+            self.outputs.append(out)
+            descs[i].in_ = c.data_ptr()
+            descs[i].codes = out.data_ptr()
+            descs[i].scales = sc.data_ptr()
+            descs[i].batch, descs[i].rows, descs[i].cols = 1, _prod(lead), cols
+            descs[i].ld, descs[i].batch_stride = cols, _prod(lead) * cols
+            nbytes += _nbytes(c) + _nbytes(sc) + _nbytes(out)
+        self.algorithmic_bytes = nbytes
+        flags = _lib.FLAG_OUT_BF16 if out_dtype == torch.bfloat16 else 0
+        self._launch = _GroupLaunch(fmt + "_dequant", descs, len(pairs), _lib.DTYPE_BF16, (1, 32),
                                     flags, dev)
         self._launch.buffers += self.outputs
         self.units = self._launch.units

@@ -278,6 +278,30 @@ def test_cast_tables():
     assert L().lrq_cast_e4m3(None, 0, 0, None, None) == 0  # nothing to do, no launch
 
 
+def test_mx_dequant_tables():
+    """MX dequant: dense [rows, cols] codes, 2 lane-chunks of 8 (bf16 out) or 4
+    (fp32 out) elements per lane, 256 lanes per work-group; codes aligned to one
+    lane-chunk of codes, output to 16 bytes."""
+    ts = _tensors([(1, 64, 1024), (2, 32, 512)])
+    for i, t in enumerate(ts):
+        t.in_, t.codes, t.scales = 0x200000000 + i * 0x100000, 0x300000000 + i * 0x100000, 0x400000000
+    for fmt in (_lib.FMT_MXFP8_DEQUANT, _lib.FMT_MXFP4_DEQUANT):
+        for flags, cpc in ((_lib.FLAG_OUT_BF16, 8), (0, 4)):
+            need = L().lrq_group_table_bytes(fmt, ts, 2, 0, 1, 32, flags)
+            assert need > 0, _lib.last_error()
+            buf = np.zeros(need, np.uint8)
+            assert L().lrq_group_pack(fmt, ts, 2, 0, 1, 32, flags, buf.ctypes.data, need) == 0
+            units = [-(-64 * 1024 // cpc // 512), -(-2 * 32 * 512 // cpc // 512)]
+            assert L().lrq_group_units(buf.ctypes.data) == sum(units)
+    ts[1].in_ = ts[1].in_ + 2  # MXFP8 codes must hold a whole lane-chunk (4 or 8 bytes)
+    assert L().lrq_group_table_bytes(_lib.FMT_MXFP8_DEQUANT, ts, 2, 0, 1, 32, 0) == _lib.ERR_ALIGN
+    fake = ctypes.c_void_p(0x10000)
+    assert L().lrq_mx_dequant(3, fake, fake, 4, 64, fake, 0, None) == _lib.ERR_ARG      # bad format
+    assert L().lrq_mx_dequant(_lib.FMT_MXFP8, fake, fake, 4, 48, fake, 0, None) == _lib.ERR_ARG  # cols % 32
+    assert L().lrq_mx_dequant(_lib.FMT_MXFP4, fake, fake, 4, 64, fake, 1, None) == _lib.ERR_ARG  # fp16 out
+    assert L().lrq_mx_dequant(_lib.FMT_MXFP4, None, None, 0, 64, None, 0, None) == 0    # nothing to do
+
+
 def test_grouped_rejects_foreign_table():
     junk = np.zeros(4096, np.uint8)
     rc = L().lrq_quant_grouped(junk.ctypes.data, ctypes.c_void_p(0x1000), None)

@@ -85,6 +85,44 @@ def test_cast_e4m3_every_16bit_pattern_vs_torch():
     assert O.cast_e4m3(np.float32([464.0, 464.00003]), "f32").tolist() == [0x7E, 0x7F]
 
 
+def test_mx_dequant_oracle_pins():
+    """torch_ref.mx_dequant: every (code, E8M0) pair against the closed form
+    code * 2^(E-127) (exact in float64, then float32), the NaN rules of the
+    vectorized body, and dequantize -> quantize idempotence with the C oracle."""
+    from oracle import torch_ref as T
+    e = np.repeat(np.arange(256, dtype=np.uint8), 8)[:, None]                   # [2048, 1]
+    for fmt, ncode in ((8, 256), (4, 16)):
+        codes = np.tile(np.arange(ncode, dtype=np.uint8), (2048, 32 // ncode + (ncode == 256) * 7))
+        if fmt == 4:
+            codes = (codes[:, 0::2] | (codes[:, 1::2] << 4)).astype(np.uint8)  # 32 elements per row
+        scales = np.repeat(e, codes.shape[1] * (1 if fmt == 8 else 2) // 32, axis=1)
+        got = T.mx_dequant(torch.from_numpy(codes), torch.from_numpy(scales), fmt)
+        got = got.numpy().view(np.uint32)
+        if fmt == 8:
+            elem = torch.from_numpy(codes).view(torch.float8_e4m3fn).float().numpy()
+        else:
+            nib = np.stack((codes & 0xF, codes >> 4), -1).reshape(codes.shape[0], -1)
+            mag = np.array([0, .5, 1, 1.5, 2, 3, 4, 6], np.float32)[nib & 7]
+            elem = np.where(nib & 8, -mag, mag).astype(np.float32)
+        ee = np.repeat(scales, 32, axis=1).astype(np.int64)
+        with np.errstate(over="ignore", invalid="ignore"):
+            want = np.ldexp(elem.astype(np.float64), ee - 127).astype(np.float32).view(np.uint32)
+        fin = (ee != 255) & np.isfinite(elem)
+        assert np.array_equal(got[fin], want[fin]), fmt
+        assert set(got[(ee == 255) & np.isfinite(elem)].tolist()) == {0x7FC00001}
+        if fmt == 8:  # a NaN code keeps its own NaN, even over a NaN scale
+            nan = ~np.isfinite(elem)
+            assert np.array_equal(got[nan], elem.view(np.uint32)[nan])
+    # idempotence: quantize(dequantize(quantize(x))) == quantize(x)
+    x = weights((64, 1024))
+    xb = bits16(bf16_t(x))
+    for fmt in (8, 4):
+        q, sc = O.mx_quant(xb, "bf16", fmt)
+        dq = T.mx_dequant(torch.from_numpy(q), torch.from_numpy(sc), fmt, torch.bfloat16)
+        q2, sc2 = O.mx_quant(bits16(dq), "bf16", fmt)
+        assert np.array_equal(q2, q) and np.array_equal(sc2, sc), fmt
+
+
 def test_e4m3_decode_all_codes_vs_torch():
     codes = np.arange(256, dtype=np.uint8)
     want = torch.from_numpy(codes).view(torch.float8_e4m3fn).float().numpy().view(np.uint32)
