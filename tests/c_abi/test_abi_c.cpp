@@ -4,6 +4,7 @@
 // Prints one line per check and "c-abi ok" at the end; exits non-zero on the
 // first mismatch or error.
 #include <hip/hip_runtime.h>
+#include <math.h>
 #include <stdint.h>
 #include <stdio.h>
 #include <stdlib.h>
@@ -240,7 +241,37 @@ int main() {
     HIP(hipFree(dx));
   }
 
-  // 7. argument errors come back as codes with a message, not as faults
+  // 7. MXFP8 dequant of tensor 1's codes back to fp32: exact products, so the
+  //    reference value is the decoded code times 2^(E-127) computed on the host
+  {
+    const int64_t n = R[1] * C[1], g = n / 32;
+    uint8_t *dq8, *ds8;
+    float* dout;
+    HIP(hipMalloc(&dq8, (size_t)n));
+    HIP(hipMalloc(&ds8, (size_t)g));
+    HIP(hipMalloc(&dout, (size_t)n * 4));
+    LRQ(lrq_mxfp8_quant(dw[1], LRQ_DTYPE_BF16, R[1], C[1], C[1], dq8, ds8, (lrq_stream_t)st));
+    LRQ(lrq_mx_dequant(LRQ_FMT_MXFP8, dq8, ds8, R[1], C[1], dout, LRQ_DTYPE_F32, (lrq_stream_t)st));
+    HIP(hipStreamSynchronize(st));
+    std::vector<uint8_t> q((size_t)n), sc((size_t)g);
+    std::vector<float> got((size_t)n);
+    HIP(hipMemcpy(q.data(), dq8, (size_t)n, hipMemcpyDeviceToHost));
+    HIP(hipMemcpy(sc.data(), ds8, (size_t)g, hipMemcpyDeviceToHost));
+    HIP(hipMemcpy(got.data(), dout, (size_t)n * 4, hipMemcpyDeviceToHost));
+    bool ok = true;
+    for (int64_t i = 0; i < n && ok; ++i) {
+      const uint32_t c = q[(size_t)i], e = (c >> 3) & 15u, m = c & 7u, E = sc[(size_t)(i / 32)];
+      if ((c & 0x7Fu) == 0x7Fu || E == 0xFFu) continue;  // NaN rules are covered by the Python tests
+      const double v = (e ? (1.0 + m / 8.0) * ldexp(1.0, (int)e - 7) : m * ldexp(1.0, -9)) * ((c & 0x80u) ? -1 : 1);
+      ok = got[(size_t)i] == (float)ldexp(v, (int)E - 127);
+    }
+    expect(ok, "lrq_mxfp8_quant + lrq_mx_dequant (fp32)");
+    HIP(hipFree(dout));
+    HIP(hipFree(ds8));
+    HIP(hipFree(dq8));
+  }
+
+  // 8. argument errors come back as codes with a message, not as faults
   {
     const int rc = lrq_fp8_block_quant(dw[0], LRQ_DTYPE_BF16, 1, R[0], C[0], C[0] - 1, R[0] * C[0], 128, 128,
                                        dcodes[0], dscales[0], 0, (lrq_stream_t)st);
