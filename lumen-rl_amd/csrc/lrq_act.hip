@@ -90,7 +90,7 @@ __global__ __launch_bounds__(256) void k_act_qdq8(const uint16_t* __restrict__ i
                                                   int64_t ld, float* __restrict__ out, int pow2) {
   const int64_t n = rows * cols;
   const int lane = threadIdx.x & 63;
-  const int64_t span = xcd_unit(blockIdx.x, gridDim.x) * 2048 + (threadIdx.x >> 6) * 512;
+  const int64_t span = xcd_unit<kXcdRunStream>(blockIdx.x, gridDim.x) * 2048 + (threadIdx.x >> 6) * 512;
   const int64_t e = span + 8 * lane;
   v4u v = {0u, 0u, 0u, 0u};
   if (e < n) v = __builtin_nontemporal_load(reinterpret_cast<const v4u*>(in + act_offset(e, cols, ld, DENSE)));
@@ -133,7 +133,7 @@ template <int DT, int LPB, int NCH, bool DENSE>
 __global__ __launch_bounds__(256) void k_act_qdq(const void* __restrict__ in, int64_t rows, int64_t cols,
                                                  int64_t ld, float* __restrict__ out, int pow2) {
   const int64_t n = rows * cols;
-  const int64_t base = xcd_unit(blockIdx.x, gridDim.x) * (1024 * NCH) + 4 * (int64_t)threadIdx.x;
+  const int64_t base = xcd_unit<kXcdRunStream>(blockIdx.x, gridDim.x) * (1024 * NCH) + 4 * (int64_t)threadIdx.x;
   float x[NCH][4];
 #pragma unroll
   for (int j = 0; j < NCH; ++j) {

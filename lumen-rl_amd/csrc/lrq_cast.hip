@@ -46,7 +46,7 @@ __global__ __launch_bounds__(256) void k_cast_e4m3(Desc single, const Desc* __re
   constexpr int NL = kCastLaneElems / EPL;  // loads per lane
   Desc d;
   int64_t u;
-  pick_desc(single, descs, map, d, u);
+  pick_desc<kXcdRunStream>(single, descs, map, d, u);
   const int64_t n = d.cols;
   const int64_t base = u * kCastUnit;
   const int tid = threadIdx.x;

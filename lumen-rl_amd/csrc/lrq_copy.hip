@@ -20,7 +20,7 @@ __global__ __launch_bounds__(256) void k_copy(Desc single, const Desc* __restric
                                               const uint32_t* __restrict__ map) {
   Desc d;
   int64_t u;
-  pick_desc(single, descs, map, d, u);
+  pick_desc<kXcdRunStream>(single, descs, map, d, u);
   const int64_t n = d.cols;  // bytes
   const char* src = static_cast<const char*>(d.in);
   char* dst = reinterpret_cast<char*>(d.codes);

@@ -47,7 +47,7 @@ __global__ __launch_bounds__(256) void k_dequant_generic(Desc single, const Desc
                                                          int blk_c) {
   Desc d;
   int64_t u;
-  pick_desc(single, descs, map, d, u);
+  pick_desc<kXcdRunStream>(single, descs, map, d, u);
   const int64_t i = u * 256 + threadIdx.x;
   if (i >= d.nblocks) return;
   const uint8_t* codes = static_cast<const uint8_t*>(d.in);
@@ -77,7 +77,7 @@ __global__ __launch_bounds__(256) void k_dequant(Desc single, const Desc* __rest
   constexpr int NCH = kDequantChunks;        // chunks per lane
   Desc d;
   int64_t u;
-  pick_desc(single, descs, map, d, u);
+  pick_desc<kXcdRunStream>(single, descs, map, d, u);
   const int tid = threadIdx.x;
   const uint8_t* codes = static_cast<const uint8_t*>(d.in);
   uint32_t cw[NCH][NW];
@@ -204,7 +204,7 @@ __global__ __launch_bounds__(256) void k_mx_dequant(Desc single, const Desc* __r
   constexpr int NCH = kDequantChunks;
   Desc d;
   int64_t u;
-  pick_desc(single, descs, map, d, u);
+  pick_desc<kXcdRunStream>(single, descs, map, d, u);
   const int tid = threadIdx.x;
   const uint8_t* codes = static_cast<const uint8_t*>(d.in);
   const uint8_t* sc = static_cast<const uint8_t*>(d.scales);

@@ -263,15 +263,16 @@ __device__ __forceinline__ void store_nt(void* p, uint32_t v) {
 
 // MI355X dispatches work-group i to XCD i % 8.  Work units adjacent in memory
 // (the tiles of a 128-row band, consecutive row blocks) are given to one XCD in
-// runs of kXcdRun, so each XCD streams contiguous megabytes instead of every
-// eighth 32 KiB piece.  A bijection on [0, n); the tail past the last whole
-// run group keeps the identity order.
-constexpr int64_t kXcdRun = 32;
+// runs of RUN, so each XCD streams contiguous hundreds of KiB instead of every
+// eighth unit.  A bijection on [0, n); the tail past the last whole run group
+// keeps the identity order.  The best RUN depends on the kernel's unit size
+// (per-kernel constants in lrq_internal.hpp).
+template <int64_t RUN>
 __device__ __forceinline__ int64_t xcd_unit(int64_t i, int64_t n) {
-  constexpr int64_t chunk = 8 * kXcdRun;
+  constexpr int64_t chunk = 8 * RUN;
   if (i >= (n / chunk) * chunk) return i;
   const int64_t r = i % chunk;
-  return (i - r) + (r % 8) * kXcdRun + r / 8;
+  return (i - r) + (r % 8) * RUN + r / 8;
 }
 
 // ---------------------------------------------------------------------------

@@ -6,7 +6,7 @@
 // e4m3 + scale out).  Three kernels:
 //   k_tile128  : 128x128 tiles (the vLLM/ATOM `weight_scale_inv` layout), one
 //                512-thread work-group per tile, the tile held in VGPRs;
-//                tiles handed to XCDs in runs of kXcdRun (xcd_unit).
+//                tiles handed to XCDs in runs of kXcdRunTile (xcd_unit).
 //   k_row      : 1xB row blocks (the reference's own layout), B/8 consecutive
 //                lanes per block so every wave instruction is one contiguous
 //                span; one scale computation per lane, shared by shuffles.
@@ -135,7 +135,7 @@ __global__ __launch_bounds__(T) void k_tile128(Desc single, const Desc* __restri
   __shared__ uint32_t red[T / 64];
   Desc d;
   int64_t u;
-  pick_desc(single, descs, map, d, u);
+  pick_desc<kXcdRunTile>(single, descs, map, d, u);
 
   const int64_t per = d.units_r * d.units_c;
   const int64_t b = u / per;
@@ -206,7 +206,7 @@ __global__ __launch_bounds__(256) void k_row(Desc single, const Desc* __restrict
   constexpr int BPI = 64 / LPB;       // blocks per wave instruction
   Desc d;
   int64_t u;
-  pick_desc(single, descs, map, d, u);
+  pick_desc<kXcdRunRow>(single, descs, map, d, u);
   const int tid = threadIdx.x, lane = tid & 63;
   const int c = lane & (LPB - 1);     // chunk of the block held by this lane
   constexpr int NJ = kRowBlocks;      // blocks per lane
@@ -279,7 +279,7 @@ __global__ __launch_bounds__(256) void k_generic(Desc single, const Desc* __rest
   __shared__ uint32_t red[4];
   Desc d;
   int64_t u;
-  pick_desc(single, descs, map, d, u);
+  pick_desc<kXcdRunStream>(single, descs, map, d, u);
   const int64_t per = d.units_r * d.units_c;
   const int64_t b = u / per;
   const int64_t rem = u - b * per;

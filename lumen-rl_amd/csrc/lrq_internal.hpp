@@ -46,16 +46,23 @@ constexpr int kDequantChunks = 2;    // k_dequant: 16-byte output chunks per lan
 constexpr int kMxLoads = 2;          // k_mx: 32-element groups per quad of lanes (2 beat 1, 3 and 4)
 constexpr int kTileThreads = 512;    // k_tile128: threads per 128x128 tile (512 beat 256 and 1024)
 constexpr int kRowBlocks = 4;        // k_row: 1xB blocks per lane, sharing one scale computation (4: 2 is 7% slower with bf16 scales, 3 slower with both)
+// XCD run length (xcd_unit) per kernel, in work units; sweeps over 8..128:
+constexpr int64_t kXcdRunTile = 32;    // k_tile128: 32 tiles = 1 MiB of bf16 (16 and 8 lose 6-7%, 64 and 128 1%)
+constexpr int64_t kXcdRunRow = 16;     // k_row: 256 KiB of bf16 (32 loses 2%)
+constexpr int64_t kXcdRunMx = 64;      // k_mx: 512 KiB of bf16 (32 loses 2.5%, 128 ties)
+constexpr int64_t kXcdRunStream = 32;  // dequant, act, amax, copy, cast, generic kernels
 constexpr int kCastLaneElems = 16;   // k_cast_e4m3: elements per lane
 constexpr int64_t kCastUnit = 256 * kCastLaneElems;  // k_cast_e4m3: elements per work-group
 constexpr int kAmaxLoads = 2;        // k_amax: 16-byte loads per lane (2 beat 1, 3, 4 and 8)
 
 // Descriptor and local work unit of this work-group: the single-tensor
 // descriptor (kernel argument) or, for a grouped launch, the one the device
-// map names for the XCD-remapped work-group index.
+// map names for the work-group index remapped into XCD runs of RUN units
+// (xcd_unit).
+template <int64_t RUN>
 __device__ __forceinline__ void pick_desc(const Desc& single, const Desc* descs,
                                           const uint32_t* map, Desc& d, int64_t& u) {
-  const int64_t wg = xcd_unit(blockIdx.x, gridDim.x);
+  const int64_t wg = xcd_unit<RUN>(blockIdx.x, gridDim.x);
   if (map != nullptr) {
     const uint32_t t = map[wg];
     d = descs[t];

@@ -106,7 +106,7 @@ __global__ __launch_bounds__(256) void k_mx(Desc single, const Desc* __restrict_
   constexpr int kEmax = FMT == 8 ? 8 : 2;
   Desc d;
   int64_t u;
-  pick_desc(single, descs, map, d, u);
+  pick_desc<kXcdRunMx>(single, descs, map, d, u);
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int p = lane & 3;
@@ -157,7 +157,7 @@ __global__ __launch_bounds__(256) void k_mx_generic(Desc single, const Desc* __r
   constexpr int kEmax = FMT == 8 ? 8 : 2;
   Desc d;
   int64_t u;
-  pick_desc(single, descs, map, d, u);
+  pick_desc<kXcdRunStream>(single, descs, map, d, u);
   const int64_t g = u * 256 + threadIdx.x;
   if (g >= d.nblocks) return;
   const int64_t row = g / d.bpr;

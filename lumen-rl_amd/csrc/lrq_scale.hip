@@ -119,7 +119,7 @@ __global__ __launch_bounds__(256) void k_amax(Desc single, const Desc* __restric
   __shared__ uint32_t lds[4];
   Desc d;
   int64_t u;
-  pick_desc(single, descs, map, d, u);
+  pick_desc<kXcdRunStream>(single, descs, map, d, u);
   uint32_t m;
   if (d.units_c) m = d.units_r ? lane_amax<DT, true, true>(d, u) : lane_amax<DT, true, false>(d, u);
   else m = d.units_r ? lane_amax<DT, false, true>(d, u) : lane_amax<DT, false, false>(d, u);
