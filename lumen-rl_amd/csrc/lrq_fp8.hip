@@ -167,7 +167,7 @@ __global__ __launch_bounds__(T) void k_tile128(Desc single, const Desc* __restri
   am.init();
 #pragma unroll
   for (int i = 0; i < NL; ++i) am.add(ch[i]);
-  uint32_t a = wave_max(am.bits());
+  uint32_t a = group_max<64>(am.bits());  // DPP within rows of 16, two shuffles across
   if ((tid & 63) == 0) red[tid >> 6] = a;
   __syncthreads();
   a = red[0];
