@@ -26,9 +26,9 @@ namespace lrq {
 
 template <int DT>
 __device__ __forceinline__ float cast_elem(const void* base, int64_t i) {
-  if constexpr (DT == kF32) return static_cast<const float*>(base)[i];
-  else if constexpr (DT == kBF16) return u2f((uint32_t)static_cast<const uint16_t*>(base)[i] << 16);
-  else return f16_to_f32(static_cast<const uint16_t*>(base)[i]);
+  if constexpr (DT == kF32) return gld<float>(static_cast<const float*>(base) + i);
+  else if constexpr (DT == kBF16) return u2f((uint32_t)gld<uint16_t>(static_cast<const uint16_t*>(base) + i) << 16);
+  else return f16_to_f32(gld<uint16_t>(static_cast<const uint16_t*>(base) + i));
 }
 
 // Four floats -> four e4m3fn bytes (element 0 in the low byte), torch's rule.
@@ -84,13 +84,13 @@ __global__ __launch_bounds__(256) void k_cast_e4m3(Desc single, const Desc* __re
     const int64_t nfull = n - n % EPL;  // tail: fewer than EPL elements
     if (nfull < n && nfull >= base && nfull < base + kCastUnit && tid < n - nfull) {
       const float x = cast_elem<DT>(d.in, nfull + tid);
-      out[nfull + tid] = (uint8_t)(x != x ? sw_e4m3(x) : (cvt_e4m3x2<false>(x, 0.0f, 0u) & 0xFFu));
+      gst<uint8_t>(out + nfull + tid, (uint8_t)(x != x ? sw_e4m3(x) : (cvt_e4m3x2<false>(x, 0.0f, 0u) & 0xFFu)));
     }
   } else {  // misaligned: element-wise walk of the unit
     const int64_t end = base + kCastUnit < n ? base + kCastUnit : n;
     for (int64_t i = base + tid; i < end; i += 256) {
       const float x = cast_elem<DT>(d.in, i);
-      out[i] = (uint8_t)(x != x ? sw_e4m3(x) : (cvt_e4m3x2<false>(x, 0.0f, 0u) & 0xFFu));
+      gst<uint8_t>(out + i, (uint8_t)(x != x ? sw_e4m3(x) : (cvt_e4m3x2<false>(x, 0.0f, 0u) & 0xFFu)));
     }
   }
 }

@@ -36,10 +36,10 @@ __global__ __launch_bounds__(256) void k_copy(Desc single, const Desc* __restric
 #pragma unroll
   for (int j = 0; j < kLoads; ++j) {
     const int64_t off = base + (int64_t)(256 * j + tid) * 16;
-    if (off + 16 <= n) __builtin_nontemporal_store(v[j], reinterpret_cast<v4u*>(dst + off));
+    if (off + 16 <= n) gst_nt<v4u>(dst + off, v[j]);
   }
   const int64_t n16 = n & ~int64_t(15);
-  if (n16 < n && n16 >= base && n16 < base + kCopyUnit && tid < n - n16) dst[n16 + tid] = src[n16 + tid];
+  if (n16 < n && n16 >= base && n16 < base + kCopyUnit && tid < n - n16) gst<char>(dst + n16 + tid, gld<char>(src + n16 + tid));
 }
 
 hipError_t launch_copy(const Desc* descs, const uint32_t* map, int64_t units, hipStream_t stream) {

@@ -28,9 +28,9 @@ __device__ __forceinline__ float x86_mul(float v, float s) {
 
 template <int SDT>
 __device__ __forceinline__ float load_scale(const void* scales, int64_t i) {
-  if constexpr (SDT == kF32) return static_cast<const float*>(scales)[i];
-  else if constexpr (SDT == kBF16) return u2f((uint32_t)static_cast<const uint16_t*>(scales)[i] << 16);
-  else return f16_to_f32(static_cast<const uint16_t*>(scales)[i]);
+  if constexpr (SDT == kF32) return gld<float>(static_cast<const float*>(scales) + i);
+  else if constexpr (SDT == kBF16) return u2f((uint32_t)gld<uint16_t>(static_cast<const uint16_t*>(scales) + i) << 16);
+  else return f16_to_f32(gld<uint16_t>(static_cast<const uint16_t*>(scales) + i));
 }
 
 // Scale index of element (b, r, c) of a [batch, rows, cols] tensor.
@@ -51,9 +51,9 @@ __global__ __launch_bounds__(256) void k_dequant_generic(Desc single, const Desc
   const int64_t i = u * 256 + threadIdx.x;
   if (i >= d.nblocks) return;
   const uint8_t* codes = static_cast<const uint8_t*>(d.in);
-  const float o = x86_mul(e4m3_decode(codes[i]), load_scale<SDT>(d.scales, scale_index(d, i, blk_r, blk_c)));
-  if constexpr (ODT == kF32) reinterpret_cast<float*>(d.codes)[i] = o;
-  else reinterpret_cast<uint16_t*>(d.codes)[i] = (uint16_t)bf16_bits(o);
+  const float o = x86_mul(e4m3_decode(gld<uint8_t>(codes + i)), load_scale<SDT>(d.scales, scale_index(d, i, blk_r, blk_c)));
+  if constexpr (ODT == kF32) gst<float>(reinterpret_cast<float*>(d.codes) + i, o);
+  else gst<uint16_t>(reinterpret_cast<uint16_t*>(d.codes) + i, (uint16_t)bf16_bits(o));
 }
 
 // Vectorized: a lane-chunk is CPC codes (8 for bf16 output, 4 for fp32) whose
@@ -83,26 +83,31 @@ __global__ __launch_bounds__(256) void k_dequant(Desc single, const Desc* __rest
   uint32_t cw[NCH][NW];
   float sc[NCH];
   bool ok[NCH];
+  int64_t at[NCH];  // chunks past the end re-read the last one: no branch around loads
 #pragma unroll
   for (int j = 0; j < NCH; ++j) {
     const int64_t ch = u * (256 * NCH) + j * 256 + tid;
     ok[j] = ch < d.nblocks;
-    if (ok[j]) {
-      if constexpr (NW == 2) {
-        const v2u v = __builtin_nontemporal_load(reinterpret_cast<const v2u*>(codes + ch * CPC));
-        cw[j][0] = v.x;
-        cw[j][1] = v.y;
-      } else {
-        cw[j][0] = __builtin_nontemporal_load(reinterpret_cast<const uint32_t*>(codes + ch * CPC));
-      }
-      const int64_t si = ROWS1 ? (ch * CPC) / blk_c : scale_index(d, ch * CPC, blk_r, blk_c);
-      sc[j] = load_scale<SDT>(d.scales, si);
+    at[j] = ok[j] ? ch : d.nblocks - 1;
+  }
+#pragma unroll
+  for (int j = 0; j < NCH; ++j) {  // every code load first, then the scales
+    if constexpr (NW == 2) {
+      const v2u v = gld_nt<v2u>(codes + at[j] * CPC);
+      cw[j][0] = v.x;
+      cw[j][1] = v.y;
+    } else {
+      cw[j][0] = gld_nt<uint32_t>(codes + at[j] * CPC);
     }
   }
 #pragma unroll
   for (int j = 0; j < NCH; ++j) {
-    if (!ok[j]) continue;
-    const int64_t ch = u * (256 * NCH) + j * 256 + tid;
+    const int64_t si = ROWS1 ? (at[j] * CPC) / blk_c : scale_index(d, at[j] * CPC, blk_r, blk_c);
+    sc[j] = load_scale<SDT>(d.scales, si);
+  }
+  v4u val[NCH];  // every chunk decoded before the first store
+#pragma unroll
+  for (int j = 0; j < NCH; ++j) {
     const float s = sc[j];
     const uint32_t as = f2u(s) & 0x7FFFFFFFu;
     bool nan_code = false;
@@ -123,21 +128,23 @@ __global__ __launch_bounds__(256) void k_dequant(Desc single, const Desc* __rest
 #pragma unroll
       for (int k = 0; k < CPC; ++k) o[k] = x86_mul(e4m3_decode((cw[j][k >> 2] >> (8 * (k & 3))) & 0xFFu), s);
     }
-    v4u val;
     if constexpr (ODT == kBF16) {
       if (fast) {
-        val = {bf16x2_bits(o[0], o[1]), bf16x2_bits(o[2], o[3]), bf16x2_bits(o[4], o[5]),
-               bf16x2_bits(o[6], o[7])};
+        val[j] = {bf16x2_bits(o[0], o[1]), bf16x2_bits(o[2], o[3]), bf16x2_bits(o[4], o[5]),
+                  bf16x2_bits(o[6], o[7])};
       } else {
-        val = {bf16_bits(o[0]) | (bf16_bits(o[1]) << 16), bf16_bits(o[2]) | (bf16_bits(o[3]) << 16),
-               bf16_bits(o[4]) | (bf16_bits(o[5]) << 16), bf16_bits(o[6]) | (bf16_bits(o[7]) << 16)};
+        val[j] = {bf16_bits(o[0]) | (bf16_bits(o[1]) << 16), bf16_bits(o[2]) | (bf16_bits(o[3]) << 16),
+                  bf16_bits(o[4]) | (bf16_bits(o[5]) << 16), bf16_bits(o[6]) | (bf16_bits(o[7]) << 16)};
       }
-      __builtin_nontemporal_store(val, reinterpret_cast<v4u*>(reinterpret_cast<uint16_t*>(d.codes) + ch * CPC));
     } else {
-      val = {f2u(o[0]), f2u(o[1]), f2u(o[2]), f2u(o[3])};
-      __builtin_nontemporal_store(val, reinterpret_cast<v4u*>(reinterpret_cast<float*>(d.codes) + ch * CPC));
+      val[j] = {f2u(o[0]), f2u(o[1]), f2u(o[2]), f2u(o[3])};
     }
   }
+  uint8_t* out = static_cast<uint8_t*>(d.codes);
+  constexpr int OB = CPC * (ODT == kBF16 ? 2 : 4);  // output bytes per chunk
+#pragma unroll
+  for (int j = 0; j < NCH; ++j)
+    if (ok[j]) gst_nt<v4u>(out + at[j] * OB, val[j]);
 }
 
 template <int SDT, int ODT>
@@ -211,27 +218,31 @@ __global__ __launch_bounds__(256) void k_mx_dequant(Desc single, const Desc* __r
   uint32_t cw[NCH][2];
   uint32_t ex[NCH];
   bool ok[NCH];
+  int64_t at[NCH];  // chunks past the end re-read the last one: no branch around loads
 #pragma unroll
   for (int j = 0; j < NCH; ++j) {
     const int64_t ch = u * (256 * NCH) + j * 256 + tid;
     ok[j] = ch < d.nblocks;
-    if (!ok[j]) continue;
-    const uint8_t* p = codes + ch * CB;
+    at[j] = ok[j] ? ch : d.nblocks - 1;
+  }
+#pragma unroll
+  for (int j = 0; j < NCH; ++j) {  // every code load first, then the scale bytes
+    const uint8_t* p = codes + at[j] * CB;
     if constexpr (CB == 8) {
-      const v2u v = __builtin_nontemporal_load(reinterpret_cast<const v2u*>(p));
+      const v2u v = gld_nt<v2u>(p);
       cw[j][0] = v.x;
       cw[j][1] = v.y;
     } else if constexpr (CB == 4) {
-      cw[j][0] = __builtin_nontemporal_load(reinterpret_cast<const uint32_t*>(p));
+      cw[j][0] = gld_nt<uint32_t>(p);
     } else {
-      cw[j][0] = __builtin_nontemporal_load(reinterpret_cast<const uint16_t*>(p));
+      cw[j][0] = gld_nt<uint16_t>(p);
     }
-    ex[j] = sc[(ch * CPC) >> 5];
   }
 #pragma unroll
+  for (int j = 0; j < NCH; ++j) ex[j] = gld<uint8_t>(sc + ((at[j] * CPC) >> 5));
+  v4u val[NCH];  // every chunk decoded before the first store
+#pragma unroll
   for (int j = 0; j < NCH; ++j) {
-    if (!ok[j]) continue;
-    const int64_t ch = u * (256 * NCH) + j * 256 + tid;
     const float s = e8m0_to_f32(ex[j]);
     float o[CPC];
     bool fast = ex[j] != 0xFFu;
@@ -258,21 +269,23 @@ __global__ __launch_bounds__(256) void k_mx_dequant(Desc single, const Desc* __r
         o[k] = fast ? v * s : mx_mul(v, s);
       }
     }
-    v4u val;
     if constexpr (ODT == kBF16) {
       if (fast) {
-        val = {bf16x2_bits(o[0], o[1]), bf16x2_bits(o[2], o[3]), bf16x2_bits(o[4], o[5]),
-               bf16x2_bits(o[6], o[7])};
+        val[j] = {bf16x2_bits(o[0], o[1]), bf16x2_bits(o[2], o[3]), bf16x2_bits(o[4], o[5]),
+                  bf16x2_bits(o[6], o[7])};
       } else {
-        val = {bf16_bits(o[0]) | (bf16_bits(o[1]) << 16), bf16_bits(o[2]) | (bf16_bits(o[3]) << 16),
-               bf16_bits(o[4]) | (bf16_bits(o[5]) << 16), bf16_bits(o[6]) | (bf16_bits(o[7]) << 16)};
+        val[j] = {bf16_bits(o[0]) | (bf16_bits(o[1]) << 16), bf16_bits(o[2]) | (bf16_bits(o[3]) << 16),
+                  bf16_bits(o[4]) | (bf16_bits(o[5]) << 16), bf16_bits(o[6]) | (bf16_bits(o[7]) << 16)};
       }
-      __builtin_nontemporal_store(val, reinterpret_cast<v4u*>(reinterpret_cast<uint16_t*>(d.codes) + ch * CPC));
     } else {
-      val = {f2u(o[0]), f2u(o[1]), f2u(o[2]), f2u(o[3])};
-      __builtin_nontemporal_store(val, reinterpret_cast<v4u*>(reinterpret_cast<float*>(d.codes) + ch * CPC));
+      val[j] = {f2u(o[0]), f2u(o[1]), f2u(o[2]), f2u(o[3])};
     }
   }
+  uint8_t* out = static_cast<uint8_t*>(d.codes);
+  constexpr int OB = CPC * (ODT == kBF16 ? 2 : 4);  // output bytes per chunk
+#pragma unroll
+  for (int j = 0; j < NCH; ++j)
+    if (ok[j]) gst_nt<v4u>(out + at[j] * OB, val[j]);
 }
 
 hipError_t launch_mx_dequant(const LaunchCfg& cfg, const Desc& single, const Desc* descs,

@@ -249,17 +249,32 @@ __device__ __forceinline__ float mx_mult(uint32_t e8m0) { return u2f((254u - e8m
 typedef unsigned int v4u __attribute__((ext_vector_type(4)));
 typedef unsigned int v2u __attribute__((ext_vector_type(2)));
 
+// Every tensor is device memory, but the kernels take their pointers from
+// descriptors, so the compiler sees generic pointers and would emit flat_*
+// accesses, which also count against the LDS counter.  These helpers access
+// memory through the global address space (global_* instructions).
+#define LRQ_GLOBAL __attribute__((address_space(1)))
+template <class T>
+__device__ __forceinline__ T gld(const void* p) {
+  return *(const LRQ_GLOBAL T*)p;
+}
+template <class T>
+__device__ __forceinline__ void gst(void* p, T v) {
+  *(LRQ_GLOBAL T*)p = v;
+}
 // Weights are read once and codes written once: non-temporal accesses keep
 // them from displacing anything in L2/MALL (measured +5% HBM throughput).
-__device__ __forceinline__ v4u load_nt(const void* p) {
-  return __builtin_nontemporal_load(static_cast<const v4u*>(p));
+template <class T>
+__device__ __forceinline__ T gld_nt(const void* p) {
+  return __builtin_nontemporal_load((const LRQ_GLOBAL T*)p);
 }
-__device__ __forceinline__ void store_nt(void* p, v2u v) {
-  __builtin_nontemporal_store(v, static_cast<v2u*>(p));
+template <class T>
+__device__ __forceinline__ void gst_nt(void* p, T v) {
+  __builtin_nontemporal_store(v, (LRQ_GLOBAL T*)p);
 }
-__device__ __forceinline__ void store_nt(void* p, uint32_t v) {
-  __builtin_nontemporal_store(v, static_cast<uint32_t*>(p));
-}
+__device__ __forceinline__ v4u load_nt(const void* p) { return gld_nt<v4u>(p); }
+__device__ __forceinline__ void store_nt(void* p, v2u v) { gst_nt<v2u>(p, v); }
+__device__ __forceinline__ void store_nt(void* p, uint32_t v) { gst_nt<uint32_t>(p, v); }
 
 // MI355X dispatches work-group i to XCD i % 8.  Work units adjacent in memory
 // (the tiles of a 128-row band, consecutive row blocks) are given to one XCD in

@@ -112,10 +112,10 @@ __device__ __forceinline__ v2u encode_chunk(const Chunk<DT>& c, const BlockScale
 template <int CDT>
 __device__ __forceinline__ void store_scale(void* scales, int64_t idx, float s, int scale_bf16) {
   if (CDT == kF32 && !scale_bf16) {
-    static_cast<float*>(scales)[idx] = s;
+    gst<float>(static_cast<float*>(scales) + idx, s);
   } else {
     uint32_t h = (CDT == kF16) ? f16_bits(s) : bf16_bits(s);
-    static_cast<uint16_t*>(scales)[idx] = (uint16_t)h;
+    gst<uint16_t>(static_cast<uint16_t*>(scales) + idx, (uint16_t)h);
   }
 }
 
@@ -267,9 +267,9 @@ __global__ __launch_bounds__(256) void k_row(Desc single, const Desc* __restrict
 // ---------------------------------------------------------------------------
 template <int DT>
 __device__ __forceinline__ float load_elem(const void* base, int64_t off) {
-  if constexpr (DT == kF32) return static_cast<const float*>(base)[off];
-  else if constexpr (DT == kBF16) return u2f((uint32_t)static_cast<const uint16_t*>(base)[off] << 16);
-  else return f16_to_f32(static_cast<const uint16_t*>(base)[off]);
+  if constexpr (DT == kF32) return gld<float>(static_cast<const float*>(base) + off);
+  else if constexpr (DT == kBF16) return u2f((uint32_t)gld<uint16_t>(static_cast<const uint16_t*>(base) + off) << 16);
+  else return f16_to_f32(gld<uint16_t>(static_cast<const uint16_t*>(base) + off));
 }
 
 template <int DT, int CDT>
@@ -312,7 +312,7 @@ __global__ __launch_bounds__(256) void k_generic(Desc single, const Desc* __rest
     const float x = load_elem<DT>(d.in, b * d.bstride + r * d.ld + c);
     const uint32_t code =
         bs.kind <= kScaleExact ? sw_e4m3(block_quot<CDT>(x, bs)) : special_code<CDT>(x, bs);
-    d.codes[(b * d.rows + r) * d.cols + c] = (uint8_t)code;
+    gst<uint8_t>(d.codes + (b * d.rows + r) * d.cols + c, (uint8_t)code);
   }
 }
 

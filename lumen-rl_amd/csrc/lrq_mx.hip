@@ -146,7 +146,7 @@ __global__ __launch_bounds__(256) void k_mx(Desc single, const Desc* __restrict_
     } else {
       store_nt(d.codes + g * 16 + p * 4, (uint32_t)c.x);
     }
-    if (p == 0) static_cast<uint8_t*>(d.scales)[g] = (uint8_t)e;
+    if (p == 0) gst<uint8_t>(static_cast<uint8_t*>(d.scales) + g, (uint8_t)e);
   }
 }
 
@@ -166,14 +166,14 @@ __global__ __launch_bounds__(256) void k_mx_generic(Desc single, const Desc* __r
   uint32_t a = 0u;
 #pragma unroll
   for (int i = 0; i < 32; ++i) {
-    if constexpr (DT == kF32) x[i] = static_cast<const float*>(d.in)[base + i];
-    else if constexpr (DT == kBF16) x[i] = u2f((uint32_t)static_cast<const uint16_t*>(d.in)[base + i] << 16);
-    else x[i] = f16_to_f32(static_cast<const uint16_t*>(d.in)[base + i]);
+    if constexpr (DT == kF32) x[i] = gld<float>(static_cast<const float*>(d.in) + base + i);
+    else if constexpr (DT == kBF16) x[i] = u2f((uint32_t)gld<uint16_t>(static_cast<const uint16_t*>(d.in) + base + i) << 16);
+    else x[i] = f16_to_f32(gld<uint16_t>(static_cast<const uint16_t*>(d.in) + base + i));
     const uint32_t m = f2u(x[i]) & 0x7FFFFFFFu;
     a = m > a ? m : a;
   }
   const uint32_t e = mx_e8m0<kEmax>(a);
-  static_cast<uint8_t*>(d.scales)[g] = (uint8_t)e;
+  gst<uint8_t>(static_cast<uint8_t*>(d.scales) + g, (uint8_t)e);
   const float mult = e != 0xFFu ? mx_mult(e) : 0.0f;
   if constexpr (FMT == 8) {
     uint8_t* out = d.codes + g * 32;
@@ -182,7 +182,7 @@ __global__ __launch_bounds__(256) void k_mx_generic(Desc single, const Desc* __r
       uint32_t c;
       if (e == 0xFFu) c = ((ux >> 24) & 0x80u) | ((ux & 0x7FFFFFFFu) >= 0x7F800000u ? 0x7Fu : 0u);
       else c = sw_e4m3(__builtin_amdgcn_fmed3f(x[i] * mult, -448.0f, 448.0f));
-      out[i] = (uint8_t)c;
+      gst<uint8_t>(out + i, (uint8_t)c);
     }
   } else {
     uint8_t* out = d.codes + g * 16;
@@ -195,7 +195,7 @@ __global__ __launch_bounds__(256) void k_mx_generic(Desc single, const Desc* __r
         lo = e2m1_code(x[i] * mult);
         hi = e2m1_code(x[i + 1] * mult);
       }
-      out[i / 2] = (uint8_t)(lo | (hi << 4));
+      gst<uint8_t>(out + i / 2, (uint8_t)(lo | (hi << 4)));
     }
   }
 }

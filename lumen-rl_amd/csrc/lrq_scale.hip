@@ -102,8 +102,8 @@ __device__ __forceinline__ uint32_t lane_amax(const Desc& d, int64_t u) {
       if (e >= n) break;
       const int64_t off = DENSE ? e : amax_offset(d, e);
       uint32_t t;
-      if constexpr (DT == kF32) t = static_cast<const uint32_t*>(d.in)[off] & 0x7FFFFFFFu;
-      else t = abs16_to_f32_bits<DT>(static_cast<const uint16_t*>(d.in)[off] & 0x7FFFu);
+      if constexpr (DT == kF32) t = gld<uint32_t>(static_cast<const uint32_t*>(d.in) + off) & 0x7FFFFFFFu;
+      else t = abs16_to_f32_bits<DT>(gld<uint16_t>(static_cast<const uint16_t*>(d.in) + off) & 0x7FFFu);
       a = t > a ? t : a;
     }
     return a;
@@ -147,7 +147,7 @@ __global__ __launch_bounds__(256) void k_tensor_scale(const Desc* __restrict__ d
       amax = amax < 0x1p-126f ? 0x1p-126f : amax;
       s = amax / 448.0f;  // IEEE division (correctly rounded, subnormal results kept)
     }
-    *static_cast<float*>(d.scales) = s;
+    gst<float>(d.scales, s);
   }
 }
 
