@@ -169,13 +169,17 @@ int lrq_mx_dequant(int fmt, const uint8_t* codes, const uint8_t* scales, int64_t
  * of WeightQuantizer.quantize_state_dict (weight_quantizer.py:91-115) and the
  * per-expert loaders (lumenrl/engine/inference/vllm_moe_weight_sync.py:232-283).
  *
- * 1. lrq_group_table_bytes() sizes a table for `n` tensors.
+ * 1. lrq_group_table_bytes() sizes the host table for `n` tensors (a header
+ *    and one 112-byte descriptor per tensor).
  * 2. lrq_group_pack() validates the tensors and writes the table into a HOST
- *    buffer (descriptors + a work-group -> tensor map).
- * 3. The caller copies the table verbatim to device memory (once; tables stay
- *    valid while the tensors' storage does) and calls lrq_quant_grouped() with
- *    both copies: the host copy supplies the launch geometry, the device copy
- *    is what the kernel reads.
+ *    buffer.
+ * 3. The caller allocates lrq_group_device_bytes(host_table) bytes of device
+ *    memory (256-byte aligned), copies the host table verbatim to its start,
+ *    and calls lrq_group_build_map() on the same stream, which writes the
+ *    work-group -> tensor map behind it (4 bytes per work-group) on the device.
+ *    Once per table: it stays valid while the tensors' storage does.
+ * 4. lrq_quant_grouped() takes both copies: the host copy supplies the launch
+ *    geometry, the device copy is what the kernel reads.
  * All tensors of a table share fmt, in_dtype, block shape and flags, and must
  * all qualify for the same kernel (the pack fails otherwise).
  * With fmt LRQ_FMT_FP8_DEQUANT the same tables drive the grouped inverse:
@@ -195,6 +199,11 @@ int64_t lrq_group_table_bytes(int fmt, const lrq_tensor* tensors, int64_t n, int
                               int64_t blk_r, int64_t blk_c, unsigned flags);
 int lrq_group_pack(int fmt, const lrq_tensor* tensors, int64_t n, int in_dtype, int64_t blk_r,
                    int64_t blk_c, unsigned flags, void* host_table, int64_t capacity);
+/* device table size: the host table plus 4 bytes per work-group */
+int64_t lrq_group_device_bytes(const void* host_table);
+/* writes the map of a device table whose first lrq_group_table_bytes() bytes
+ * hold the uploaded host table (stream-ordered before this call) */
+int lrq_group_build_map(const void* host_table, void* device_table, lrq_stream_t stream);
 int lrq_quant_grouped(const void* host_table, const void* device_table, lrq_stream_t stream);
 /* work-groups of a packed table's launch (for bandwidth accounting) */
 int64_t lrq_group_units(const void* host_table);

@@ -38,7 +38,7 @@ bool valid_dtype(int dt) { return dt == lrq::kBF16 || dt == lrq::kF16 || dt == l
 bool pow2_block(int64_t b) { return b == 32 || b == 64 || b == 128 || b == 256 || b == 512; }
 
 constexpr uint32_t kMagic = 0x4C525154u;  // "LRQT"
-constexpr uint32_t kTableVersion = 1u;
+constexpr uint32_t kTableVersion = 2u;
 // HIP takes a launch's thread count (work-groups x threads per work-group) as
 // a 32-bit value.  kMaxGrid is the limit for 256-thread work-groups;
 // max_units() gives it per kernel.
@@ -47,10 +47,14 @@ int64_t max_units(int kernel) {
   return 0xFFFFFFFFll / (kernel == lrq::kKernTile128 ? lrq::kTileThreads : 256);
 }
 
+// Table layout, host and device alike: [header | n descriptors | map].  The
+// host table ends at map_off (`bytes`); the device table adds the uint32
+// work-group -> tensor map (4 bytes per work-group, `dev_bytes` in all), which
+// the device writes itself (lrq_group_build_map) instead of uploading it.
 struct GroupHeader {
   uint32_t magic, version;
   LaunchCfg cfg;
-  int64_t n, units, desc_off, map_off, bytes;
+  int64_t n, units, desc_off, map_off, bytes, dev_bytes;
 };
 
 int64_t align_up(int64_t x, int64_t a) { return (x + a - 1) / a * a; }
@@ -224,11 +228,29 @@ int mx_quant(int fmt, const void* in, int in_dtype, int64_t rows, int64_t cols, 
   return run_single(cfg, d, stream);
 }
 
-int64_t table_layout(int64_t n, int64_t units, int64_t* desc_off, int64_t* map_off) {
+// Host table bytes; *map_off is also where the device table's map starts.
+int64_t table_layout(int64_t n, int64_t* desc_off, int64_t* map_off) {
   const int64_t h = align_up((int64_t)sizeof(GroupHeader), 256);
   *desc_off = h;
   *map_off = align_up(h + n * (int64_t)sizeof(Desc), 256);
-  return *map_off + units * 4;
+  return *map_off;
+}
+
+// Work-group -> tensor map, one thread per work-group: tensors own consecutive
+// ranges [unit0, unit0 + units) in table order (checked by lrq_group_pack), so
+// the owner of w is the LAST tensor with unit0 <= w; an empty tensor shares
+// its unit0 with a later one and is never picked.
+__global__ __launch_bounds__(256) void k_build_map(const Desc* __restrict__ descs, int64_t n,
+                                                   int64_t units, uint32_t* __restrict__ map) {
+  const int64_t w = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (w >= units) return;
+  int64_t lo = 0, hi = n;  // descs[lo].unit0 <= w, and every t >= hi has unit0 > w
+  while (hi - lo > 1) {
+    const int64_t mid = (lo + hi) / 2;
+    if (lrq::gld<int64_t>(&descs[mid].unit0) <= w) lo = mid;
+    else hi = mid;
+  }
+  lrq::gst<uint32_t>(map + w, (uint32_t)lo);
 }
 
 // Build the launch configuration and descriptors for a group; `ds` may be null
@@ -488,7 +510,7 @@ int64_t lrq_group_table_bytes(int fmt, const lrq_tensor* tensors, int64_t n, int
   if (int rc = plan_group(fmt, tensors, n, in_dtype, blk_r, blk_c, flags, &cfg, nullptr, &units))
     return rc;
   int64_t a, b;
-  return table_layout(n, units, &a, &b);
+  return table_layout(n, &a, &b);
 }
 
 int lrq_group_pack(int fmt, const lrq_tensor* tensors, int64_t n, int in_dtype, int64_t blk_r,
@@ -500,24 +522,50 @@ int lrq_group_pack(int fmt, const lrq_tensor* tensors, int64_t n, int in_dtype, 
   if (int rc = plan_group(fmt, tensors, n, in_dtype, blk_r, blk_c, flags, &cfg, nullptr, &units))
     return rc;
   GroupHeader h{};
-  const int64_t bytes = table_layout(n, units, &h.desc_off, &h.map_off);
+  const int64_t bytes = table_layout(n, &h.desc_off, &h.map_off);
   if (capacity < bytes)
     return fail(LRQ_ERR_CAPACITY, "table needs %lld bytes, have %lld", (long long)bytes, (long long)capacity);
   char* base = static_cast<char*>(host_table);
-  memset(base, 0, (size_t)h.map_off);
+  memset(base, 0, (size_t)bytes);
   Desc* ds = reinterpret_cast<Desc*>(base + h.desc_off);
   if (int rc = plan_group(fmt, tensors, n, in_dtype, blk_r, blk_c, flags, &cfg, ds, &units)) return rc;
-  uint32_t* map = reinterpret_cast<uint32_t*>(base + h.map_off);
-  for (int64_t i = 0; i < n; ++i)
-    for (int64_t w = 0; w < ds[i].units; ++w) map[ds[i].unit0 + w] = (uint32_t)i;
+  for (int64_t i = 0, next = 0; i < n; next += ds[i].units, ++i)  // the order k_build_map relies on
+    if (ds[i].unit0 != next || ds[i].units < 0)
+      return fail(LRQ_ERR_TABLE, "tensor %lld: work-groups out of table order", (long long)i);
   h.magic = kMagic;
   h.version = kTableVersion;
   h.cfg = cfg;
   h.n = n;
   h.units = units;
   h.bytes = bytes;
+  h.dev_bytes = h.map_off + units * 4;
   memcpy(base, &h, sizeof(h));
   return 0;
+}
+
+int64_t lrq_group_device_bytes(const void* host_table) {
+  g_err.clear();
+  if (!host_table) return fail(LRQ_ERR_ARG, "null table");
+  GroupHeader h;
+  memcpy(&h, host_table, sizeof(h));
+  if (h.magic != kMagic || h.version != kTableVersion) return fail(LRQ_ERR_TABLE, "not an lrq table");
+  return h.dev_bytes;
+}
+
+int lrq_group_build_map(const void* host_table, void* device_table, lrq_stream_t stream) {
+  g_err.clear();
+  if (!host_table || !device_table) return fail(LRQ_ERR_ARG, "null table");
+  GroupHeader h;
+  memcpy(&h, host_table, sizeof(h));
+  if (h.magic != kMagic || h.version != kTableVersion) return fail(LRQ_ERR_TABLE, "not an lrq table");
+  if (!aligned(device_table, 256)) return fail(LRQ_ERR_ALIGN, "device table must be 256-byte aligned");
+  if (h.units == 0) return 0;
+  char* dev = static_cast<char*>(device_table);
+  const int64_t grid = (h.units + 255) / 256;
+  hipLaunchKernelGGL(k_build_map, dim3((unsigned)grid), dim3(256), 0, (hipStream_t)stream,
+                     reinterpret_cast<const Desc*>(dev + h.desc_off), h.n, h.units,
+                     reinterpret_cast<uint32_t*>(dev + h.map_off));
+  return check_hip(hipGetLastError(), "kernel launch");
 }
 
 int lrq_quant_grouped(const void* host_table, const void* device_table, lrq_stream_t stream) {

@@ -331,11 +331,16 @@ class _GroupLaunch:
         # is never overwritten while an earlier launch may still read it.  The
         # copy is from pinned memory and does not block the host (a pageable
         # copy would wait for the stream to drain, serializing plan building,
-        # e.g. every quantize_state_dict call, with the device).
-        self.dev = torch.empty(int(need), dtype=torch.uint8, device=device)
+        # e.g. every quantize_state_dict call, with the device).  Only the
+        # header and descriptors travel; the device writes the work-group map
+        # behind them itself (4 bytes per work-group: 8 MB for a whole 8B state).
+        self.dev = torch.empty(int(L.lrq_group_device_bytes(self.host.data_ptr())),
+                               dtype=torch.uint8, device=device)
         with _on(device):
             self.home = torch.cuda.current_stream(device)
-            self.dev.copy_(self.host, non_blocking=True)
+            self.dev[: int(need)].copy_(self.host, non_blocking=True)
+            rc = L.lrq_group_build_map(self.host.data_ptr(), self.dev.data_ptr(), _stream(device))
+            _lib.check(rc, "lrq_group_build_map")
             self.ready = torch.cuda.Event()
             self.ready.record(self.home)
         self.device = device

@@ -128,8 +128,11 @@ int main() {
   std::vector<uint8_t> host_table((size_t)bytes);
   LRQ(lrq_group_pack(LRQ_FMT_FP8_BLOCK, ts, 2, LRQ_DTYPE_BF16, 128, 128, 0, host_table.data(), bytes));
   void* dev_table;
-  HIP(hipMalloc(&dev_table, (size_t)bytes));
+  const int64_t dev_bytes = lrq_group_device_bytes(host_table.data());
+  if (dev_bytes < bytes) LRQ((int)dev_bytes);
+  HIP(hipMalloc(&dev_table, (size_t)dev_bytes));
   HIP(hipMemcpy(dev_table, host_table.data(), (size_t)bytes, hipMemcpyHostToDevice));
+  LRQ(lrq_group_build_map(host_table.data(), dev_table, (lrq_stream_t)st));
   for (int i = 0; i < 2; ++i) HIP(hipMemset(dcodes[i], 0xAB, (size_t)(R[i] * C[i])));
   LRQ(lrq_quant_grouped(host_table.data(), dev_table, (lrq_stream_t)st));
   HIP(hipStreamSynchronize(st));
@@ -188,8 +191,9 @@ int main() {
     std::vector<uint8_t> ht((size_t)tb);
     LRQ(lrq_group_pack(LRQ_FMT_TENSOR_SCALE, tt, 2, LRQ_DTYPE_BF16, 1, 1, 0, ht.data(), tb));
     void* dt;
-    HIP(hipMalloc(&dt, (size_t)tb));
+    HIP(hipMalloc(&dt, (size_t)lrq_group_device_bytes(ht.data())));
     HIP(hipMemcpy(dt, ht.data(), (size_t)tb, hipMemcpyHostToDevice));
+    LRQ(lrq_group_build_map(ht.data(), dt, (lrq_stream_t)st));
     const int64_t wsb = lrq_group_workspace_bytes(ht.data());
     void* dws;
     HIP(hipMalloc(&dws, (size_t)wsb));

@@ -119,9 +119,15 @@ def test_group_pack_tiles_qwen3_layer():
     units = L().lrq_group_units(buf.ctypes.data)
     tiles = [(r // 128) * (c // 128) for _, r, c in QWEN3_8B_LAYER]
     assert units == sum(tiles)
-    # the work-group -> tensor map is the tail of the table
-    wmap = buf[-4 * units:].view(np.uint32)
-    assert np.array_equal(wmap, np.repeat(np.arange(7, dtype=np.uint32), tiles))
+    # host table: a 256-byte header, then one 112-byte descriptor per tensor whose
+    # work-groups [unit0, unit0 + units) follow table order (the device map relies on it)
+    assert buf.size == 256 + -(-7 * 112 // 256) * 256
+    d = buf[256:256 + 7 * 112].view(np.int64).reshape(7, 14)
+    assert np.array_equal(d[:, 8], np.cumsum([0] + tiles[:-1])) and np.array_equal(d[:, 9], tiles)
+    # the device table adds 4 bytes of work-group -> tensor map per work-group
+    assert L().lrq_group_device_bytes(buf.ctypes.data) == buf.size + 4 * units
+    assert L().lrq_group_device_bytes(None) == _lib.ERR_ARG
+    assert L().lrq_group_build_map(None, None, None) == _lib.ERR_ARG
 
 
 def test_group_pack_rows_and_mx_units():
@@ -169,8 +175,9 @@ def test_tensor_scale_tables():
     units = [4096 * 4096 // 4096, 1024 * 4096 // 4096, 1024 * 4096 // 4096, -(-300 * 100 // 8192)]
     assert L().lrq_group_units(buf.ctypes.data) == sum(units)
     assert L().lrq_group_workspace_bytes(buf.ctypes.data) == 4 * sum(units)
-    wmap = buf[-4 * sum(units):].view(np.uint32)
-    assert np.array_equal(wmap, np.repeat(np.arange(4, dtype=np.uint32), units))
+    d = buf[256:256 + 4 * 112].view(np.int64).reshape(4, 14)
+    assert np.array_equal(d[:, 8], np.cumsum([0] + units[:-1])) and np.array_equal(d[:, 9], units)
+    assert L().lrq_group_device_bytes(buf.ctypes.data) == need + 4 * sum(units)
     # argument errors are reported before any device work
     assert L().lrq_quant_grouped(buf.ctypes.data, buf.ctypes.data, None) == _lib.ERR_ARG
     assert "workspace" in _lib.last_error()
@@ -244,6 +251,8 @@ def test_group_units_rejects_null_and_foreign_tables():
     assert L().lrq_group_units(None) == _lib.ERR_ARG and "null" in _lib.last_error()
     junk = np.zeros(4096, np.uint8)
     assert L().lrq_group_units(junk.ctypes.data) == _lib.ERR_TABLE
+    assert L().lrq_group_device_bytes(junk.ctypes.data) == _lib.ERR_TABLE
+    assert L().lrq_group_build_map(junk.ctypes.data, ctypes.c_void_p(0x1000), None) == _lib.ERR_TABLE
 
 
 def test_cast_tables():

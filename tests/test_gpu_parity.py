@@ -292,7 +292,7 @@ def test_tiles_across_tensors_batches_and_edges():
     assert_fp8_matches_oracle(base[:, :200, :264], (128, 128))    # batch stride != rows * ld
     say("tiles: grouped ragged tensors")
     shapes = [(1000, 8), (130, 136), (2, 128, 128), (257, 384), (3, 136, 264), (129, 1032)]
-    ws = [weights(s).to(DEV) for s in shapes]
+    ws = [(weights(s) if s[0] else torch.zeros(s, dtype=torch.bfloat16)).to(DEV) for s in shapes]
     ws[1][129, 135] = float("inf")
     ws[3][256, :] = 0.0
     for n in (1, 2, 3, len(ws)):                                   # 8 .. 60 tiles per launch
@@ -409,6 +409,39 @@ def test_grouped_qwen3_layer_matches_oracle(fmt, blk):
     if fmt == "fp8_block":
         oc, osc = O.fp8_block_quant(host_bits(ws[0]), "bf16", "f32", blk)
         assert np.array_equal(u8(plan.outputs[0][0]).reshape(oc.shape), oc)
+
+
+def test_device_built_work_group_map():
+    """lrq_group_build_map writes map[w] = the tensor owning work-group w, empty
+    tensors (first, between, last) owning none, as a host loop over the
+    descriptors' [unit0, unit0 + units) ranges would."""
+    shapes = [(0, 4096), (256, 4096), (0, 128), (0, 4096), (4096, 4096), (128, 128), (0, 128)]
+    ws = [(weights(s) if s[0] else torch.zeros(s, dtype=torch.bfloat16)).to(DEV) for s in shapes]
+    say("device map", shapes)
+    L = _lib.lib()
+    descs = (_lib.LrqTensor * len(ws))()
+    outs = []
+    for i, w in enumerate(ws):
+        c = torch.empty(w.shape, dtype=torch.float8_e4m3fn, device=DEV)
+        s = torch.empty((-(-w.shape[0] // 128), w.shape[1] // 128), dtype=torch.float32, device=DEV)
+        outs.append((c, s))
+        descs[i].in_, descs[i].codes, descs[i].scales = w.data_ptr(), c.data_ptr(), s.data_ptr()
+        descs[i].batch, descs[i].rows, descs[i].cols = 1, w.shape[0], w.shape[1]
+        descs[i].ld, descs[i].batch_stride = w.shape[1], w.numel()
+    launch = ops._GroupLaunch("fp8_block", descs, len(ws), _lib.DTYPE_BF16, (128, 128), 0, DEV)
+    tiles = [(r // 128) * (c // 128) for r, c in shapes]
+    assert launch.units == sum(tiles)
+    host_bytes = launch.host.numel()
+    torch.cuda.synchronize()
+    wmap = launch.dev[host_bytes:].cpu().numpy().view(np.uint32)
+    assert np.array_equal(wmap, np.repeat(np.arange(len(shapes), dtype=np.uint32), tiles))
+    launch.run()
+    torch.cuda.synchronize()
+    for w, (c, s) in zip(ws, outs):
+        if w.numel():
+            oc, osc = O.fp8_block_quant(host_bits(w), "bf16", "f32", (128, 128))
+            assert np.array_equal(u8(c).reshape(oc.shape), oc)
+            assert np.array_equal(scale_bits(s).reshape(-1), osc.view(np.uint32).reshape(-1))
 
 
 def test_grouped_expert_stacks_single_launch():
