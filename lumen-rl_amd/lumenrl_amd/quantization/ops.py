@@ -318,6 +318,11 @@ class _GroupLaunch:
     def __init__(self, fmt: str, descs, n: int, in_dtype: int, block: tuple[int, int],
                  flags: int, device: torch.device) -> None:
         L = _lib.lib()
+        with _on(device):
+            if torch.cuda.is_current_stream_capturing():
+                # a captured upload would re-read this plan's pinned table on every
+                # replay, after the plan (and its table) may be gone
+                raise RuntimeError("build lrq plans before HIP graph capture; capture only run()")
         br, bc = int(block[0]), int(block[1])
         need = L.lrq_group_table_bytes(_FMTS[fmt], descs, n, in_dtype, br, bc, flags)
         if need < 0:

@@ -106,6 +106,23 @@ def test_graph_replay_of_grouped_launches():
         assert np.array_equal(f32bits(act_out), O.act_qdq(host_in(xa, "bf16"), "bf16", 128).view(np.uint32))
 
 
+@pytest.mark.filterwarnings("ignore:The CUDA Graph is empty")  # the refused capture records nothing
+def test_plan_built_under_capture_is_refused():
+    """A plan's table upload inside a capture would replay from a host buffer
+    the plan frees; building one there raises before any device work."""
+    w = torch.zeros(256, 256, dtype=torch.bfloat16, device=DEV)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with pytest.raises(RuntimeError, match="before HIP graph capture"):
+        with torch.cuda.graph(graph):
+            QuantPlan([w], "fp8_block", (128, 128))
+    torch.cuda.synchronize()
+    plan = QuantPlan([w], "fp8_block", (128, 128))  # outside a capture it builds and runs
+    plan.run()
+    torch.cuda.synchronize()
+    assert torch.all(plan.outputs[0][0].view(torch.uint8) == 0)
+
+
 def test_random_shape_sweep():
     """Seeded random shapes, strides, dtypes and blocks through every kernel family."""
     rng = np.random.default_rng(2026)
