@@ -58,7 +58,7 @@ QWEN3_8B = [("q_proj", 4096, 4096), ("k_proj", 1024, 4096), ("v_proj", 1024, 409
             ("down_proj", 4096, 12288)]
 
 
-PROFILE_FOR = {"c2": "k_tile128_qwen3_8b_fp8_128x128", "c2r": "k_row_qwen3_8b_fp8_1x128",
+PROFILE_FOR = {"c1": "k_tile128_single_4096x4096_c1", "c2": "k_tile128_qwen3_8b_fp8_128x128", "c2r": "k_row_qwen3_8b_fp8_1x128",
                "c3": "k_tile128_qwen3_30b_a3b_experts", "c4": "k_mx_qwen3_8b_mxfp8",
                "c5": "k_mx_qwen3_8b_mxfp4", "c2d": "k_dequant_qwen3_8b_fp8_1x128_to_bf16",
                "act": "k_act_qdq_qwen3_8b_prefill_8192", "kv": "k_amax_qwen3_8b_qkv_scales",
