@@ -258,6 +258,7 @@ __global__ __launch_bounds__(256) void k_build_map(const Desc* __restrict__ desc
 int plan_group(int fmt, const lrq_tensor* ts, int64_t n, int in_dtype, int64_t blk_r,
                int64_t blk_c, unsigned flags, LaunchCfg* cfg_out, Desc* ds, int64_t* units_out) {
   if (n < 0 || (n > 0 && !ts)) return fail(LRQ_ERR_ARG, "bad tensor list");
+  if (n > 0xFFFFFFFFll) return fail(LRQ_ERR_ARG, "more than 2^32 tensors in one table");  // uint32 map
   if (!valid_dtype(in_dtype)) return fail(LRQ_ERR_ARG, "bad input dtype %d", in_dtype);
   LaunchCfg cfg{};
   cfg.in_dtype = in_dtype;
