@@ -3,8 +3,8 @@
 Same class, method, arguments, config keys and log texts.  With FP8 enabled the
 reference casts every floating tensor of the state dict with
 ``tensor.to(torch.float8_e4m3fn)`` (unscaled, :19-43) one tensor at a time;
-here every device tensor of one dtype goes through ONE grouped liblrq launch
-whose bytes equal torch's cast (round to nearest even; |x| rounding past 448,
+here the tensors of one dtype go through a few grouped liblrq launches (8, 16,
+32, then 64 tensors each, issued as each is planned) whose bytes equal torch's cast (round to nearest even; |x| rounding past 448,
 +-inf and NaN -> NaN 0x7F|sign).  CPU tensors are staged through the current
 HIP device and come back on the CPU, as the reference returns them.
 
@@ -66,7 +66,7 @@ def _kernel_input(t: torch.Tensor, device: torch.device) -> torch.Tensor:
 
 
 def _cast_all(tensors: dict[str, torch.Tensor]) -> dict[str, torch.Tensor]:
-    """e4m3fn casts of ``tensors``: one grouped launch per (device, dtype)."""
+    """e4m3fn casts of ``tensors``: chunked grouped launches per (device, dtype)."""
     dev = None
     staged: dict[str, torch.Tensor] = {}
     for name, t in tensors.items():
@@ -86,10 +86,11 @@ def _cast_all(tensors: dict[str, torch.Tensor]) -> dict[str, torch.Tensor]:
         if not x.numel():
             out[name] = torch.empty(tensors[name].shape, dtype=torch.float8_e4m3fn,
                                     device=tensors[name].device)
-    for names in groups.values():
-        plan = ops.CastPlan([staged[n] for n in names])
-        for n, q in zip(names, plan.run()):
-            out[n] = q if tensors[n].is_cuda else q.to(tensors[n].device)
+    for group in groups.values():
+        for names in ops.launch_chunks(group):
+            plan = ops.CastPlan([staged[n] for n in names])
+            for n, q in zip(names, plan.run()):
+                out[n] = q if tensors[n].is_cuda else q.to(tensors[n].device)
     return out
 
 
@@ -114,9 +115,10 @@ def _scaled(tensors: dict[str, torch.Tensor], block: tuple[int, int],
             results[name] = (torch.empty(x.shape, dtype=torch.float8_e4m3fn, device=x.device),
                              torch.empty((*lead, -(-r // block[0]), -(-c // block[1])),
                                          dtype=torch.float32, device=x.device))
-    for names in groups.values():
-        plan = ops.QuantPlan([picked[n] for n in names], "fp8_block", block)
-        results.update(zip(names, plan.run()))
+    for group in groups.values():
+        for names in ops.launch_chunks(group):
+            plan = ops.QuantPlan([picked[n] for n in names], "fp8_block", block)
+            results.update(zip(names, plan.run()))
     out: dict[str, torch.Tensor] = {}
     for name, t in tensors.items():
         if name not in results:

@@ -384,6 +384,19 @@ class _GroupLaunch:
         _lib.check(rc, "lrq_tensor_scale_grouped")
 
 
+def launch_chunks(items: Sequence, first: int = 8, most: int = 64):
+    """Consecutive slices of ``items`` for the per-call drop-ins (quantize_state_dict,
+    dequantize_state_dict, load_weights): 8, 16, 32, then ``most`` tensors per grouped
+    launch.  Each slice is launched as soon as its plan is built, so the device starts on
+    the first tensors while the host still plans the rest (the planning costs a few
+    microseconds per tensor, the launch tens of them)."""
+    i, n = 0, first
+    while i < len(items):
+        yield items[i:i + n]
+        i += n
+        n = min(2 * n, most)
+
+
 def _nbytes(t: Tensor) -> int:
     return t.numel() * t.element_size()
 

@@ -11,8 +11,10 @@ x86 CPU:
   (torch's vectorized x86 kernels; its scalar tail loop writes 0x7FC0/0x7F).
 * ``quantize_state_dict`` upcasts to float32 (:109); for bf16/fp16 weights the
   upcast is exact, so the kernel reads them directly in float32 arithmetic and
-  writes the bf16 ``_fp8_scales`` sidecar itself (:111).  All eligible weights
-  go through ONE grouped kernel launch.
+  writes the bf16 ``_fp8_scales`` sidecar itself (:111).  The eligible weights
+  go through a few grouped kernel launches (8, 16, 32, then 64 tensors each),
+  each issued as soon as it is planned, so the device works while the host
+  plans the rest.
 
 Tensors on the CPU are staged through the current HIP device and the results
 copied back, so the reference's CPU-tensor call sites keep working; there is no
@@ -144,11 +146,12 @@ class WeightQuantizer:
             else:
                 results[key] = ops.fp8_block_quant(x, (1, 128), pow2=pow2,
                                                    scale_dtype=torch.bfloat16)
-        for keys in groups.values():
-            plan = ops.QuantPlan([staged[k][0] for k in keys], "fp8_block", (1, 128),
-                                 use_pow2_scale=pow2, scale_dtype=torch.bfloat16)
-            plan.run()
-            results.update(zip(keys, plan.outputs))
+        for group in groups.values():
+            for keys in ops.launch_chunks(group):
+                plan = ops.QuantPlan([staged[k][0] for k in keys], "fp8_block", (1, 128),
+                                     use_pow2_scale=pow2, scale_dtype=torch.bfloat16)
+                plan.run()
+                results.update(zip(keys, plan.outputs))
 
         out: dict[str, Tensor | Any] = {}
         for key, value in state_dict.items():
@@ -171,8 +174,9 @@ class WeightQuantizer:
     def dequantize_state_dict(self, state_dict: dict[str, Tensor]) -> dict[str, Tensor | Any]:
         """Strip FP8 tensors back to BF16 weights using stored scales (:117-134).
 
-        Every (codes, scales) pair goes through ONE grouped kernel launch that
-        writes bf16 directly (fp32 product, then the bf16 cast of :133).
+        The (codes, scales) pairs go through grouped kernel launches (chunked as in
+        quantize_state_dict) that write bf16 directly (fp32 product, then the bf16
+        cast of :133).
         """
         consumed_suffixes = {"_fp8_scales", "_fp8_meta"}
         pending: dict[str, tuple[Tensor, Tensor, torch.device | None]] = {}
@@ -199,9 +203,10 @@ class WeightQuantizer:
                 groups.setdefault((s.dtype, q.device), []).append(key)
             else:
                 results[key] = ops.fp8_block_dequant(q, s, (1, 128), torch.bfloat16)
-        for keys in groups.values():
-            plan = ops.DequantPlan([pending[k][:2] for k in keys], (1, 128), torch.bfloat16)
-            results.update(zip(keys, plan.run()))
+        for group in groups.values():
+            for keys in ops.launch_chunks(group):
+                plan = ops.DequantPlan([pending[k][:2] for k in keys], (1, 128), torch.bfloat16)
+                results.update(zip(keys, plan.run()))
 
         out: dict[str, Tensor | Any] = {}
         for key, value in state_dict.items():

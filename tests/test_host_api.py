@@ -204,3 +204,23 @@ def test_bucket_layout_properties(fw, bucket_bytes):
         else:
             assert cn == lead * rows * (cols if fmt == "mxfp8" else cols // 2)
             assert sn == lead * rows * (cols // 32) and sdt == torch.uint8
+
+
+from lumenrl_amd.quantization.ops import launch_chunks  # noqa: E402
+
+
+@given(st.integers(min_value=0, max_value=1000))
+@settings(max_examples=60, deadline=None)
+def test_launch_chunks_cover_every_item_once_in_order(n):
+    """The drop-ins' launch slices: 8, 16, 32, then 64 items, in order, none lost."""
+    items = list(range(n))
+    chunks = list(launch_chunks(items))
+    assert [x for c in chunks for x in c] == items
+    sizes = [len(c) for c in chunks]
+    want = []
+    left, k = n, 8
+    while left > 0:
+        want.append(min(k, left))
+        left -= k
+        k = min(2 * k, 64)
+    assert sizes == want
