@@ -161,3 +161,24 @@ def test_single_call_entry_point_through_the_c_abi():
     _lib.check(rc, "lrq_cast_e4m3")
     torch.cuda.synchronize()
     assert np.array_equal(out.cpu().numpy(), torch_cast(x))
+
+
+def test_dynamic_weight_loader_over_several_launches():
+    """A 45-tensor state of two dtypes: each dtype's group launches in chunks
+    (8, 16, then the rest); every tensor equals torch's own cast, in key order."""
+    g = torch.Generator(device=DEV).manual_seed(8)
+    sd = {}
+    for i in range(45):
+        n = 1000 + 37 * i
+        t = torch.randn(n, generator=g, device=DEV) * (0.01 * (1 + i % 5))
+        if i % 11 == 4:
+            t[7] = float("inf")
+        sd[f"t{i}"] = t.to(torch.float16 if i % 3 == 0 else torch.bfloat16)
+    say("DynamicWeightLoader over several launches")
+    eng = _Engine()
+    DynamicWeightLoader.load_weights(eng, sd, fp8_config={"enabled": True})
+    assert list(eng.sd) == list(sd)
+    for k, t in sd.items():
+        q = eng.sd[k]
+        assert q.dtype == torch.float8_e4m3fn and q.shape == t.shape, k
+        assert np.array_equal(u8(q), torch_cast(t)), k

@@ -225,3 +225,35 @@ def test_back_to_back_state_dict_calls_keep_every_result():
             assert np.array_equal(bits(out[n]), oc[0]), n
             want_s = torch.from_numpy(osc[0]).to(torch.bfloat16)
             assert np.array_equal(bits(out[f"{n}_fp8_scales"]), bits(want_s)), n
+
+
+def test_state_dict_calls_spanning_several_launches():
+    """quantize_state_dict / dequantize_state_dict on 60 weights: the calls launch
+    in chunks of 8, 16, 32 and 4 tensors; every output matches the reference ops,
+    in key order, across the chunk boundaries."""
+    g = torch.Generator().manual_seed(31)
+    shapes = [(128, 256), (64, 384), (256, 128), (32, 512), (96, 640)]
+    sd = {}
+    for i in range(60):
+        r, c = shapes[i % len(shapes)]
+        w = (torch.randn(r, c, generator=g) * 0.02 * (1 + i % 7)).to(torch.bfloat16)
+        if i % 13 == 5:
+            w[1, 2] = float("nan")
+        if i % 17 == 3:
+            w[:, :128] = 0.0
+        sd[f"layers.{i}.weight"] = w
+        if i % 9 == 0:
+            sd[f"layers.{i}.norm"] = torch.ones(c)
+    print("state dict over several launches", len(sd), flush=True)
+    wq = WeightQuantizer(FP8Config())
+    out = wq.quantize_state_dict({k: v.to(DEV) for k, v in sd.items()})
+    ref = T.quantize_state_dict(sd)
+    assert list(out) == list(ref)
+    for k, rv in ref.items():
+        assert out[k].dtype == rv.dtype and tuple(out[k].shape) == tuple(rv.shape), k
+        assert np.array_equal(bits(out[k]), bits(rv)), k
+    back = wq.dequantize_state_dict(out)
+    rback = T.dequantize_state_dict(ref)
+    assert list(back) == list(rback)
+    for k, rv in rback.items():
+        assert np.array_equal(bits(back[k]), bits(rv)), k
