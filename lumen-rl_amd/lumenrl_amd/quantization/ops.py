@@ -339,8 +339,10 @@ class _GroupLaunch:
         # e.g. every quantize_state_dict call, with the device).  Only the
         # header and descriptors travel; the device writes the work-group map
         # behind them itself (4 bytes per work-group: 8 MB for a whole 8B state).
-        self.dev = torch.empty(int(L.lrq_group_device_bytes(self.host.data_ptr())),
-                               dtype=torch.uint8, device=device)
+        dev_bytes = int(L.lrq_group_device_bytes(self.host.data_ptr()))
+        if dev_bytes < 0:
+            _lib.check(dev_bytes, "lrq_group_device_bytes")
+        self.dev = torch.empty(dev_bytes, dtype=torch.uint8, device=device)
         with _on(device):
             self.home = torch.cuda.current_stream(device)
             self.dev[: int(need)].copy_(self.host, non_blocking=True)
