@@ -1,0 +1,108 @@
+"""Seeded random sweep of grouped launches against the oracle, on an MI355X.
+
+Each case is one plan over 1-12 tensors of random shape, dtype, row stride and
+magnitude (Student-t values, planted +-inf/NaN/zero/tiny/huge entries, zero
+rows): 128x128 and 1x128 FP8, MXFP8, MXFP4, the unscaled cast, per-tensor KV
+scales, and FP8 dequant of the 1x128 results to float32 and bf16.  Every code,
+scale and output bit is compared with the oracle.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle as O
+from lumenrl_amd.quantization import ops
+
+pytestmark = pytest.mark.gpu
+
+if not torch.cuda.is_available():  # pragma: no cover - CPU container
+    pytest.skip("needs a HIP device", allow_module_level=True)
+
+DEV = torch.device("cuda", 0)
+DT = {"bf16": torch.bfloat16, "f16": torch.float16, "f32": torch.float32}
+KINDS = ["tile", "row", "mx8", "mx4", "cast", "kv", "deq"]
+
+
+def host(t: torch.Tensor, dt: str) -> np.ndarray:
+    t = t.detach().cpu().contiguous()
+    return t.numpy() if dt == "f32" else t.view(torch.int16).numpy().view(np.uint16)
+
+
+def u8(t: torch.Tensor) -> np.ndarray:
+    return t.detach().cpu().contiguous().view(torch.uint8).numpy()
+
+
+def fbits(t: torch.Tensor) -> np.ndarray:
+    t = t.detach().cpu().contiguous()
+    return t.numpy().view(np.uint32) if t.dtype == torch.float32 else t.view(torch.int16).numpy().view(np.uint16)
+
+
+def _tensor(rng, rows, cols, dt, strided):
+    ld = cols + (8 * int(rng.integers(1, 9)) if strided else 0)
+    x = (rng.standard_t(4, (rows, ld)) * 10.0 ** rng.uniform(-4, 1)).astype(np.float32)
+    for _ in range(int(rng.integers(0, 3))):
+        x[rng.integers(0, rows), rng.integers(0, ld)] = rng.choice([np.inf, -np.inf, np.nan, 0.0, 1e-30, 6e4])
+    if rng.random() < 0.1:
+        r0 = int(rng.integers(0, rows))
+        x[r0:r0 + 3, :] = 0.0
+    t = torch.from_numpy(x).to(DT[dt]).to(DEV)
+    return t[:, :cols] if strided else t
+
+
+def _shape(rng, kind):
+    if kind == "tile":
+        return int(rng.integers(1, 600)), 8 * int(rng.integers(1, 120))
+    if kind in ("row", "deq"):
+        return int(rng.integers(1, 300)), 128 * int(rng.integers(1, 8))
+    if kind in ("mx8", "mx4"):
+        return int(rng.integers(1, 300)), 32 * int(rng.integers(1, 30))
+    return 1, int(rng.integers(1, 70000))
+
+
+@pytest.mark.parametrize("seed", [101, 202, 303])
+def test_grouped_plans_random_sweep(seed):
+    rng = np.random.default_rng(seed)
+    for case in range(60):
+        kind = KINDS[rng.integers(0, len(KINDS))]
+        dt = ["bf16", "f16", "f32"][rng.integers(0, 3)]
+        ts = []
+        for _ in range(int(rng.integers(1, 13))):
+            rows, cols = _shape(rng, kind)
+            strided = kind not in ("cast", "kv") and rng.random() < 0.3
+            ts.append(_tensor(rng, rows, cols, dt, strided))
+        print("group sweep", seed, case, kind, dt, [tuple(t.shape) for t in ts], flush=True)
+        if kind in ("tile", "row", "deq", "mx8", "mx4"):
+            fmt = {"mx8": "mxfp8", "mx4": "mxfp4"}.get(kind, "fp8_block")
+            blk = {"tile": (128, 128), "mx8": (1, 32), "mx4": (1, 32)}.get(kind, (1, 128))
+            outs = ops.QuantPlan(ts, fmt, blk).run()
+        elif kind == "cast":
+            outs = ops.CastPlan([t.reshape(-1) for t in ts]).run()
+        else:
+            scales = ops.TensorScalePlan(ts).run()
+        torch.cuda.synchronize()
+        for i, t in enumerate(ts):
+            xh = host(t, dt)
+            if kind in ("tile", "row", "deq"):
+                oc, osc = O.fp8_block_quant(xh, dt, "f32", (128, 128) if kind == "tile" else (1, 128))
+                assert np.array_equal(u8(outs[i][0]), oc[0]), (case, i)
+                assert np.array_equal(fbits(outs[i][1]).reshape(-1), osc[0].view(np.uint32).reshape(-1)), (case, i)
+            elif kind in ("mx8", "mx4"):
+                oc, osc = O.mx_quant(xh, dt, 8 if kind == "mx8" else 4)
+                assert np.array_equal(u8(outs[i][0]), oc) and np.array_equal(u8(outs[i][1]), osc), (case, i)
+            elif kind == "cast":
+                assert np.array_equal(u8(outs[i]), O.cast_e4m3(xh.reshape(-1), dt)), (case, i)
+            else:
+                assert fbits(scales)[i] == O.tensor_scale(xh, dt), (case, i)
+        if kind == "deq":
+            pairs = [(c.reshape(c.shape[0], -1), s) for c, s in outs]
+            for odt, oname in ((torch.float32, "f32"), (torch.bfloat16, "bf16")):
+                back = ops.DequantPlan(pairs, (1, 128), odt).run()
+                torch.cuda.synchronize()
+                for i, (c, s) in enumerate(pairs):
+                    want = O.fp8_block_dequant(u8(c), fbits(s).view(np.float32).reshape(s.shape), "f32",
+                                               (1, 128), oname)[0]
+                    assert np.array_equal(fbits(back[i]), want.view(np.uint32) if oname == "f32" else want), \
+                        (case, i, oname)
