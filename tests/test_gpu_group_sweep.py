@@ -2,9 +2,12 @@
 
 Each case is one plan over 1-12 tensors of random shape, dtype, row stride and
 magnitude (Student-t values, planted +-inf/NaN/zero/tiny/huge entries, zero
-rows): 128x128 and 1x128 FP8, MXFP8, MXFP4, the unscaled cast, per-tensor KV
-scales, and FP8 dequant of the 1x128 results to float32 and bf16.  Every code,
-scale and output bit is compared with the oracle.
+rows): 128x128 and 1x128 FP8 (float32 or native arithmetic, pow2 and bf16
+scale options), MXFP8, MXFP4, the unscaled cast, per-tensor KV scales, FP8
+dequant of the 1x128 results and MX dequant of the MX results, to float32 and
+bf16.  Every code, scale and output bit is compared with the oracle (MX dequant
+with the torch restatement, NaN payloads aside: they depend on torch's loop
+split, which a dedicated test pins).
 """
 
 from __future__ import annotations
@@ -14,6 +17,7 @@ import pytest
 import torch
 
 from oracle import oracle as O
+from oracle import torch_ref as TR
 from lumenrl_amd.quantization import ops
 
 pytestmark = pytest.mark.gpu
@@ -23,7 +27,7 @@ if not torch.cuda.is_available():  # pragma: no cover - CPU container
 
 DEV = torch.device("cuda", 0)
 DT = {"bf16": torch.bfloat16, "f16": torch.float16, "f32": torch.float32}
-KINDS = ["tile", "row", "mx8", "mx4", "cast", "kv", "deq"]
+KINDS = ["tile", "row", "mx8", "mx4", "cast", "kv", "deq", "mxdeq"]
 
 
 def host(t: torch.Tensor, dt: str) -> np.ndarray:
@@ -57,9 +61,15 @@ def _shape(rng, kind):
         return int(rng.integers(1, 600)), 8 * int(rng.integers(1, 120))
     if kind in ("row", "deq"):
         return int(rng.integers(1, 300)), 128 * int(rng.integers(1, 8))
-    if kind in ("mx8", "mx4"):
+    if kind in ("mx8", "mx4", "mxdeq"):
         return int(rng.integers(1, 300)), 32 * int(rng.integers(1, 30))
     return 1, int(rng.integers(1, 70000))
+
+
+def _same_or_both_nan(got: torch.Tensor, want: torch.Tensor) -> bool:
+    g, w = got.detach().cpu().float(), want.float()
+    nan = torch.isnan(g)
+    return bool(torch.equal(nan, torch.isnan(w))) and np.array_equal(fbits(got.cpu()[~nan]), fbits(want[~nan]))
 
 
 @pytest.mark.parametrize("seed", [101, 202, 303])
@@ -68,16 +78,22 @@ def test_grouped_plans_random_sweep(seed):
     for case in range(60):
         kind = KINDS[rng.integers(0, len(KINDS))]
         dt = ["bf16", "f16", "f32"][rng.integers(0, 3)]
+        native = kind in ("tile", "row") and dt != "f32" and rng.random() < 0.3
+        pow2 = kind in ("tile", "row") and rng.random() < 0.3
+        sbf16 = kind == "row" and not native and rng.random() < 0.3
         ts = []
         for _ in range(int(rng.integers(1, 13))):
             rows, cols = _shape(rng, kind)
             strided = kind not in ("cast", "kv") and rng.random() < 0.3
             ts.append(_tensor(rng, rows, cols, dt, strided))
-        print("group sweep", seed, case, kind, dt, [tuple(t.shape) for t in ts], flush=True)
-        if kind in ("tile", "row", "deq", "mx8", "mx4"):
-            fmt = {"mx8": "mxfp8", "mx4": "mxfp4"}.get(kind, "fp8_block")
-            blk = {"tile": (128, 128), "mx8": (1, 32), "mx4": (1, 32)}.get(kind, (1, 128))
-            outs = ops.QuantPlan(ts, fmt, blk).run()
+        mxf = int(rng.choice([8, 4])) if kind == "mxdeq" else (8 if kind == "mx8" else 4)
+        print("group sweep", seed, case, kind, dt, native, pow2, sbf16, [tuple(t.shape) for t in ts], flush=True)
+        if kind in ("tile", "row", "deq"):
+            outs = ops.QuantPlan(ts, "fp8_block", (128, 128) if kind == "tile" else (1, 128),
+                                 native_arith=native, use_pow2_scale=pow2,
+                                 scale_dtype=torch.bfloat16 if sbf16 else torch.float32).run()
+        elif kind in ("mx8", "mx4", "mxdeq"):
+            outs = ops.QuantPlan(ts, "mxfp8" if mxf == 8 else "mxfp4", (1, 32)).run()
         elif kind == "cast":
             outs = ops.CastPlan([t.reshape(-1) for t in ts]).run()
         else:
@@ -86,16 +102,25 @@ def test_grouped_plans_random_sweep(seed):
         for i, t in enumerate(ts):
             xh = host(t, dt)
             if kind in ("tile", "row", "deq"):
-                oc, osc = O.fp8_block_quant(xh, dt, "f32", (128, 128) if kind == "tile" else (1, 128))
+                oc, osc = O.fp8_block_quant(xh, dt, "native" if native else "f32",
+                                            (128, 128) if kind == "tile" else (1, 128), pow2)
                 assert np.array_equal(u8(outs[i][0]), oc[0]), (case, i)
-                assert np.array_equal(fbits(outs[i][1]).reshape(-1), osc[0].view(np.uint32).reshape(-1)), (case, i)
-            elif kind in ("mx8", "mx4"):
-                oc, osc = O.mx_quant(xh, dt, 8 if kind == "mx8" else 4)
+                want_s = O.bf16_from_f32(osc[0]) if sbf16 else osc[0]
+                want_s = want_s.view(np.uint32) if want_s.dtype == np.float32 else want_s
+                assert np.array_equal(fbits(outs[i][1]).reshape(-1), want_s.reshape(-1)), (case, i)
+            elif kind in ("mx8", "mx4", "mxdeq"):
+                oc, osc = O.mx_quant(xh, dt, mxf)
                 assert np.array_equal(u8(outs[i][0]), oc) and np.array_equal(u8(outs[i][1]), osc), (case, i)
             elif kind == "cast":
                 assert np.array_equal(u8(outs[i]), O.cast_e4m3(xh.reshape(-1), dt)), (case, i)
             else:
                 assert fbits(scales)[i] == O.tensor_scale(xh, dt), (case, i)
+        if kind == "mxdeq":
+            for odt in (torch.float32, torch.bfloat16):
+                back = ops.DequantPlan(outs, (1, 32), odt, fmt="mxfp8" if mxf == 8 else "mxfp4").run()
+                torch.cuda.synchronize()
+                for i, (c, s) in enumerate(outs):
+                    assert _same_or_both_nan(back[i], TR.mx_dequant(c.cpu(), s.cpu(), mxf, odt)), (case, i, odt)
         if kind == "deq":
             pairs = [(c.reshape(c.shape[0], -1), s) for c, s in outs]
             for odt, oname in ((torch.float32, "f32"), (torch.bfloat16, "bf16")):
