@@ -66,31 +66,26 @@ def _kernel_input(t: torch.Tensor, device: torch.device) -> torch.Tensor:
 
 
 def _cast_all(tensors: dict[str, torch.Tensor]) -> dict[str, torch.Tensor]:
-    """e4m3fn casts of ``tensors``: chunked grouped launches per (device, dtype)."""
+    """e4m3fn casts of ``tensors``: chunked grouped launches per (device, dtype),
+    issued while the rest is still being staged."""
     dev = None
-    staged: dict[str, torch.Tensor] = {}
+    host = any(not t.is_cuda for t in tensors.values())
+    launches = ops.ChunkedLaunches(lambda xs: ops.CastPlan(xs).run(), defer=host)
+    out = dict(tensors)
     for name, t in tensors.items():
         if t.dtype == torch.float8_e4m3fn:
             continue  # tensor.to(its own dtype) is the tensor itself
         if t.is_cuda:
-            staged[name] = _kernel_input(t, t.device)
+            x = _kernel_input(t, t.device)
         else:
             dev = dev or ops.require_device()
-            staged[name] = _kernel_input(t, dev)
-    groups: dict[tuple[torch.device, torch.dtype], list[str]] = {}
-    for name, x in staged.items():
+            x = _kernel_input(t, dev)
         if x.numel():
-            groups.setdefault((x.device, x.dtype), []).append(name)
-    out = dict(tensors)
-    for name, x in staged.items():
-        if not x.numel():
-            out[name] = torch.empty(tensors[name].shape, dtype=torch.float8_e4m3fn,
-                                    device=tensors[name].device)
-    for group in groups.values():
-        for names in ops.launch_chunks(group):
-            plan = ops.CastPlan([staged[n] for n in names])
-            for n, q in zip(names, plan.run()):
-                out[n] = q if tensors[n].is_cuda else q.to(tensors[n].device)
+            launches.add((x.device, x.dtype), name, x)
+        else:
+            out[name] = torch.empty(t.shape, dtype=torch.float8_e4m3fn, device=t.device)
+    for n, q in launches.flush().items():
+        out[n] = q if tensors[n].is_cuda else q.to(tensors[n].device)
     return out
 
 

@@ -386,6 +386,49 @@ class _GroupLaunch:
         _lib.check(rc, "lrq_tensor_scale_grouped")
 
 
+class ChunkedLaunches:
+    """Grouped launches issued while the caller is still collecting tensors.
+
+    ``add(group, name, item)`` files an item under a group key such as
+    (dtype, device); a group calls ``run(items) -> outputs`` as soon as it holds
+    the next chunk size (8, 16, 32, then 64), so the device starts on the first
+    tensors of a state dict while the host still stages and plans the rest.
+    ``flush()`` runs what is left and returns ``{name: output}``.  With
+    ``defer`` every launch waits for ``flush()`` (same chunk sizes): callers that
+    stage host tensors use it, since a blocking host-to-device copy would
+    otherwise wait for the launches queued before it.
+    """
+
+    def __init__(self, run, *, defer: bool = False, first: int = 8, most: int = 64) -> None:
+        self._run, self._defer, self._first, self._most = run, defer, first, most
+        self._groups: dict = {}
+        self.results: dict = {}
+
+    def add(self, group, name, item) -> None:
+        g = self._groups.get(group)
+        if g is None:
+            g = self._groups[group] = {"names": [], "items": [], "next": self._first}
+        g["names"].append(name)
+        g["items"].append(item)
+        if not self._defer and len(g["names"]) == g["next"]:
+            self._launch(g["names"], g["items"])
+            g["names"], g["items"] = [], []
+            g["next"] = min(2 * g["next"], self._most)
+
+    def _launch(self, names, items) -> None:
+        self.results.update(zip(names, self._run(items)))
+
+    def flush(self) -> dict:
+        for g in self._groups.values():
+            names, items = g["names"], g["items"]
+            i = 0
+            for chunk in launch_chunks(names, g["next"], self._most):
+                self._launch(chunk, items[i:i + len(chunk)])
+                i += len(chunk)
+            g["names"], g["items"] = [], []
+        return self.results
+
+
 def launch_chunks(items: Sequence, first: int = 8, most: int = 64):
     """Consecutive slices of ``items`` for the per-call drop-ins (quantize_state_dict,
     dequantize_state_dict, load_weights): 8, 16, 32, then ``most`` tensors per grouped

@@ -127,31 +127,36 @@ class WeightQuantizer:
 
     def quantize_state_dict(self, state_dict: dict[str, Tensor]) -> dict[str, Tensor | Any]:
         """Return a new dict with 2-D float weights converted to FP8 + sidecar scales (:91-115)."""
-        staged: dict[str, tuple[Tensor, torch.device | None]] = {}
-        for key, value in state_dict.items():
-            if self._eligible(value):
-                x, home = _stage(value)
-                if x.dtype == torch.float64:
-                    x = x.to(torch.float32)  # the reference's own upcast (:109)
-                staged[key] = (x if x.is_contiguous() else x.contiguous(), home)
-
         pow2 = self._config.use_weight_pow2_scale
+
+        def run(xs: list[Tensor]) -> list[tuple[Tensor, Tensor]]:
+            plan = ops.QuantPlan(xs, "fp8_block", (1, 128), use_pow2_scale=pow2,
+                                 scale_dtype=torch.bfloat16)
+            plan.run()
+            return plan.outputs
+
+        # Grouped launches per (dtype, device) for 16-byte aligned weights,
+        # issued while the rest is still being staged; anything else is
+        # quantized by a single launch.
+        host = any(isinstance(v, Tensor) and not v.is_cuda and self._eligible(v)
+                   for v in state_dict.values())
+        launches = ops.ChunkedLaunches(run, defer=host)
+        staged: dict[str, tuple[Tensor, torch.device | None]] = {}
         results: dict[str, tuple[Tensor, Tensor]] = {}
-        # One grouped kernel launch per (dtype, device) for 16-byte aligned
-        # weights; anything else is quantized by a single launch.
-        groups: dict[tuple[torch.dtype, torch.device], list[str]] = {}
-        for key, (x, _) in staged.items():
+        for key, value in state_dict.items():
+            if not self._eligible(value):
+                continue
+            x, home = _stage(value)
+            if x.dtype == torch.float64:
+                x = x.to(torch.float32)  # the reference's own upcast (:109)
+            x = x if x.is_contiguous() else x.contiguous()
+            staged[key] = (x, home)
             if x.data_ptr() % 16 == 0 and x.numel() > 0:
-                groups.setdefault((x.dtype, x.device), []).append(key)
+                launches.add((x.dtype, x.device), key, x)
             else:
                 results[key] = ops.fp8_block_quant(x, (1, 128), pow2=pow2,
                                                    scale_dtype=torch.bfloat16)
-        for group in groups.values():
-            for keys in ops.launch_chunks(group):
-                plan = ops.QuantPlan([staged[k][0] for k in keys], "fp8_block", (1, 128),
-                                     use_pow2_scale=pow2, scale_dtype=torch.bfloat16)
-                plan.run()
-                results.update(zip(keys, plan.outputs))
+        results.update(launches.flush())
 
         out: dict[str, Tensor | Any] = {}
         for key, value in state_dict.items():
@@ -180,6 +185,10 @@ class WeightQuantizer:
         """
         consumed_suffixes = {"_fp8_scales", "_fp8_meta"}
         pending: dict[str, tuple[Tensor, Tensor, torch.device | None]] = {}
+        results: dict[str, Tensor] = {}
+        host = any(isinstance(v, Tensor) and not v.is_cuda for v in state_dict.values())
+        launches = ops.ChunkedLaunches(
+            lambda pairs: ops.DequantPlan(pairs, (1, 128), torch.bfloat16).run(), defer=host)
         for key, value in state_dict.items():
             if any(key.endswith(sfx) for sfx in consumed_suffixes) or not isinstance(value, Tensor):
                 continue
@@ -194,19 +203,13 @@ class WeightQuantizer:
             leading = 1
             for d in value.shape[:-1]:
                 leading *= int(d)
-            pending[key] = (q.contiguous().reshape(leading, last),
-                         s.contiguous().reshape(leading, last // 128), home)
-        results: dict[str, Tensor] = {}
-        groups: dict[tuple[torch.dtype, torch.device], list[str]] = {}
-        for key, (q, s, _) in pending.items():
+            q, s = q.contiguous().reshape(leading, last), s.contiguous().reshape(leading, last // 128)
+            pending[key] = (q, s, home)
             if q.numel() > 0 and q.data_ptr() % 16 == 0:
-                groups.setdefault((s.dtype, q.device), []).append(key)
+                launches.add((s.dtype, q.device), key, (q, s))
             else:
                 results[key] = ops.fp8_block_dequant(q, s, (1, 128), torch.bfloat16)
-        for group in groups.values():
-            for keys in ops.launch_chunks(group):
-                plan = ops.DequantPlan([pending[k][:2] for k in keys], (1, 128), torch.bfloat16)
-                results.update(zip(keys, plan.run()))
+        results.update(launches.flush())
 
         out: dict[str, Tensor | Any] = {}
         for key, value in state_dict.items():
