@@ -224,3 +224,29 @@ def test_launch_chunks_cover_every_item_once_in_order(n):
         left -= k
         k = min(2 * k, 64)
     assert sizes == want
+
+
+from lumenrl_amd.quantization.ops import ChunkedLaunches  # noqa: E402
+
+
+@pytest.mark.parametrize("defer", [False, True])
+def test_chunked_launches_schedule_and_results(defer):
+    """Groups launch 8, 16, 32, then 64 items each (eagerly, or all at flush when
+    deferred); results map every name to its own output; groups never mix."""
+    calls = []
+
+    def run(items):
+        calls.append(list(items))
+        return [x * 10 for x in items]
+
+    cl = ChunkedLaunches(run, defer=defer)
+    for i in range(150):
+        cl.add("a" if i % 3 else "b", f"n{i}", i)
+        if not defer and i == 30:
+            assert [len(c) for c in calls] == [8, 8]  # a: 8 of 20 so far; b: 8 of 11
+    res = cl.flush()
+    assert res == {f"n{i}": i * 10 for i in range(150)}
+    a_sizes = [len(c) for c in calls if c[0] % 3]
+    b_sizes = [len(c) for c in calls if c[0] % 3 == 0]
+    assert a_sizes == [8, 16, 32, 44] and b_sizes == [8, 16, 26]
+    assert all(len({x % 3 == 0 for x in c}) == 1 for c in calls)
