@@ -92,28 +92,25 @@ def _cast_all(tensors: dict[str, torch.Tensor]) -> dict[str, torch.Tensor]:
 def _scaled(tensors: dict[str, torch.Tensor], block: tuple[int, int],
             quantize_if: Callable[[str, torch.Tensor], bool]) -> dict[str, torch.Tensor]:
     """Blockwise FP8 + ``<name>_scale_inv`` for accepted tensors, the rest kept."""
-    picked: dict[str, torch.Tensor] = {}
     dev = None
-    for name, t in tensors.items():
-        if quantize_if(name, t):
-            if not t.is_cuda:
-                dev = dev or ops.require_device()
-            picked[name] = _kernel_input(t, t.device if t.is_cuda else dev)
-    groups: dict[tuple[torch.device, torch.dtype], list[str]] = {}
-    for name, x in picked.items():
-        if x.numel():
-            groups.setdefault((x.device, x.dtype), []).append(name)
+    host = any(not t.is_cuda for t in tensors.values() if isinstance(t, torch.Tensor))
+    launches = ops.ChunkedLaunches(lambda xs: ops.QuantPlan(xs, "fp8_block", block).run(),
+                                   defer=host)
     results: dict[str, tuple[torch.Tensor, torch.Tensor]] = {}
-    for name, x in picked.items():
-        if not x.numel():  # nothing to launch: empty codes and scales of the right shapes
+    for name, t in tensors.items():
+        if not quantize_if(name, t):
+            continue
+        if not t.is_cuda:
+            dev = dev or ops.require_device()
+        x = _kernel_input(t, t.device if t.is_cuda else dev)
+        if x.numel():
+            launches.add((x.device, x.dtype), name, x)
+        else:  # nothing to launch: empty codes and scales of the right shapes
             *lead, r, c = x.shape
             results[name] = (torch.empty(x.shape, dtype=torch.float8_e4m3fn, device=x.device),
                              torch.empty((*lead, -(-r // block[0]), -(-c // block[1])),
                                          dtype=torch.float32, device=x.device))
-    for group in groups.values():
-        for names in ops.launch_chunks(group):
-            plan = ops.QuantPlan([picked[n] for n in names], "fp8_block", block)
-            results.update(zip(names, plan.run()))
+    results.update(launches.flush())
     out: dict[str, torch.Tensor] = {}
     for name, t in tensors.items():
         if name not in results:
