@@ -63,7 +63,7 @@ PROFILE_FOR = {"c1": "k_tile128_single_4096x4096_c1", "c2": "k_tile128_qwen3_8b_
                "c5": "k_mx_qwen3_8b_mxfp4", "c2d": "k_dequant_qwen3_8b_fp8_1x128_to_bf16",
                "act": "k_act_qdq_qwen3_8b_prefill_8192", "kv": "k_amax_qwen3_8b_qkv_scales",
                "cast": "k_cast_e4m3_qwen3_8b_state_dynamic_weight_loader",
-               "c4d": "k_mx_dequant_qwen3_8b_mxfp8_to_bf16"}
+               "c4d": "k_mx_dequant_qwen3_8b_mxfp8_to_bf16", "c2sd": "k_row_qwen3_8b_state_dict_dropin"}
 KERNEL_FOR = {"c1": "k_tile128", "c2": "k_tile128", "c3": "k_tile128", "c4": "k_mx", "c5": "k_mx",
               "c2r": "k_row", "c2d": "k_dequant", "act": "k_act_qdq8", "kv": "k_amax", "c2sd": "k_row", "bucket": "k_tile128",
               "cast": "k_cast_e4m3", "c4d": "k_mx_dequant"}
