@@ -209,8 +209,8 @@ def test_back_to_back_state_dict_calls_keep_every_result():
     from oracle import oracle as O
 
     g = torch.Generator(device=DEV).manual_seed(21)
-    sd = {f"l{i}.weight": (torch.randn(1024, 2048, generator=g, device=DEV) * 0.02).to(torch.bfloat16)
-          for i in range(6)}
+    sd = {f"l{i}.weight": (torch.randn(512, 1024, generator=g, device=DEV) * 0.02).to(torch.bfloat16)
+          for i in range(20)}  # two chunked launches (8 + 12) per call
     wq = WeightQuantizer(FP8Config())
     outs = []
     for k in range(5):
