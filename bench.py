@@ -317,16 +317,20 @@ class _LoaderCall:
         self.loader.load_weights(self, self.sd, fp8_config={"enabled": True})
 
 
-class _ActCall:
-    """One activation fake-quant launch into a preallocated float32 output."""
+class _ActLayer:
+    """The activation fake-quant of one layer's linear inputs: one launch per
+    input, back to back, each into a preallocated float32 output.  Timed as one
+    span per step: an event pair around each 30-100 us launch would add its own
+    ~3 us to every launch."""
 
-    def __init__(self, torch, ops, x):
-        self.ops, self.x = ops, x
-        self.out = torch.empty(x.shape, dtype=torch.float32, device=x.device)
-        self.algorithmic_bytes = x.numel() * (x.element_size() + 4)
+    def __init__(self, torch, ops, xs):
+        self.ops, self.xs = ops, xs
+        self.outs = [torch.empty(x.shape, dtype=torch.float32, device=x.device) for x in xs]
+        self.algorithmic_bytes = sum(x.numel() * (x.element_size() + 4) for x in xs)
 
     def run(self):
-        self.ops.act_qdq(self.x, 128, out=self.out)
+        for x, out in zip(self.xs, self.outs):
+            self.ops.act_qdq(x, 128, out=out)
 
 
 # ---------------------------------------------------------------------------
@@ -431,7 +435,7 @@ def run(args):
             x[:, :: 97] *= 30.0  # outlier channels
             ws.append(x.to(torch.bfloat16))
             del x
-        plans = [_ActCall(torch, ops, x) for x in ws]
+        plans = [_ActLayer(torch, ops, ws)]
         workload = f"qwen3-8b-layer-act-fake-quant-1x128-prefill-{PREFILL_TOKENS}"
         cpu_ws, cpu_blk, cpu_fmt = ws, (1, 128), "act"
         extra = {"tensors": len(ws), "tokens": PREFILL_TOKENS, "elements": sum(x.numel() for x in ws),
