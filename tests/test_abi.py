@@ -325,3 +325,40 @@ def test_check_maps_codes_to_exceptions():
         _lib.check(_lib.ERR_TABLE, "x")
     with pytest.raises(_lib.LrqError):
         _lib.check(1, "x")
+
+
+from hypothesis import given, settings, strategies as st  # noqa: E402
+
+_FMT_BLK = [(_lib.FMT_FP8_BLOCK, (128, 128)), (_lib.FMT_FP8_BLOCK, (1, 128)), (_lib.FMT_FP8_BLOCK, (3, 40)),
+            (_lib.FMT_MXFP8, (1, 32)), (_lib.FMT_MXFP4, (1, 32)), (_lib.FMT_FP8_DEQUANT, (1, 128)),
+            (_lib.FMT_TENSOR_SCALE, (1, 1)), (_lib.FMT_COPY, (1, 1)), (_lib.FMT_CAST_E4M3, (1, 1)),
+            (_lib.FMT_MXFP8_DEQUANT, (1, 32)), (_lib.FMT_MXFP4_DEQUANT, (1, 32))]
+
+
+@given(fmt_blk=st.sampled_from(_FMT_BLK),
+       dims=st.lists(st.tuples(st.integers(-2, 4), st.integers(-2, 3000), st.integers(-2, 3000),
+                               st.integers(-8, 64), st.integers(0, 7)), min_size=1, max_size=6),
+       dtype=st.integers(-1, 3), flags=st.integers(0, 15))
+@settings(max_examples=400, deadline=None)
+def test_group_packer_never_crashes_and_is_consistent(fmt_blk, dims, dtype, flags):
+    """Random (often invalid) extents, strides, pointer offsets, dtypes and flags through
+    the table packer, host side only: every call returns 0 or an LRQ_ERR_* code, and a
+    table that sizes also packs, with units matching lrq_group_units."""
+    fmt, blk = fmt_blk
+    arr = (_lib.LrqTensor * len(dims))()
+    p = 0x100000000
+    for i, (b, r, c, pad, off) in enumerate(dims):
+        arr[i].in_, arr[i].codes, arr[i].scales = p + off, p + (1 << 32) + off, p + (2 << 32)
+        arr[i].batch, arr[i].rows, arr[i].cols = b, r, c
+        arr[i].ld, arr[i].batch_stride = c + pad, max(r, 0) * (c + pad)
+        p += 3 << 32
+    need = L().lrq_group_table_bytes(fmt, arr, len(dims), dtype, blk[0], blk[1], flags)
+    errs = {_lib.ERR_ARG, _lib.ERR_ALIGN, _lib.ERR_CAPACITY, _lib.ERR_TABLE}
+    if need < 0:
+        assert need in errs and _lib.last_error()
+        return
+    buf = np.zeros(need, np.uint8)
+    assert L().lrq_group_pack(fmt, arr, len(dims), dtype, blk[0], blk[1], flags, buf.ctypes.data, need) == 0
+    units = L().lrq_group_units(buf.ctypes.data)
+    assert units >= 0
+    assert L().lrq_group_device_bytes(buf.ctypes.data) == need + 4 * units
