@@ -2,8 +2,8 @@
 
 Each case is one plan over 1-12 tensors of random shape, dtype, row stride and
 magnitude (Student-t values, planted +-inf/NaN/zero/tiny/huge entries, zero
-rows): 128x128 and 1x128 FP8 (float32 or native arithmetic, pow2 and bf16
-scale options), MXFP8, MXFP4, the unscaled cast, per-tensor KV scales, FP8
+rows): 128x128, 1x128 and odd-block FP8 (float32 or native arithmetic, pow2
+and bf16 scale options), MXFP8, MXFP4, the unscaled cast, per-tensor KV scales, FP8
 dequant of the 1x128 results and MX dequant of the MX results, to float32 and
 bf16.  Every code, scale and output bit is compared with the oracle (MX dequant
 with the torch restatement, NaN payloads aside: they depend on torch's loop
@@ -27,7 +27,8 @@ if not torch.cuda.is_available():  # pragma: no cover - CPU container
 
 DEV = torch.device("cuda", 0)
 DT = {"bf16": torch.bfloat16, "f16": torch.float16, "f32": torch.float32}
-KINDS = ["tile", "row", "mx8", "mx4", "cast", "kv", "deq", "mxdeq"]
+KINDS = ["tile", "row", "mx8", "mx4", "cast", "kv", "deq", "mxdeq", "blk"]
+BLOCKS = [(1, 32), (1, 64), (1, 256), (1, 512), (3, 40), (64, 96), (128, 64), (2, 128)]
 
 
 def host(t: torch.Tensor, dt: str) -> np.ndarray:
@@ -61,6 +62,8 @@ def _shape(rng, kind):
         return int(rng.integers(1, 600)), 8 * int(rng.integers(1, 120))
     if kind in ("row", "deq"):
         return int(rng.integers(1, 300)), 128 * int(rng.integers(1, 8))
+    if kind == "blk":
+        return int(rng.integers(1, 200)), 8 * int(rng.integers(1, 80))
     if kind in ("mx8", "mx4", "mxdeq"):
         return int(rng.integers(1, 300)), 32 * int(rng.integers(1, 30))
     return 1, int(rng.integers(1, 70000))
@@ -78,19 +81,21 @@ def test_grouped_plans_random_sweep(seed):
     for case in range(60):
         kind = KINDS[rng.integers(0, len(KINDS))]
         dt = ["bf16", "f16", "f32"][rng.integers(0, 3)]
-        native = kind in ("tile", "row") and dt != "f32" and rng.random() < 0.3
-        pow2 = kind in ("tile", "row") and rng.random() < 0.3
+        native = kind in ("tile", "row", "blk") and dt != "f32" and rng.random() < 0.3
+        pow2 = kind in ("tile", "row", "blk") and rng.random() < 0.3
+        blk = BLOCKS[rng.integers(0, len(BLOCKS))] if kind == "blk" else (128, 128) if kind == "tile" else (1, 128)
         sbf16 = kind == "row" and not native and rng.random() < 0.3
         ts = []
+        blk_cols = _shape(rng, "blk")[1]  # one width per odd-block plan: one kernel for all
         for _ in range(int(rng.integers(1, 13))):
             rows, cols = _shape(rng, kind)
+            cols = blk_cols if kind == "blk" else cols
             strided = kind not in ("cast", "kv") and rng.random() < 0.3
             ts.append(_tensor(rng, rows, cols, dt, strided))
         mxf = int(rng.choice([8, 4])) if kind == "mxdeq" else (8 if kind == "mx8" else 4)
         print("group sweep", seed, case, kind, dt, native, pow2, sbf16, [tuple(t.shape) for t in ts], flush=True)
-        if kind in ("tile", "row", "deq"):
-            outs = ops.QuantPlan(ts, "fp8_block", (128, 128) if kind == "tile" else (1, 128),
-                                 native_arith=native, use_pow2_scale=pow2,
+        if kind in ("tile", "row", "deq", "blk"):
+            outs = ops.QuantPlan(ts, "fp8_block", blk, native_arith=native, use_pow2_scale=pow2,
                                  scale_dtype=torch.bfloat16 if sbf16 else torch.float32).run()
         elif kind in ("mx8", "mx4", "mxdeq"):
             outs = ops.QuantPlan(ts, "mxfp8" if mxf == 8 else "mxfp4", (1, 32)).run()
@@ -101,9 +106,8 @@ def test_grouped_plans_random_sweep(seed):
         torch.cuda.synchronize()
         for i, t in enumerate(ts):
             xh = host(t, dt)
-            if kind in ("tile", "row", "deq"):
-                oc, osc = O.fp8_block_quant(xh, dt, "native" if native else "f32",
-                                            (128, 128) if kind == "tile" else (1, 128), pow2)
+            if kind in ("tile", "row", "deq", "blk"):
+                oc, osc = O.fp8_block_quant(xh, dt, "native" if native else "f32", blk, pow2)
                 assert np.array_equal(u8(outs[i][0]), oc[0]), (case, i)
                 want_s = O.bf16_from_f32(osc[0]) if sbf16 else osc[0]
                 want_s = want_s.view(np.uint32) if want_s.dtype == np.float32 else want_s
