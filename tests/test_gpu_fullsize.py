@@ -121,3 +121,29 @@ def test_c3_all_48_layers_experts():
                 assert np.array_equal(host8(codes), oc), layer
                 assert np.array_equal(got.view(np.uint32), osc.view(np.uint32)), layer
         del gu, dn, plan, outs
+
+
+def test_cast_full_qwen3_8b_state_through_the_loader():
+    """bench.py's cast workload at full size: the whole Qwen3-8B state (399 tensors,
+    8.19 G elements, embeddings and lm_head included) through DynamicWeightLoader's
+    chunked grouped launches (2 M work-groups in all), each tensor bit-equal to
+    torch's own cast of it.  The state is finite, where torch's device cast and
+    its x86 cast agree (every bf16 pattern is checked against the x86 cast in
+    test_gpu_cast.py)."""
+    from lumenrl_amd.engine.inference import DynamicWeightLoader
+
+    class Sink:
+        def update_weights(self, sd):
+            self.sd = sd
+
+    named = B.qwen3_8b_state(torch, DEV, SEED)
+    sd = dict(named)
+    sink = Sink()
+    DynamicWeightLoader.load_weights(sink, sd, fp8_config={"enabled": True})
+    torch.cuda.synchronize()
+    say("cast of the whole state done; comparing", len(sd), "tensors")
+    assert list(sink.sd) == list(sd)
+    for name, w in sd.items():
+        assert torch.isfinite(w).all(), name
+        want = w.to(torch.float8_e4m3fn).view(torch.uint8)
+        assert torch.equal(sink.sd[name].view(torch.uint8), want), name
