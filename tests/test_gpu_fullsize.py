@@ -147,3 +147,24 @@ def test_cast_full_qwen3_8b_state_through_the_loader():
         assert torch.isfinite(w).all(), name
         want = w.to(torch.float8_e4m3fn).view(torch.uint8)
         assert torch.equal(sink.sd[name].view(torch.uint8), want), name
+
+
+@pytest.mark.parametrize("kind,fmt", [("student_t", "mxfp8"), ("rowscale", "mxfp4")])
+def test_mx_full_set_dequantize_then_requantize_is_identity(kind, fmt):
+    """C4 / C5 at full size, size-independent property: MX dequantization is exact
+    (element * 2^(E-127)), and re-quantizing those float32 values gives back the same
+    E8M0 exponents and codes (the group maximum keeps its binade), so
+    quantize -> dequantize -> quantize is the identity on every one of the 252 tensors."""
+    from lumenrl_amd.quantization.ops import DequantPlan
+
+    ws, names = B.qwen3_8b_set(torch, DEV, SEED, kind)
+    q1 = QuantPlan(ws, fmt, (1, 32)).run()
+    torch.cuda.synchronize()
+    del ws
+    back = DequantPlan(q1, (1, 32), torch.float32, fmt=fmt).run()
+    q2 = QuantPlan(back, fmt, (1, 32)).run()
+    torch.cuda.synchronize()
+    say(fmt, "round trip of", len(names), "tensors done; comparing")
+    for name, (c1, s1), (c2, s2) in zip(names, q1, q2):
+        assert torch.equal(c1.view(torch.uint8), c2.view(torch.uint8)), name
+        assert torch.equal(s1, s2), name
