@@ -168,3 +168,23 @@ def test_mx_full_set_dequantize_then_requantize_is_identity(kind, fmt):
     for name, (c1, s1), (c2, s2) in zip(names, q1, q2):
         assert torch.equal(c1.view(torch.uint8), c2.view(torch.uint8)), name
         assert torch.equal(s1, s2), name
+
+
+def test_c2d_full_dequantize_state_dict_layout_matches_torch_ops():
+    """bench.py's c2d workload at full size: the C2 weights quantized to 1x128 blocks
+    with bf16 scales (quantize_state_dict's layout), then dequantized to bf16 in one
+    grouped launch, equal on every tensor to the reference's op sequence
+    (weight_quantizer.py:79-89, :133: fp32(code) * fp32(scale), then bf16) run by
+    torch on the same device (finite data: no NaN payloads involved)."""
+    from lumenrl_amd.quantization.ops import DequantPlan
+
+    ws, names = B.qwen3_8b_set(torch, DEV, SEED, "normal")
+    pairs = QuantPlan(ws, "fp8_block", (1, 128), scale_dtype=torch.bfloat16).run()
+    torch.cuda.synchronize()
+    del ws
+    outs = DequantPlan(pairs, (1, 128), torch.bfloat16).run()
+    torch.cuda.synchronize()
+    say("c2d", len(names), "tensors dequantized; comparing with torch's ops")
+    for name, (c, s), out in zip(names, pairs, outs):
+        want = (c.float() * s.float().repeat_interleave(128, dim=1)).to(torch.bfloat16)
+        assert torch.equal(out.view(torch.int16), want.view(torch.int16)), name
