@@ -188,3 +188,28 @@ def test_c2d_full_dequantize_state_dict_layout_matches_torch_ops():
     for name, (c, s), out in zip(names, pairs, outs):
         want = (c.float() * s.float().repeat_interleave(128, dim=1)).to(torch.bfloat16)
         assert torch.equal(out.view(torch.int16), want.view(torch.int16)), name
+
+
+def test_act_and_kv_full_size_match_torch_ops_on_device():
+    """bench.py's act and kv workloads at full size against the reference's op
+    sequences (fp8_rollout.py:53-72; fp8_kv_cache.py:52-54) run by torch on the same
+    device: the 7 linear inputs of a Qwen3-8B layer for an 8192-token prefill chunk,
+    and the 108 q/k/v_proj weights of the C2 set (finite data)."""
+    from oracle import torch_ref as T
+    from lumenrl_amd.quantization import TensorScalePlan, act_qdq
+
+    g = torch.Generator(device=DEV).manual_seed(SEED)
+    for k in (4096,) * 6 + (12288,):
+        x = torch.empty(B.PREFILL_TOKENS, k, device=DEV, dtype=torch.float32).normal_(0.0, 1.0, generator=g)
+        x[:, ::97] *= 30.0
+        xb = x.to(torch.bfloat16)
+        got = act_qdq(xb, 128)
+        want = T.act_qdq(xb, 128)
+        assert torch.equal(got.view(torch.int32), want.view(torch.int32)), k
+    ws, names = B.qwen3_8b_set(torch, DEV, SEED, "normal")
+    qkv = [w for w, n in zip(ws, names) if n.split(".")[-1] in ("q_proj", "k_proj", "v_proj")]
+    assert len(qkv) == 108
+    scales = TensorScalePlan(qkv).run()
+    want = torch.stack([T.kv_scale(w) for w in qkv])
+    torch.cuda.synchronize()
+    assert torch.equal(scales.view(torch.int32), want.view(torch.int32))
