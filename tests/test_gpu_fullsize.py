@@ -213,3 +213,31 @@ def test_act_and_kv_full_size_match_torch_ops_on_device():
     want = torch.stack([T.kv_scale(w) for w in qkv])
     torch.cuda.synchronize()
     assert torch.equal(scales.view(torch.int32), want.view(torch.int32))
+
+
+def test_bucket_full_qwen3_8b_state_sync():
+    """bench.py's bucket workload at full size: the whole Qwen3-8B state synced into
+    2 GiB transfer buckets.  Every quantized entry (codes and `_scale_inv`) read back
+    through the receiver's views equals a separate grouped launch on the same weight,
+    whose bytes test_c2 pins to the oracle; every pass-through tensor arrives intact."""
+    from lumenrl_amd.quantization import QuantizedBucketWriter
+
+    named = B.qwen3_8b_state(torch, DEV, SEED)
+    src = dict(named)
+    writer = QuantizedBucketWriter(named, bucket_bytes=2 << 30, fmt="fp8_block")
+    quantized = [n for n, _ in named if n.endswith("proj.weight")]
+    ref = dict(zip(quantized, QuantPlan([src[n] for n in quantized], "fp8_block", (128, 128)).run()))
+    seen = set()
+    for bucket in writer:
+        bucket.fill()
+        torch.cuda.synchronize()
+        for name, t in bucket.views():
+            seen.add(name)
+            if name.endswith("_scale_inv"):
+                assert torch.equal(t, ref[name[: -len("_scale_inv")]][1]), name
+            elif name in ref:
+                assert torch.equal(t.view(torch.uint8), ref[name][0].view(torch.uint8)), name
+            else:
+                assert torch.equal(t, src[name]), name
+    assert seen == set(src) | {n + "_scale_inv" for n in quantized}
+    say("bucket sync of", len(src), "tensors in", len(writer), "buckets checked")
