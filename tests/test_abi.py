@@ -128,6 +128,9 @@ def test_group_pack_tiles_qwen3_layer():
     assert L().lrq_group_device_bytes(buf.ctypes.data) == buf.size + 4 * units
     assert L().lrq_group_device_bytes(None) == _lib.ERR_ARG
     assert L().lrq_group_build_map(None, None, None) == _lib.ERR_ARG
+    # a device table off its 256-byte alignment is refused before any launch
+    assert L().lrq_group_build_map(buf.ctypes.data, ctypes.c_void_p(0x1000 + 64), None) == _lib.ERR_ALIGN
+    assert "256-byte" in _lib.last_error()
 
 
 def test_group_pack_rows_and_mx_units():
