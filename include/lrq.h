@@ -9,7 +9,8 @@
  * Conventions
  *   - Every pointer argument named in/codes/scales/out is DEVICE memory the
  *     caller allocated (torch does, in the Python package).  The library never
- *     allocates or frees device memory.
+ *     allocates or frees device memory (its one static device array is part of
+ *     the loaded code object).
  *   - Work is enqueued on `stream` (a hipStream_t; NULL = the null stream) and
  *     is stream-ordered; no entry point synchronizes the device.
  *   - Return 0 on success, LRQ_ERR_* (< 0) for a rejected argument, or a
@@ -18,7 +19,8 @@
  *   - Element counts and strides are in elements of the input dtype.
  *   - Layouts: codes are dense row-major [batch, rows, cols] (e4m3 bytes) or
  *     [rows, cols/2] (e2m1, element 2i in the low nibble of byte i).
- *   - Entry points are re-entrant; the library keeps no device state.
+ *   - Entry points are re-entrant.  The library keeps no device state other
+ *     than the static workspace of lrq_tensor_scale_grouped_static.
  */
 #ifndef LRQ_H_
 #define LRQ_H_
@@ -224,6 +226,28 @@ int64_t lrq_group_units(const void* host_table);
 int64_t lrq_group_workspace_bytes(const void* host_table);
 int lrq_tensor_scale_grouped(const void* host_table, const void* device_table, void* workspace,
                              int64_t workspace_bytes, lrq_stream_t stream);
+
+/*
+ * No counterpart in the reference.  For callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc): lrq_tensor_scale_grouped with the partial-maximum
+ * workspace taken from a library-owned static device array of
+ * LRQ_STATIC_WORKSPACE_BYTES per device instead of a caller buffer.  Same
+ * tables, same results, and no allocation of any kind.
+ *   - A table needing more than LRQ_STATIC_WORKSPACE_BYTES of workspace
+ *     (lrq_group_workspace_bytes(), 4 bytes per 8 KiB of weights: 4 MiB
+ *     covers at least 8 GiB of weights) is rejected with LRQ_ERR_CAPACITY
+ *     before any device work.
+ *   - Every call on one device shares that device's array.  Calls ordered on
+ *     one stream are safe (every partial is written before it is read); calls
+ *     that overlap on one device (different streams, or threads without
+ *     ordering) race and may return wrong scales.
+ *   - The array's address is looked up once per device, on the first call
+ *     that runs there.
+ */
+#define LRQ_STATIC_WORKSPACE_BYTES (4u << 20)
+int lrq_tensor_scale_grouped_static(const void* host_table, const void* device_table,
+                                    lrq_stream_t stream);
 
 /* Library version string ("lrq <semver> gfx950"). */
 const char* lrq_version(void);

@@ -622,6 +622,32 @@ int lrq_tensor_scale_grouped(const void* host_table, const void* device_table, v
                    "kernel launch");
 }
 
+int lrq_tensor_scale_grouped_static(const void* host_table, const void* device_table,
+                                    lrq_stream_t stream) {
+  g_err.clear();
+  if (!host_table || !device_table) return fail(LRQ_ERR_ARG, "null table");
+  GroupHeader h;
+  memcpy(&h, host_table, sizeof(h));
+  if (h.magic != kMagic || h.version != kTableVersion) return fail(LRQ_ERR_TABLE, "not an lrq table");
+  if (h.cfg.kernel != lrq::kKernAmax) return fail(LRQ_ERR_ARG, "not a tensor-scale table");
+  if (h.n == 0) return 0;
+  if (h.units > (int64_t)(LRQ_STATIC_WORKSPACE_BYTES / 4))
+    return fail(LRQ_ERR_CAPACITY, "table needs %lld bytes of workspace, the static workspace holds %lld",
+                (long long)(h.units * 4), (long long)LRQ_STATIC_WORKSPACE_BYTES);
+  if (h.n > kMaxGrid) return fail(LRQ_ERR_ARG, "too many tensors for one launch");
+  int dev = -1;
+  if (int rc = check_hip(stream ? hipStreamGetDevice((hipStream_t)stream, &dev) : hipGetDevice(&dev),
+                         "device of the stream"))
+    return rc;
+  uint32_t* ws = nullptr;
+  if (int rc = check_hip(lrq::static_workspace(dev, &ws), "static workspace address")) return rc;
+  const char* dt = static_cast<const char*>(device_table);
+  const Desc* descs = reinterpret_cast<const Desc*>(dt + h.desc_off);
+  const uint32_t* map = reinterpret_cast<const uint32_t*>(dt + h.map_off);
+  return check_hip(lrq::launch_tensor_scale(h.cfg, descs, map, h.n, h.units, ws, (hipStream_t)stream),
+                   "kernel launch");
+}
+
 int64_t lrq_group_units(const void* host_table) {
   g_err.clear();
   if (!host_table) return fail(LRQ_ERR_ARG, "null table");

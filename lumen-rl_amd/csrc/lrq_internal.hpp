@@ -105,6 +105,10 @@ int64_t amax_unit_elems(int dtype, bool vec);
 hipError_t launch_tensor_scale(const LaunchCfg& cfg, const Desc* descs, const uint32_t* map, int64_t n,
                                int64_t units, uint32_t* partial, hipStream_t stream);
 
+// Device address of the library-owned tensor-scale workspace
+// (LRQ_STATIC_WORKSPACE_BYTES) on device `dev`, looked up once per device.
+hipError_t static_workspace(int dev, uint32_t** out);
+
 // Grouped byte copy over `units` work-groups.
 hipError_t launch_copy(const Desc* descs, const uint32_t* map, int64_t units, hipStream_t stream);
 hipError_t launch_mx_dequant(const LaunchCfg& cfg, const Desc& single, const Desc* descs,

@@ -14,11 +14,49 @@
 // it is read, and the result does not depend on scheduling.
 #include <string.h>
 
+#include <mutex>
+
 #include "lrq.h"
 #include "lrq_device.hpp"
 #include "lrq_internal.hpp"
 
+// The partial-maximum workspace of lrq_tensor_scale_grouped_static, for callers
+// that cannot allocate device memory.  Every device the library runs on holds
+// its own copy for the life of the process.  Host code never passes `scratch`
+// itself to a kernel (on the host it is only a stand-in for the symbol): it
+// looks up the device address once per device (static_workspace) and passes
+// that.
+static __device__ __align__(256) uint32_t scratch[LRQ_STATIC_WORKSPACE_BYTES / 4];
+
 namespace lrq {
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+uint32_t* g_scratch_ptr[kMaxDevices];  // device address of `scratch`, per device
+}  // namespace
+
+hipError_t static_workspace(int dev, uint32_t** out) {
+  if (dev < 0 || dev >= kMaxDevices) return hipErrorInvalidDevice;
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    int cur = -1;
+    hipError_t e = hipGetDevice(&cur);
+    if (e != hipSuccess) return e;
+    if (cur != dev && (e = hipSetDevice(dev)) != hipSuccess) return e;
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));  // with `dev` current
+    if (cur != dev) {
+      const hipError_t r = hipSetDevice(cur);
+      if (e == hipSuccess) e = r;
+    }
+    if (e != hipSuccess) return e;
+    if (p == nullptr) return hipErrorInvalidSymbol;
+    g_scratch_ptr[dev] = static_cast<uint32_t*>(p);
+  }
+  *out = g_scratch_ptr[dev];
+  return hipSuccess;
+}
 
 
 // Elements per unit of the vector kernel (256 lanes x kAmaxLoads x 16 bytes).

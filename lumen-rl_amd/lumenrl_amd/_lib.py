@@ -18,6 +18,7 @@ FLAG_POW2_SCALE, FLAG_NATIVE_ARITH, FLAG_SCALE_BF16, FLAG_OUT_BF16 = 1, 2, 4, 8
 FMT_FP8_BLOCK, FMT_MXFP8, FMT_MXFP4, FMT_FP8_DEQUANT, FMT_TENSOR_SCALE, FMT_COPY = 0, 1, 2, 3, 4, 5
 FMT_CAST_E4M3, FMT_MXFP8_DEQUANT, FMT_MXFP4_DEQUANT = 6, 7, 8
 ERR_ARG, ERR_ALIGN, ERR_CAPACITY, ERR_TABLE = -1, -2, -3, -4
+STATIC_WORKSPACE_BYTES = 4 << 20  # LRQ_STATIC_WORKSPACE_BYTES
 
 
 class LrqError(RuntimeError):
@@ -57,6 +58,7 @@ SIGNATURES = {
     "lrq_group_build_map": (_CI, [_VP, _VP, _VP]),
     "lrq_group_workspace_bytes": (_I64, [_VP]),
     "lrq_tensor_scale_grouped": (_CI, [_VP, _VP, _VP, _I64, _VP]),
+    "lrq_tensor_scale_grouped_static": (_CI, [_VP, _VP, _VP]),
     "lrq_version": (ctypes.c_char_p, []),
     "lrq_last_error": (ctypes.c_char_p, []),
     "lrq_diag_e4m3_bits": (_CI, [ctypes.c_uint32, _I64, _VP, _VP]),

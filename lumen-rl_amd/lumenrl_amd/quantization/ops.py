@@ -385,6 +385,13 @@ class _GroupLaunch:
                                                      _stream(self.device))
         _lib.check(rc, "lrq_tensor_scale_grouped")
 
+    def run_tensor_scale_static(self) -> None:
+        with _on(self.device):
+            self._enter()
+            rc = _lib.lib().lrq_tensor_scale_grouped_static(self.host.data_ptr(), self.dev.data_ptr(),
+                                                            _stream(self.device))
+        _lib.check(rc, "lrq_tensor_scale_grouped_static")
+
 
 class ChunkedLaunches:
     """Grouped launches issued while the caller is still collecting tensors.
@@ -683,6 +690,15 @@ class TensorScalePlan:
     def run(self) -> Tensor:
         """Enqueue both launches on the current stream; returns ``scales``."""
         self._launch.run_tensor_scale(self.workspace)
+        return self.scales
+
+    def run_static(self) -> Tensor:
+        """``run()`` through lrq_tensor_scale_grouped_static: the partial maxima
+        go to the library's per-device static workspace, so the launch itself
+        allocates nothing.  Calls that overlap on one device race on that
+        workspace; calls ordered on one stream do not.  Tables needing more than
+        ``_lib.STATIC_WORKSPACE_BYTES`` of workspace raise ValueError."""
+        self._launch.run_tensor_scale_static()
         return self.scales
 
 

@@ -365,3 +365,23 @@ def test_group_packer_never_crashes_and_is_consistent(fmt_blk, dims, dtype, flag
     units = L().lrq_group_units(buf.ctypes.data)
     assert units >= 0
     assert L().lrq_group_device_bytes(buf.ctypes.data) == need + 4 * units
+
+
+def test_static_workspace_entry_rejects_oversized_table_before_any_hip_call():
+    fake = 1 << 20
+    t = (_lib.LrqTensor * 1)()
+    rows, cols = 1 << 20, 8192  # 2 M partials: more than LRQ_STATIC_WORKSPACE_BYTES holds
+    t[0].in_, t[0].codes, t[0].scales = fake, None, fake
+    t[0].batch, t[0].rows, t[0].cols, t[0].ld, t[0].batch_stride = 1, rows, cols, cols, rows * cols
+    need = L().lrq_group_table_bytes(_lib.FMT_TENSOR_SCALE, t, 1, _lib.DTYPE_BF16, 1, 1, 0)
+    host = (ctypes.c_uint8 * need)()
+    assert L().lrq_group_pack(_lib.FMT_TENSOR_SCALE, t, 1, _lib.DTYPE_BF16, 1, 1, 0, host, need) == 0
+    assert L().lrq_group_workspace_bytes(host) == 4 * (rows * cols // 4096) > _lib.STATIC_WORKSPACE_BYTES
+    rc = L().lrq_tensor_scale_grouped_static(host, ctypes.c_void_p(fake), None)
+    assert rc == _lib.ERR_CAPACITY and "static workspace" in _lib.last_error()
+    # a table of another format is refused the same way
+    t[0].rows, t[0].codes = 128, fake
+    need = L().lrq_group_table_bytes(_lib.FMT_FP8_BLOCK, t, 1, _lib.DTYPE_BF16, 128, 128, 0)
+    host = (ctypes.c_uint8 * need)()
+    assert L().lrq_group_pack(_lib.FMT_FP8_BLOCK, t, 1, _lib.DTYPE_BF16, 128, 128, 0, host, need) == 0
+    assert L().lrq_tensor_scale_grouped_static(host, ctypes.c_void_p(fake), None) == _lib.ERR_ARG
