@@ -37,6 +37,11 @@ typedef struct ihipStream_t* lrq_stream_t; /* == hipStream_t */
 #define LRQ_DTYPE_BF16 0
 #define LRQ_DTYPE_F16 1
 #define LRQ_DTYPE_F32 2
+#define LRQ_DTYPE_F64 3 /* FP8 block quantization only (lrq_fp8_block_quant and LRQ_FMT_FP8_BLOCK
+                           tables), with LRQ_FLAG_NATIVE_ARITH: float64 arithmetic and
+                           float64 scales, as quantize_tensor on a float64 tensor
+                           (weight_quantizer.py:59-71, the quotient rounded to float32 at
+                           :68 before the e4m3 cast) */
 
 /* flags */
 #define LRQ_FLAG_POW2_SCALE 1u   /* FP8Config.use_weight_pow2_scale (fp8_config.py:22) */
@@ -89,9 +94,10 @@ typedef struct ihipStream_t* lrq_stream_t; /* == hipStream_t */
  *   in      : batch matrices [rows, cols]; row r of matrix b at
  *             in + b*batch_stride + r*ld (elements of in_dtype).
  *   codes   : [batch, rows, cols] e4m3fn bytes.
- *   scales  : [batch, ceil(rows/blk_r), ceil(cols/blk_c)]: float32, or 16-bit
- *             words of the input dtype with LRQ_FLAG_NATIVE_ARITH, or bf16 with
- *             LRQ_FLAG_SCALE_BF16.  Edge blocks may be partial.
+ *   scales  : [batch, ceil(rows/blk_r), ceil(cols/blk_c)]: float32, or values of
+ *             the input dtype with LRQ_FLAG_NATIVE_ARITH (16-bit words, or float64
+ *             for LRQ_DTYPE_F64), or bf16 with LRQ_FLAG_SCALE_BF16.  Edge blocks
+ *             may be partial.
  * Bit-exact with the reference evaluated by torch on x86, including NaN, inf,
  * all-zero and subnormal blocks.
  */

@@ -32,7 +32,7 @@ int check_hip(hipError_t e, const char* what) {
   return fail((int)e, "%s: %s", what, hipGetErrorString(e));
 }
 
-int64_t esize(int dt) { return dt == lrq::kF32 ? 4 : 2; }
+int64_t esize(int dt) { return dt == lrq::kF64 ? 8 : dt == lrq::kF32 ? 4 : 2; }
 bool aligned(const void* p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
 bool valid_dtype(int dt) { return dt == lrq::kBF16 || dt == lrq::kF16 || dt == lrq::kF32; }
 bool pow2_block(int64_t b) { return b == 32 || b == 64 || b == 128 || b == 256 || b == 512; }
@@ -110,6 +110,7 @@ bool fold_batch(Desc& d) {
 }
 
 int fp8_kernel_for(const Desc& d, int in_dtype, int64_t blk_r, int64_t blk_c) {
+  if (in_dtype == lrq::kF64) return lrq::kKernF64;
   const int64_t es = esize(in_dtype);
   const bool vec = aligned(d.in, 16) && (d.ld * es) % 16 == 0 &&
                    (d.batch == 1 || (d.bstride * es) % 16 == 0) && aligned(d.codes, 8) &&
@@ -149,6 +150,12 @@ bool plan_units(const LaunchCfg& cfg, Desc& d) {
       d.units_r = (d.rows + cfg.blk_r - 1) / cfg.blk_r;
       d.units_c = (d.cols + cfg.blk_c - 1) / cfg.blk_c;
       d.units = d.batch * d.units_r * d.units_c;
+      return true;
+    case kKernF64:  // one wave per block, four per work-group
+      d.units_r = (d.rows + cfg.blk_r - 1) / cfg.blk_r;
+      d.units_c = (d.cols + cfg.blk_c - 1) / cfg.blk_c;
+      d.nblocks = d.batch * d.units_r * d.units_c;
+      d.units = (d.nblocks + 3) / 4;
       return true;
     case kKernRowQuad: {
       if (!fold_batch(d)) return false;
@@ -195,6 +202,7 @@ hipError_t launch(const LaunchCfg& cfg, const Desc& single, const Desc* descs_de
     return launch_mx(cfg, single, descs_dev, map_dev, total_units, stream);
   if (cfg.kernel == kKernDequant || cfg.kernel == kKernGenericDequant)
     return launch_dequant(cfg, single, descs_dev, map_dev, total_units, stream);
+  if (cfg.kernel == kKernF64) return launch_f64(cfg, single, descs_dev, map_dev, total_units, stream);
   return launch_fp8(cfg, single, descs_dev, map_dev, total_units, stream);
 }
 
@@ -259,7 +267,15 @@ int plan_group(int fmt, const lrq_tensor* ts, int64_t n, int in_dtype, int64_t b
                int64_t blk_c, unsigned flags, LaunchCfg* cfg_out, Desc* ds, int64_t* units_out) {
   if (n < 0 || (n > 0 && !ts)) return fail(LRQ_ERR_ARG, "bad tensor list");
   if (n > 0xFFFFFFFFll) return fail(LRQ_ERR_ARG, "more than 2^32 tensors in one table");  // uint32 map
-  if (!valid_dtype(in_dtype)) return fail(LRQ_ERR_ARG, "bad input dtype %d", in_dtype);
+  if (in_dtype == lrq::kF64) {
+    // float64 input: quantize_tensor on a float64 tensor, float64 arithmetic only
+    if (fmt != LRQ_FMT_FP8_BLOCK)
+      return fail(LRQ_ERR_ARG, "float64 input is accepted by the FP8 block format only");
+    if (!(flags & LRQ_FLAG_NATIVE_ARITH))
+      return fail(LRQ_ERR_ARG, "float64 input is quantized in float64 arithmetic: pass LRQ_FLAG_NATIVE_ARITH");
+  } else if (!valid_dtype(in_dtype)) {
+    return fail(LRQ_ERR_ARG, "bad input dtype %d", in_dtype);
+  }
   LaunchCfg cfg{};
   cfg.in_dtype = in_dtype;
   if (fmt == LRQ_FMT_FP8_BLOCK) {
@@ -365,6 +381,8 @@ int plan_group(int fmt, const lrq_tensor* ts, int64_t n, int in_dtype, int64_t b
     }
     int k;
     if (fmt == LRQ_FMT_FP8_BLOCK) {
+      if (in_dtype == lrq::kF64 && (!aligned(d.in, 8) || (d.scales && !aligned(d.scales, 8))))
+        return fail(LRQ_ERR_ALIGN, "tensor %lld: float64 input and scales must be 8-byte aligned", (long long)i);
       k = fp8_kernel_for(d, in_dtype, blk_r, blk_c);
     } else if (fmt == LRQ_FMT_FP8_DEQUANT) {
       if (d.ld != d.cols || d.bstride != d.rows * d.cols)

@@ -13,7 +13,7 @@
 
 namespace lrq {
 
-enum : int { kBF16 = 0, kF16 = 1, kF32 = 2 };
+enum : int { kBF16 = 0, kF16 = 1, kF32 = 2, kF64 = 3 };
 
 // ---------------------------------------------------------------------------
 // bit helpers

@@ -37,6 +37,7 @@ enum Kernel : int {
   kKernCopy = 8,           // grouped byte copy (bucket pass-through tensors)
   kKernCast = 9,           // grouped unscaled cast to float8_e4m3fn
   kKernMxDequant = 10,     // MXFP8 / MXFP4 dequant, 8 (bf16 out) or 4 (fp32) elements per lane-chunk
+  kKernF64 = 11,           // FP8 blocks of a float64 tensor in float64 arithmetic, one wave per block
 };
 
 // Work per lane of the streaming kernels, shared by the kernels and the
@@ -76,7 +77,7 @@ __device__ __forceinline__ void pick_desc(const Desc& single, const Desc* descs,
 // Launch parameters common to every tensor of one launch.
 struct LaunchCfg {
   int kernel;     // Kernel
-  int in_dtype;   // kBF16 / kF16 / kF32
+  int in_dtype;   // kBF16 / kF16 / kF32 (kF64: FP8 blocks in float64 arithmetic only)
   int arith;      // 0: float32 arithmetic, 1: input dtype's arithmetic
   int pow2;       // pow2 scale rounding
   int blk_r, blk_c;
@@ -98,6 +99,7 @@ hipError_t launch(const LaunchCfg& cfg, const Desc& single, const Desc* descs_de
 hipError_t launch_fp8(const LaunchCfg&, const Desc&, const Desc*, const uint32_t*, int64_t, hipStream_t);
 hipError_t launch_mx(const LaunchCfg&, const Desc&, const Desc*, const uint32_t*, int64_t, hipStream_t);
 hipError_t launch_dequant(const LaunchCfg&, const Desc&, const Desc*, const uint32_t*, int64_t, hipStream_t);
+hipError_t launch_f64(const LaunchCfg&, const Desc&, const Desc*, const uint32_t*, int64_t, hipStream_t);
 
 // Per-tensor scales: k_amax over `units` work-groups writing partial[unit],
 // then one work-group per tensor (n) reducing them into the tensor's scale.

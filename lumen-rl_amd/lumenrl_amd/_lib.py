@@ -13,7 +13,7 @@ import threading
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "liblrq.so")
 
-DTYPE_BF16, DTYPE_F16, DTYPE_F32 = 0, 1, 2
+DTYPE_BF16, DTYPE_F16, DTYPE_F32, DTYPE_F64 = 0, 1, 2, 3
 FLAG_POW2_SCALE, FLAG_NATIVE_ARITH, FLAG_SCALE_BF16, FLAG_OUT_BF16 = 1, 2, 4, 8
 FMT_FP8_BLOCK, FMT_MXFP8, FMT_MXFP4, FMT_FP8_DEQUANT, FMT_TENSOR_SCALE, FMT_COPY = 0, 1, 2, 3, 4, 5
 FMT_CAST_E4M3, FMT_MXFP8_DEQUANT, FMT_MXFP4_DEQUANT = 6, 7, 8

@@ -56,13 +56,14 @@ def _on(device: torch.device):
     return torch.cuda.device(device)
 
 
-def _check_input(x: Tensor, what: str) -> None:
+def _check_input(x: Tensor, what: str, allow_f64: bool = False) -> None:
     if not isinstance(x, Tensor):
         raise TypeError(f"{what}: expected a torch.Tensor, got {type(x)!r}")
     if not x.is_cuda:
         raise ValueError(f"{what}: expected a HIP device tensor, got device {x.device}")
-    if x.dtype not in _IN_DTYPES:
-        raise TypeError(f"{what}: unsupported input dtype {x.dtype} (bf16, fp16, fp32)")
+    if x.dtype not in _IN_DTYPES and not (allow_f64 and x.dtype == torch.float64):
+        raise TypeError(f"{what}: unsupported input dtype {x.dtype} (bf16, fp16, fp32"
+                        f"{', fp64' if allow_f64 else ''})")
 
 
 def matrix_view(x: Tensor) -> tuple[Tensor, int, int, int, int, int]:
@@ -99,12 +100,17 @@ def fp8_block_quant(x: Tensor, block: tuple[int, int], *, native_arith: bool = F
     """Blockwise e4m3 of ``x`` [..., rows, cols]; scales [..., ceil(rows/br), ceil(cols/bc)].
 
     ``native_arith`` evaluates the reference's arithmetic in x's own dtype
-    (quantize_tensor called on a bf16/fp16 tensor); otherwise float32
+    (quantize_tensor called on a bf16/fp16/fp64 tensor); otherwise float32
     (quantize_state_dict's upcast, weight_quantizer.py:109).  ``scale_dtype``
     torch.bfloat16 rounds float32 scales to bf16 in the kernel (the
-    ``_fp8_scales`` sidecar, :111).
+    ``_fp8_scales`` sidecar, :111).  float64 input takes float64 arithmetic
+    only (scales float64; the quotient rounded to float32 before the e4m3
+    cast, :68-71).
     """
-    _check_input(x, "fp8_block_quant")
+    _check_input(x, "fp8_block_quant", allow_f64=True)
+    if x.dtype == torch.float64 and not native_arith:
+        raise ValueError("fp8_block_quant: float64 input is quantized in float64 arithmetic "
+                         "(native_arith=True); cast it to float32 for float32 arithmetic")
     if x.dim() < 1:
         raise ValueError("fp8_block_quant expects a tensor with at least one dimension")
     br, bc = int(block[0]), int(block[1])
@@ -133,8 +139,8 @@ def fp8_block_quant(x: Tensor, block: tuple[int, int], *, native_arith: bool = F
         return codes.reshape(x.shape), scales
     with _on(x.device):
         rc = _lib.lib().lrq_fp8_block_quant(
-            xm.data_ptr(), _IN_DTYPES[x.dtype], batch, rows, cols, ld, bstride, br, bc,
-            codes.data_ptr(), scales.data_ptr(), flags, _stream(x.device))
+            xm.data_ptr(), _IN_DTYPES.get(x.dtype, _lib.DTYPE_F64), batch, rows, cols, ld, bstride,
+            br, bc, codes.data_ptr(), scales.data_ptr(), flags, _stream(x.device))
     _lib.check(rc, "lrq_fp8_block_quant")
     return codes.reshape(x.shape), scales
 

@@ -15,12 +15,12 @@ x86 CPU:
   go through a few grouped kernel launches (8, 16, 32, then 64 tensors each),
   each issued as soon as it is planned, so the device works while the host
   plans the rest.
+* ``quantize_tensor`` on a float64 tensor computes in float64 (float64 scales)
+  and rounds each quotient to float32 before the e4m3 cast, as :59-71 do.
 
 Tensors on the CPU are staged through the current HIP device and the results
 copied back, so the reference's CPU-tensor call sites keep working; there is no
-CPU compute path.  float64 tensors are accepted where the reference upcasts
-them (quantize_state_dict); ``quantize_tensor`` on float64 (float64 arithmetic
-in the reference) raises TypeError.
+CPU compute path.
 """
 
 from __future__ import annotations
@@ -68,16 +68,13 @@ class WeightQuantizer:
 
         Returns ``(quantized, scales)``: ``quantized`` is float8_e4m3fn with the
         input shape, ``scales`` has shape ``tensor.shape[:-1] + (last // block_size,)``
-        and the compute dtype (float32 for float32 input, else the input dtype).
+        and the compute dtype, which is the input dtype (bf16, fp16, fp32 or fp64).
         """
         if tensor.dim() < 1:
             raise ValueError("quantize_tensor expects tensor.dim() >= 1")
         last = tensor.shape[-1]
         if last % block_size != 0:
             raise ValueError(f"Last dim {last} must be divisible by block_size={block_size}")
-        if tensor.dtype == torch.float64:
-            raise TypeError("lumenrl_amd quantize_tensor computes in bf16/fp16/fp32; "
-                            "cast float64 tensors to float32 first")
         x, home = _stage(tensor)
         leading = 1
         for d in tensor.shape[:-1]:

@@ -13,6 +13,8 @@
  *                          optional pow2 -> x/s -> float8_e4m3fn), applied to
  *                          1xB row blocks (the reference) or to 2-D tiles
  *                          (128x128, same op order).
+ *   lrqo_fp8_block_quant_f64  the same on a float64 tensor, every op in
+ *                          float64 (:59-71), then the float32 step of :68.
  *   lrqo_pow2_*            _round_scale_pow2, weight_quantizer.py:24-27.
  *   lrqo_fp8_block_dequant WeightQuantizer.dequantize_tensor, :79-89, and the
  *                          bf16 cast of dequantize_state_dict, :133.
@@ -317,6 +319,78 @@ int lrqo_fp8_block_quant(const void* in, int in_dtype, int arith, int64_t batch,
       }
   }
   return 0;
+}
+
+/* ------------------------------------------------------------------ */
+/* float64 arithmetic: quantize_tensor on a float64 tensor             */
+/* ------------------------------------------------------------------ */
+/* weight_quantizer.py:59-71 evaluated in float64, the dtype of the tensor:
+ * amax (a NaN anywhere gives the canonical 0x7FF8000000000000), amax / 448.0,
+ * clamp(min=finfo(float64).tiny = 2^-1022), optional pow2, x / s in float64,
+ * then the explicit .to(float32) of :68 (round to nearest even: a double
+ * rounding, f64 quotient -> f32 -> e4m3) and .to(float8_e4m3fn) of :71.
+ * torch's x86 NaN choices are the float32 ones (observed with torch 2.10):
+ * a division with a NaN operand returns that operand quieted (x's own
+ * first), inf/inf is the default NaN 0xFFF8000000000000 (negative), a float64
+ * NaN converts to a float32 NaN of the same sign, and torch.pow(2, NaN)
+ * returns all-ones bits in the vectorized loop body (pinned here). */
+static inline uint64_t d2u(double d) { uint64_t u; memcpy(&u, &d, 8); return u; }
+static inline double u2d(uint64_t u) { double d; memcpy(&d, &u, 8); return d; }
+
+double lrqo_x86_div_f64(double a, double b) {
+  if (isnan(a)) return u2d(d2u(a) | 0x0008000000000000ull);
+  if (isnan(b)) return u2d(d2u(b) | 0x0008000000000000ull);
+  if ((isinf(a) && isinf(b)) || (a == 0.0 && b == 0.0)) return u2d(0xFFF8000000000000ull);
+  return a / b;
+}
+
+/* _round_scale_pow2 (weight_quantizer.py:24-27) on a float64 scale >= 2^-1022:
+ * 2^roundeven(log2 s).  The double log2 here gives the same rounding cut as
+ * torch's float64 log2 on every exponent (checked against torch in tests/). */
+double lrqo_pow2_f64(double s) {
+  if (isnan(s) || isinf(s)) return s;
+  double r = nearbyint(log2(s));
+  return ldexp(1.0, (int)r); /* 2^1024 overflows to inf, as torch.pow does */
+}
+
+int lrqo_fp8_block_quant_f64(const double* in, int64_t batch, int64_t rows, int64_t cols,
+                             int64_t ld, int64_t bstride, int64_t blk_r, int64_t blk_c,
+                             int pow2, uint8_t* codes, double* scales, int nthreads) {
+  if (blk_r < 1 || blk_c < 1 || batch < 0 || rows < 0 || cols < 0) return 1;
+  int64_t tr = (rows + blk_r - 1) / blk_r, tc = (cols + blk_c - 1) / blk_c;
+  int64_t ntiles = batch * tr * tc;
+#ifdef _OPENMP
+  if (nthreads > 0) omp_set_num_threads(nthreads);
+#pragma omp parallel for schedule(dynamic, 16)
+#endif
+  for (int64_t t = 0; t < ntiles; ++t) {
+    int64_t b = t / (tr * tc), rem = t % (tr * tc);
+    int64_t r0 = (rem / tc) * blk_r, c0 = (rem % tc) * blk_c;
+    int64_t r1 = r0 + blk_r < rows ? r0 + blk_r : rows;
+    int64_t c1 = c0 + blk_c < cols ? c0 + blk_c : cols;
+    uint64_t amax_bits = 0;
+    for (int64_t r = r0; r < r1; ++r)
+      for (int64_t c = c0; c < c1; ++c) {
+        uint64_t a = d2u(in[b * bstride + r * ld + c]) & 0x7FFFFFFFFFFFFFFFull;
+        if (a > amax_bits) amax_bits = a;
+      }
+    double amax = amax_bits > 0x7FF0000000000000ull ? u2d(0x7FF8000000000000ull) : u2d(amax_bits);
+    double s = lrqo_x86_div_f64(amax, 448.0);
+    if (!isnan(s) && s < DBL_MIN) s = DBL_MIN;
+    if (pow2) s = isnan(s) ? u2d(0xFFFFFFFFFFFFFFFFull) : lrqo_pow2_f64(s);
+    scales[t] = s;
+    for (int64_t r = r0; r < r1; ++r)
+      for (int64_t c = c0; c < c1; ++c) {
+        double x = in[b * bstride + r * ld + c];
+        float q = (float)lrqo_x86_div_f64(x, s); /* RNE; a NaN keeps its sign */
+        codes[(b * rows + r) * cols + c] = lrqo_f32_to_e4m3(q);
+      }
+  }
+  return 0;
+}
+
+void lrqo_pow2_f64_n(const double* in, double* out, int64_t n) {
+  for (int64_t i = 0; i < n; ++i) out[i] = lrqo_pow2_f64(in[i]);
 }
 
 /* dequantize_tensor (:79-89): fp32(code) * fp32(scale) per block; optional

@@ -45,6 +45,8 @@ def lib() -> ctypes.CDLL:
         L.lrqo_f32_to_bf16_n.argtypes = [vp, vp, i64]
         L.lrqo_f32_to_f16_n.argtypes = [vp, vp, i64]
         L.lrqo_pow2_f32_n.argtypes = [vp, vp, i64]
+        L.lrqo_pow2_f64_n.argtypes = [vp, vp, i64]
+        L.lrqo_fp8_block_quant_f64.argtypes = [vp, i64, i64, i64, i64, i64, i64, i64, ci, vp, vp, ci]
         L.lrqo_f32_to_e4m3_bits_range.argtypes = [ctypes.c_uint32, i64, vp]
         L.lrqo_pow2_bf16.argtypes = [ctypes.c_uint16]
         L.lrqo_pow2_bf16.restype = ctypes.c_uint16
@@ -81,6 +83,8 @@ def fp8_block_quant(x: np.ndarray, dtype: str = "bf16", arith: str = "f32",
     Returns (codes uint8 [batch, rows, cols], scales [batch, ceil(rows/br), ceil(cols/bc)])
     with scales float32 for float32 arithmetic, else the 16-bit bit patterns.
     """
+    if dtype == "f64":
+        return _fp8_block_quant_f64(x, arith, block, pow2, nthreads)
     x = _as_input(x, dtype)
     if x.ndim == 2:
         x = x[None]
@@ -96,6 +100,33 @@ def fp8_block_quant(x: np.ndarray, dtype: str = "bf16", arith: str = "f32",
     if rc:
         raise ValueError("oracle rejected the arguments")
     return codes, scales
+
+
+def _fp8_block_quant_f64(x, arith, block, pow2, nthreads):
+    """float64 input: the reference computes in float64 (quantize_tensor on a
+    float64 tensor); scales come back float64."""
+    if arith != "native":
+        raise ValueError("float64 input is quantized in float64 arithmetic (arith='native')")
+    x = np.ascontiguousarray(x, dtype=np.float64)
+    if x.ndim == 2:
+        x = x[None]
+    batch, rows, cols = x.shape
+    br, bc = block
+    tr, tc = -(-rows // br), -(-cols // bc)
+    codes = np.zeros((batch, rows, cols), np.uint8)
+    scales = np.zeros((batch, tr, tc), np.float64)
+    rc = lib().lrqo_fp8_block_quant_f64(_ptr(x), batch, rows, cols, cols, rows * cols, br, bc,
+                                        int(pow2), _ptr(codes), _ptr(scales), nthreads)
+    if rc:
+        raise ValueError("oracle rejected the arguments")
+    return codes, scales
+
+
+def pow2_f64(x: np.ndarray) -> np.ndarray:
+    x = np.ascontiguousarray(x, dtype=np.float64)
+    out = np.empty_like(x)
+    lib().lrqo_pow2_f64_n(_ptr(x), _ptr(out), x.size)
+    return out
 
 
 def fp8_block_dequant(codes: np.ndarray, scales: np.ndarray, scale_dtype: str,

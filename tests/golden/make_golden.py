@@ -7,7 +7,8 @@ by the independent numpy restatement of OCP MX v1.0 below (float64 exact
 scaling, torch's float8_e4m3fn cast for E4M3, nearest-even grid search for
 E2M1) -- not by the C oracle, which the tests check against these files.
 
-    python tests/golden/make_golden.py
+    python tests/golden/make_golden.py        (all fixtures)
+    python tests/golden/make_golden.py f64    (the float64 ones only)
 """
 
 from __future__ import annotations
@@ -66,7 +67,7 @@ def fp8_row_case(name, x_bf16_or_f, dtype_name, native, pow2, rows_edge=True):
     tin = t if native else t.float()
     q, s = torch_ref.quantize_tensor(tin, 128, pow2)
     rec = {"codes": q.view(torch.uint8).numpy(), "block": np.array([1, 128])}
-    if dtype_name == "f32":
+    if dtype_name in ("f32", "f64"):
         rec["x"] = t.numpy()
     elif dtype_name == "f16":
         rec["x"] = t.view(torch.int16).numpy().view(np.uint16)
@@ -75,6 +76,8 @@ def fp8_row_case(name, x_bf16_or_f, dtype_name, native, pow2, rows_edge=True):
     if s.dtype == torch.float32:
         rec["scales"] = s.numpy()
         rec["scales_bf16"] = bits16(s.to(torch.bfloat16))
+    elif s.dtype == torch.float64:
+        rec["scales"] = s.numpy()
     else:
         rec["scales"] = s.view(torch.int16).numpy().view(np.uint16)
     rec["meta"] = np.array([dtype_name, "native" if native else "f32", int(pow2)], dtype="U8")
@@ -86,6 +89,51 @@ def fp8_tile_case(name, t, pow2=False):
     np.savez_compressed(os.path.join(OUT, name), x=bits16(t), codes=q.view(torch.uint8).numpy(),
                         scales=s.numpy(), block=np.array([128, 128]),
                         meta=np.array(["bf16", "f32", int(pow2)], dtype="U8"))
+
+
+def f64_edges(rng: np.random.Generator, rows: int = 24, cols: int = 384) -> np.ndarray:
+    """float64 weights with edge 1x128 blocks in the first rows."""
+    x = rng.normal(0.0, 0.02, (rows, cols))
+    idx = rng.choice(x.size, 10, replace=False)
+    x.flat[idx] = rng.choice([-1.0, 1.0], 10) * rng.uniform(0.5, 4.0, 10)
+    x[0, :128] = 0.0
+    x[0, 5] = -0.0
+    x[1, 3], x[1, 4], x[1, 5] = np.inf, -np.inf, -0.0
+    x[2, 7] = np.nan
+    x[2, 128 + 9] = -np.nan
+    x[3, :128] = 5e-324                       # float64 subnormals
+    x[3, 1], x[3, 2] = -1e-310, 2.2e-308
+    x[4, :128] = rng.normal(0.0, 1e-300, 128)
+    x[5, 9], x[5, 10] = 1.7e308, -1.7e308
+    x[6, 130], x[6, 131] = np.nan, -np.inf
+    # s == 1 exactly (amax 448): 1.0625 +- 2^-40 round to the float32 1.0625, an
+    # e4m3 tie that goes to even (1.0); a single rounding would give 1.125
+    x[7, :128] = 1.0625 + 2.0 ** -40
+    x[7, 0], x[7, 1], x[7, 2] = 448.0, 1.0625 - 2.0 ** -40, -(1.1875 + 2.0 ** -35)
+    x[8, :128] = rng.normal(0.0, 1.0, 128) * 2.0 ** -1030   # scale clamps to 2^-1022
+    x[9, :128] = rng.normal(0.0, 1.0, 128) * 1e-320
+    return x
+
+
+def write_f64_fixtures() -> None:
+    """quantize_tensor on float64 tensors: float64 arithmetic and scales."""
+    rng = np.random.default_rng(20261202)
+    x = f64_edges(rng)
+    fp8_row_case("fp8_row_f64.npz", torch.from_numpy(x), "f64", native=True, pow2=False)
+    # pow2: the NaN scale of a pow2 block depends on torch's loop position, so no
+    # NaN here (tests/test_oracle.py pins that rule on a large tensor)
+    xp = x.copy()
+    xp[2, 7], xp[2, 128 + 9], xp[6, 130] = 0.3, -0.2, 0.1
+    fp8_row_case("fp8_row_f64_pow2.npz", torch.from_numpy(xp), "f64", native=True, pow2=True)
+    xt = rng.normal(0.0, 0.02, (256, 320))
+    xt[0:128, 0:128] = 0.0
+    xt[0:128, 128:256][5, 7] = np.inf
+    xt[128:256, 0:128][9, 1] = np.nan
+    xt[128:256, 128:256] = rng.normal(0.0, 1.0, (128, 128)) * 1e-310
+    q, s = torch_ref.quantize_tensor_tiles(torch.from_numpy(xt), (128, 128), False)
+    np.savez_compressed(os.path.join(OUT, "fp8_tile_f64.npz"), x=xt, codes=q.view(torch.uint8).numpy(),
+                        scales=s.numpy(), block=np.array([128, 128]),
+                        meta=np.array(["f64", "native", 0], dtype="U8"))
 
 
 # ---------------------------------------------------------------- MX (numpy)
@@ -215,8 +263,12 @@ def main() -> None:
     for fmt, name in ((8, "mxfp8_f32.npz"), (4, "mxfp4_f32.npz")):
         c, s = mx_reference(xm32, fmt)
         np.savez_compressed(os.path.join(OUT, name), x=xm32, codes=c, scales=s)
+    write_f64_fixtures()
     print("wrote", sorted(f for f in os.listdir(OUT) if f.endswith(".npz")))
 
 
 if __name__ == "__main__":
-    main()
+    if sys.argv[1:] == ["f64"]:
+        write_f64_fixtures()
+    else:
+        main()

@@ -385,3 +385,25 @@ def test_static_workspace_entry_rejects_oversized_table_before_any_hip_call():
     host = (ctypes.c_uint8 * need)()
     assert L().lrq_group_pack(_lib.FMT_FP8_BLOCK, t, 1, _lib.DTYPE_BF16, 128, 128, 0, host, need) == 0
     assert L().lrq_tensor_scale_grouped_static(host, ctypes.c_void_p(fake), None) == _lib.ERR_ARG
+
+
+def test_float64_input_needs_float64_arithmetic_and_the_fp8_block_format():
+    fake = ctypes.c_void_p(0x10000)
+    rc = L().lrq_fp8_block_quant(fake, _lib.DTYPE_F64, 1, 4, 128, 128, 512, 1, 128, fake, fake, 0, None)
+    assert rc == _lib.ERR_ARG and "LRQ_FLAG_NATIVE_ARITH" in _lib.last_error()
+    rc = L().lrq_mxfp8_quant(fake, _lib.DTYPE_F64, 4, 64, 64, fake, fake, None)
+    assert rc == _lib.ERR_ARG
+    # misaligned float64 input
+    odd = ctypes.c_void_p(0x10004)
+    rc = L().lrq_fp8_block_quant(odd, _lib.DTYPE_F64, 1, 4, 128, 128, 512, 1, 128, fake, fake,
+                                 _lib.FLAG_NATIVE_ARITH, None)
+    assert rc == _lib.ERR_ALIGN
+    # a table packs (host memory only) with the float64 kernel's one-wave-per-block geometry
+    t = (_lib.LrqTensor * 1)()
+    t[0].in_, t[0].codes, t[0].scales = 0x10000, 0x20000, 0x30000
+    t[0].batch, t[0].rows, t[0].cols, t[0].ld, t[0].batch_stride = 1, 5, 256, 256, 1280
+    need = L().lrq_group_table_bytes(_lib.FMT_FP8_BLOCK, t, 1, _lib.DTYPE_F64, 1, 128, _lib.FLAG_NATIVE_ARITH)
+    host = (ctypes.c_uint8 * need)()
+    assert L().lrq_group_pack(_lib.FMT_FP8_BLOCK, t, 1, _lib.DTYPE_F64, 1, 128, _lib.FLAG_NATIVE_ARITH,
+                              host, need) == 0
+    assert L().lrq_group_units(host) == (5 * 2 + 3) // 4

@@ -1,0 +1,141 @@
+"""quantize_tensor on float64 tensors, on an MI355X: the float64 kernel against
+the CPU oracle and the reference's torch op sequence, bit for bit.
+
+The reference evaluates every op of weight_quantizer.py:59-71 in float64 for a
+float64 tensor (float64 scales) and rounds each quotient to float32 before the
+e4m3 cast.  Cases: random and edge blocks (zero, +-inf, NaN, float64
+subnormals, huge values, scales clamped to 2^-1022, float32 ties after the
+float64 division), 1xB and 2-D blocks, strided and batched views, pow2 scales,
+the drop-in WeightQuantizer on device and host tensors, and one 4096 x 4096
+float64 weight in full.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle as O
+from oracle import torch_ref as T
+from lumenrl_amd.quantization import FP8Config, WeightQuantizer, ops
+
+pytestmark = pytest.mark.gpu
+
+if not torch.cuda.is_available():  # pragma: no cover - CPU container
+    pytest.skip("needs a HIP device", allow_module_level=True)
+
+DEV = torch.device("cuda", 0)
+RNG = np.random.default_rng(6464)
+
+
+def say(*a):
+    print(*a, flush=True)
+
+
+def edge64(rows=16, cols=384):
+    x = RNG.normal(0, 0.02, (rows, cols))
+    x[0, :128] = 0
+    x[0, 5] = -0.0
+    x[1, 3], x[1, 4], x[1, 5] = np.inf, -np.inf, -0.0
+    x[2, 7] = np.nan
+    x[2, 200] = -np.nan
+    x[3, :128] = 5e-324
+    x[3, 1], x[3, 2] = -1e-310, 2.2e-308
+    x[4, :128] = RNG.normal(0, 1e-300, 128)
+    x[5, 9], x[5, 10] = 1.7e308, -1.7e308
+    x[6, 130], x[6, 131] = np.nan, -np.inf
+    x[7, :128] = 1.0625 + 2.0 ** -40
+    x[7, 0], x[7, 1] = 448.0, 1.0625 - 2.0 ** -40
+    x[8, :128] = -np.nan
+    x[9, :128] = RNG.normal(0, 1, 128) * 1e-320
+    x[10, 128:256] = RNG.normal(0, 1, 128) * 2.0 ** -1030
+    x[11, 256:384] = RNG.uniform(-1, 1, 128) * 448.0 * 2.0 ** 900
+    return x
+
+
+def check(xd: torch.Tensor, blk, pow2):
+    c, s = ops.fp8_block_quant(xd, blk, native_arith=True, pow2=pow2)
+    torch.cuda.synchronize()
+    assert s.dtype == torch.float64
+    xh = xd.cpu().numpy()
+    x3 = xh.reshape((-1,) + xh.shape[-2:])
+    oc, osc = O.fp8_block_quant(x3, "f64", "native", blk, pow2)
+    assert np.array_equal(c.view(torch.uint8).cpu().numpy().reshape(oc.shape), oc)
+    assert np.array_equal(s.cpu().numpy().view(np.uint64).reshape(-1), osc.view(np.uint64).reshape(-1))
+
+
+@pytest.mark.parametrize("pow2", [False, True])
+@pytest.mark.parametrize("blk", [(1, 128), (1, 32), (1, 96), (1, 384), (128, 128), (3, 40), (64, 96)])
+@pytest.mark.parametrize("data", ["weights", "edge"])
+def test_f64_blocks_vs_oracle(data, blk, pow2):
+    say("f64", data, blk, pow2)
+    if data == "weights":
+        x = RNG.normal(0, 0.02, (200, 384))
+        x.flat[RNG.integers(0, x.size, 80)] *= 150
+    else:
+        x = edge64()
+    check(torch.from_numpy(x).to(DEV), blk, pow2)
+
+
+@pytest.mark.parametrize("pow2", [False, True])
+def test_f64_views_and_batches(pow2):
+    base = torch.from_numpy(edge64(48, 640)).to(DEV)
+    check(base[:, 64:448], (1, 128), pow2)          # row stride 640, offset view
+    check(base[::3, :512], (1, 128), pow2)          # row stride 1920
+    check(base[:40].reshape(5, 8, 640), (1, 64), pow2)  # batched matrices
+    check(base.reshape(3, 16, 640)[:, :, :384], (8, 128), pow2)  # strided batch, 2-D blocks
+    e = torch.empty(0, 128, dtype=torch.float64, device=DEV)
+    c, s = ops.fp8_block_quant(e, (1, 128), native_arith=True)
+    assert c.shape == (0, 128) and s.shape == (0, 1) and s.dtype == torch.float64
+
+
+def test_f64_needs_float64_arithmetic():
+    x = torch.zeros(4, 128, dtype=torch.float64, device=DEV)
+    with pytest.raises(ValueError, match="float64 arithmetic"):
+        ops.fp8_block_quant(x, (1, 128))
+    with pytest.raises(TypeError):
+        ops.quantize_mxfp8(x)
+
+
+@pytest.mark.parametrize("pow2", [False, True])
+def test_dropin_quantize_tensor_f64_vs_reference_ops(pow2):
+    """WeightQuantizer.quantize_tensor on float64, device and host tensors, against
+    the reference's torch ops on the CPU (non-NaN data: no loop-position rule)."""
+    wq = WeightQuantizer(FP8Config(use_weight_pow2_scale=pow2))
+    x = RNG.normal(0, 0.02, (6, 64, 512))
+    x[0, 0, :128] = 0.0
+    x[1, 3, 7] = np.inf
+    x[2, 5, 128:256] = 1e-310
+    x[3, 9, :128] = 1.0625 + 2.0 ** -40
+    x[3, 9, 0] = 448.0
+    t = torch.from_numpy(x)
+    want_q, want_s = T.quantize_tensor(t, 128, pow2)
+    for src in (t, t.to(DEV)):
+        q, s = wq.quantize_tensor(src, 128)
+        assert q.device == src.device and s.device == src.device
+        assert q.dtype == torch.float8_e4m3fn and s.dtype == torch.float64
+        assert tuple(s.shape) == (6, 64, 4)
+        assert torch.equal(q.cpu().view(torch.uint8), want_q.view(torch.uint8))
+        assert np.array_equal(s.cpu().numpy().view(np.uint64), want_s.numpy().view(np.uint64))
+    if pow2:
+        # a pow2 scale rounded down lets |x/s| reach 448*sqrt(2), which the
+        # non-saturating e4m3fn cast turns into NaN in the reference too
+        return
+    # the reference's own unit contract (test_weight_quantizer.py:9-16), in float64
+    w = torch.randn(64, 256, dtype=torch.float64, device=DEV)
+    q, s = wq.quantize_tensor(w, 128)
+    err = (wq.dequantize_tensor(q, s, 128).double() - w).abs().max().item()
+    assert err < 0.25
+
+
+def test_f64_full_4096x4096_vs_oracle():
+    say("f64 4096x4096")
+    x = RNG.normal(0, 0.02, (4096, 4096))
+    x.flat[RNG.choice(x.size, x.size // 1000, replace=False)] = RNG.uniform(0.5, 4.0, x.size // 1000)
+    xd = torch.from_numpy(x).to(DEV)
+    c, s = ops.fp8_block_quant(xd, (1, 128), native_arith=True)
+    torch.cuda.synchronize()
+    oc, osc = O.fp8_block_quant(x, "f64", "native", (1, 128), False, nthreads=16)
+    assert np.array_equal(s.cpu().numpy().view(np.uint64).reshape(-1), osc.view(np.uint64).reshape(-1))
+    assert np.array_equal(c.view(torch.uint8).cpu().numpy(), oc[0])

@@ -43,6 +43,8 @@ def host_bits(t: torch.Tensor) -> np.ndarray:
 def dev_from_bits(x: np.ndarray, dt: str) -> torch.Tensor:
     if dt == "f32":
         return torch.from_numpy(np.ascontiguousarray(x, np.float32)).to(DEV)
+    if dt == "f64":
+        return torch.from_numpy(np.ascontiguousarray(x, np.float64)).to(DEV)
     t = torch.from_numpy(np.ascontiguousarray(x, np.uint16).view(np.int16))
     return t.view(DT[dt]).to(DEV)
 
@@ -55,6 +57,8 @@ def scale_bits(t: torch.Tensor) -> np.ndarray:
     t = t.detach().cpu().contiguous()
     if t.dtype == torch.float32:
         return t.numpy().view(np.uint32)
+    if t.dtype == torch.float64:
+        return t.numpy().view(np.uint64)
     if t.dtype in (torch.bfloat16, torch.float16):
         return t.view(torch.int16).numpy().view(np.uint16)
     return t.numpy()
@@ -202,7 +206,8 @@ def test_fp8_golden_on_device(name):
     assert np.array_equal(u8(c).reshape(g["codes"].shape), g["codes"])
     want = g["scales"]
     got = scale_bits(s).reshape(want.shape)
-    assert np.array_equal(got, want.view(np.uint32) if want.dtype == np.float32 else want)
+    wbits = {np.dtype(np.float32): np.uint32, np.dtype(np.float64): np.uint64}.get(want.dtype)
+    assert np.array_equal(got, want.view(wbits) if wbits else want)
     if "scales_bf16" in g:
         c2, s2 = ops.fp8_block_quant(xd, blk, pow2=pow2, scale_dtype=torch.bfloat16)
         torch.cuda.synchronize()
