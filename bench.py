@@ -277,8 +277,7 @@ class _BucketFill:
 
     def __init__(self, bucket):
         self.bucket = bucket
-        q = bucket.plan.algorithmic_bytes if bucket.plan is not None else 0
-        self.algorithmic_bytes = q + 2 * sum(e.nbytes for e in bucket.copies)
+        self.algorithmic_bytes = bucket.algorithmic_bytes
 
     def run(self):
         self.bucket.fill()

@@ -12,7 +12,7 @@ The rollout engine then re-quantizes the bf16 weights to FP8 itself
 (vllm_fp8_utils.py:111-118).
 
 `QuantizedBucketWriter` moves that quantization to the sender.  Each planned bucket is ONE
-kernel launch that reads the bf16 weights and writes e4m3 codes and
+kernel launch per input dtype that reads the weights and writes e4m3 codes and
 `<name>_scale_inv` scales directly at their offsets in the bucket (no
 intermediate tensors, no copy).  Tensors that are not quantized (norms,
 embeddings, lm_head, anything the predicate rejects) are copied in as-is, as
@@ -51,30 +51,58 @@ class _Entry:
 
 
 class Bucket:
-    """One planned bucket: a grouped quantize launch plus the pass-through copies,
-    which (16-byte-aligned sources, the torch norm) go in one grouped copy launch."""
+    """One planned bucket: grouped quantize launches (one per input dtype: a
+    bucket may hold bf16 weights next to an fp32 router gate) plus the
+    pass-through copies, which (16-byte-aligned sources, the torch norm) go in
+    one grouped copy launch.
 
-    def __init__(self, buffer: Tensor, entries: list[_Entry], plan: Optional[ops.QuantPlan],
-                 copies: list[_Entry]) -> None:
+    Sources are looked up in the writer's name -> tensor map at every
+    ``fill()``: a weight re-bound by ``QuantizedBucketWriter.rebind`` or moved to
+    other storage (``param.data = new``) is re-planned before its launch."""
+
+    def __init__(self, buffer: Tensor, entries: list[_Entry],
+                 quant: list[tuple[str, Tensor, Tensor]], copies: list[_Entry], src: dict,
+                 fmt: str, block_size: tuple[int, int]) -> None:
         self.buffer = buffer
         self.entries = entries
-        self.plan = plan
         self.copies = copies
+        self._src = src
         self.nbytes = max((e.offset + e.nbytes for e in entries), default=0)
+        by_dtype: dict[torch.dtype, list[tuple[str, Tensor, Tensor]]] = {}
+        for name, codes, scales in quant:
+            by_dtype.setdefault(src[name].dtype, []).append((name, codes, scales))
+        self.plans: list[tuple[list[str], ops.QuantPlan]] = [
+            ([n for n, _, _ in items],
+             ops.QuantPlan([src[n] for n, _, _ in items], fmt, block_size,
+                           outputs=[(c, sc) for _, c, sc in items]))
+            for items in by_dtype.values()]
+        self._plan_copies()
+
+    def _plan_copies(self) -> None:
         pairs, self._loose = [], []
-        for e in copies:
-            dst = buffer[e.offset:e.offset + e.nbytes]
-            src = e.src.reshape(-1).view(torch.uint8)
+        for e in self.copies:
+            dst = self.buffer[e.offset:e.offset + e.nbytes]
+            src = self._src[e.name].reshape(-1).view(torch.uint8)
             if e.nbytes and src.data_ptr() % 16 == 0 and dst.data_ptr() % 16 == 0:
                 pairs.append((dst, src))
             elif e.nbytes:
                 self._loose.append((dst, src))
+        self._copy_ptrs = [self._src[e.name].data_ptr() for e in self.copies]
         self.copy_plan = ops.CopyPlan(pairs) if pairs else None
 
+    @property
+    def algorithmic_bytes(self) -> int:
+        """Bytes one fill() reads and writes: quantized inputs, codes and scales,
+        and twice each pass-through tensor."""
+        q = sum(plan.algorithmic_bytes for _, plan in self.plans)
+        return q + 2 * sum(e.nbytes for e in self.copies)
+
     def fill(self) -> "Bucket":
-        """Enqueue the quantize launch and the pass-through copies (current stream)."""
-        if self.plan is not None:
-            self.plan.run()
+        """Enqueue the quantize launches and the pass-through copies (current stream)."""
+        for names, plan in self.plans:
+            plan.run([self._src[n] for n in names])
+        if [self._src[e.name].data_ptr() for e in self.copies] != self._copy_ptrs:
+            self._plan_copies()
         if self.copy_plan is not None:
             self.copy_plan.run()
         for dst, src in self._loose:
@@ -160,8 +188,11 @@ def plan_layout(weights: Sequence[tuple[str, tuple, torch.dtype, bool]], bucket_
 class QuantizedBucketWriter:
     """Plans buckets over a fixed list of named weights and fills them on demand.
 
-    Plan once (the parameter storage is stable across RL steps), then per sync:
+    Plan once, then per sync:
     ``for bucket in writer: bucket.fill(); send(bucket.buffer, bucket.bucket_meta())``.
+    A sync whose weights are new tensors (a ``DTensor.full_tensor()`` or a
+    dtype cast every step) first calls ``writer.rebind(named_weights)`` with
+    them; weights whose storage merely moved are picked up by ``fill()``.
     All buckets share one device buffer of ``bucket_bytes``; the caller must not
     refill it before the receiver has consumed the previous bucket (the
     reference's REQ/REP handshake guarantees that).
@@ -185,33 +216,48 @@ class QuantizedBucketWriter:
         self.scale_suffix = scale_suffix
         self.fmt = fmt
         self.block_size = block_size
-        src = dict(named_weights)
         for name, w in named_weights:
             if not w.is_contiguous():
                 raise ValueError(f"{name}: bucket planning needs contiguous weights "
                                  "(the plan keeps pointers to their storage)")
+        self._src = dict(named_weights)   # name -> current tensor, shared with the buckets
+        self._planned = {n: (tuple(w.shape), w.dtype, w.device) for n, w in named_weights}
         layouts = plan_layout([(n, tuple(w.shape), w.dtype, bool(quantize_if(n, w)))
                                for n, w in named_weights],
                               self.bucket_bytes, fmt, block_size, scale_suffix)
-        self.buckets = [self._bucket(lay, src) for lay in layouts]
+        self.buckets = [self._bucket(lay) for lay in layouts]
 
-    def _bucket(self, lay: BucketLayout, src: dict) -> Bucket:
+    def _bucket(self, lay: BucketLayout) -> Bucket:
         by_name = {e.name: e for e in lay.entries}
-        copies, qin, qout = [], [], []
+        copies, quant = [], []
         for name, q in lay.items:
-            w = src[name]
             if not q:
                 e = by_name[name]
-                e.src = w
+                e.src = self._src[name]
                 copies.append(e)
                 continue
             ce, se = by_name[name], by_name[name + self.scale_suffix]
             codes = self.buffer[ce.offset:ce.offset + ce.nbytes].view(ce.dtype).view(ce.shape)
             scales = self.buffer[se.offset:se.offset + se.nbytes].view(se.dtype).view(se.shape)
-            qin.append(w)
-            qout.append((codes, scales))
-        plan = ops.QuantPlan(qin, self.fmt, self.block_size, outputs=qout) if qin else None
-        return Bucket(self.buffer, lay.entries, plan, copies)
+            quant.append((name, codes, scales))
+        return Bucket(self.buffer, lay.entries, quant, copies, self._src, self.fmt, self.block_size)
+
+    def rebind(self, named_weights: Sequence[tuple[str, Tensor]]) -> None:
+        """Point the planned weights at this sync's tensors (same names, shapes,
+        dtypes, device; contiguous).  Weights left out keep their tensors."""
+        new = {}
+        for name, w in named_weights:
+            if name not in self._planned:
+                raise KeyError(f"{name} was not planned")
+            shape, dtype, dev = self._planned[name]
+            if tuple(w.shape) != shape or w.dtype != dtype or w.device != dev or not w.is_contiguous():
+                raise ValueError(f"{name}: got {w.dtype} {tuple(w.shape)} on {w.device}, planned "
+                                 f"contiguous {dtype} {shape} on {dev}")
+            new[name] = w
+        self._src.update(new)
+        for b in self.buckets:
+            for e in b.copies:
+                e.src = self._src[e.name]
 
     def __iter__(self) -> Iterator[Bucket]:
         return iter(self.buckets)

@@ -465,8 +465,16 @@ class QuantPlan:
     The plan allocates every output once (or takes caller-provided output
     views, e.g. slices of a transfer bucket) and uploads a small descriptor
     table (tensor pointers and shapes plus a work-group -> tensor map).
-    ``run()`` re-quantizes whatever the input tensors currently hold -- the RL
-    weight-sync pattern, where the same parameter storage is refreshed every step.
+    ``run()`` re-quantizes whatever the inputs currently hold -- the RL
+    weight-sync pattern, where the same parameters are refreshed every step.
+
+    The table records each input's storage address, so ``run()`` checks them:
+    if an input now points at other storage (``param.data = new``, an FSDP
+    re-gather into a fresh buffer) the table is re-packed and uploaded before
+    the launch.  Callers whose sync produces brand-new tensors every step (a
+    ``DTensor.full_tensor()`` or a ``.to(dtype)``) pass them as
+    ``run(inputs=...)``; they must have the planned shapes and dtype.  The
+    outputs stay the same tensors across re-binds.
 
     Inputs must be device tensors with 16-byte aligned rows (every torch
     allocation of a [N, K] weight with K % 8 == 0 qualifies).
@@ -490,9 +498,10 @@ class QuantPlan:
             raise ValueError("outputs must pair up with tensors")
         self.fmt = fmt
         self.device = dev
-        self.inputs = list(tensors)
+        self.dtype = dt
         self.outputs: list[tuple[Tensor, Tensor]] = []
         br, bc = (int(block_size[0]), int(block_size[1])) if fmt == "fp8_block" else (1, 32)
+        self._block = (br, bc)
         flags = 0
         native = native_arith and dt != torch.float32
         if fmt == "fp8_block":
@@ -502,15 +511,13 @@ class QuantPlan:
                 flags |= _lib.FLAG_NATIVE_ARITH
             elif scale_dtype == torch.bfloat16:
                 flags |= _lib.FLAG_SCALE_BF16
-        descs = (_lib.LrqTensor * len(tensors))()
-        self._views = []
+        self._flags = flags
+        self._owned = outputs is None
+        self._shapes = [tuple(t.shape) for t in tensors]
         nbytes = 0
         for i, t in enumerate(tensors):
-            xm, batch, rows, cols, ld, bstride = matrix_view(t)
-            if xm.data_ptr() != t.data_ptr():
-                raise ValueError(f"tensor {i} is not a strided matrix view; pass .contiguous()")
-            self._views.append(xm)
             shape = tuple(t.shape) if t.dim() >= 2 else (1,) + tuple(t.shape)
+            *_, rows, cols = shape
             if fmt == "fp8_block":
                 cshape, cdt = shape, torch.float8_e4m3fn
                 sdt = dt if native else (torch.bfloat16 if flags & _lib.FLAG_SCALE_BF16 else torch.float32)
@@ -534,22 +541,67 @@ class QuantPlan:
                     raise ValueError(f"output {i} must be contiguous device views of "
                                      f"{cshape} codes and {sshape} {sdt} scales")
             self.outputs.append((codes, scales))
+            nbytes += _nbytes(t) + _nbytes(codes) + _nbytes(scales)
+        self.algorithmic_bytes = nbytes
+        self._bind(list(tensors))
+
+    def _bind(self, tensors: list[Tensor]) -> None:
+        """Pack and upload the descriptor table for the tensors' current storage."""
+        descs = (_lib.LrqTensor * len(tensors))()
+        views = []
+        for i, (t, (codes, scales)) in enumerate(zip(tensors, self.outputs)):
+            xm, batch, rows, cols, ld, bstride = matrix_view(t)
+            if xm.data_ptr() != t.data_ptr():
+                raise ValueError(f"tensor {i} is not a strided matrix view; pass .contiguous()")
+            views.append(xm)
             descs[i].in_ = xm.data_ptr()
             descs[i].codes = codes.data_ptr()
             descs[i].scales = scales.data_ptr()
             descs[i].batch, descs[i].rows, descs[i].cols = batch, rows, cols
             descs[i].ld, descs[i].batch_stride = ld, bstride
-            nbytes += _nbytes(t) + _nbytes(codes) + _nbytes(scales)
-        self.algorithmic_bytes = nbytes
-        self._launch = _GroupLaunch(fmt, descs, len(tensors), _IN_DTYPES[dt], (br, bc), flags, dev)
-        if outputs is None:
-            self._launch.buffers += [t for pair in self.outputs for t in pair]
-        self.units = self._launch.units
+        launch = _GroupLaunch(self.fmt, descs, len(tensors), _IN_DTYPES[self.dtype], self._block,
+                              self._flags, self.device)
+        if self._owned:
+            launch.buffers += [t for pair in self.outputs for t in pair]
+        self._launch = launch
+        self._views = views
+        self.inputs = tensors
+        self._sig = [(t.data_ptr(), t.stride()) for t in tensors]
+        self.units = launch.units
 
-    def run(self) -> list[tuple[Tensor, Tensor]]:
-        """Enqueue the launch on the current stream; returns the (codes, scales) list."""
+    def run(self, inputs: Optional[Sequence[Tensor]] = None) -> list[tuple[Tensor, Tensor]]:
+        """Enqueue the launch on the current stream; returns the (codes, scales) list.
+
+        ``inputs``: the current tensors, when the sync produced new ones (same
+        count, shapes, dtype and device as planned).  Without it, the planned
+        tensors are re-read, re-bound first if any now points at other storage.
+        """
+        if inputs is not None:
+            inputs = list(inputs)
+            if len(inputs) != len(self._shapes):
+                raise ValueError(f"QuantPlan.run: {len(inputs)} inputs for a plan of {len(self._shapes)}")
+            for i, t in enumerate(inputs):
+                _check_input(t, "QuantPlan.run")
+                if t.dtype != self.dtype or t.device != self.device or tuple(t.shape) != self._shapes[i]:
+                    raise ValueError(f"QuantPlan.run: input {i} is {t.dtype} {tuple(t.shape)} on "
+                                     f"{t.device}; the plan has {self.dtype} {self._shapes[i]} on "
+                                     f"{self.device} (build a new plan)")
+            if self._moved(inputs):
+                self._bind(inputs)
+            else:
+                self.inputs = inputs  # same storage: keep the caller's current objects alive
+        elif self._moved(self.inputs):
+            for i, t in enumerate(self.inputs):
+                if tuple(t.shape) != self._shapes[i] or t.dtype != self.dtype:
+                    raise ValueError(f"QuantPlan.run: input {i} changed to {t.dtype} {tuple(t.shape)}"
+                                     f" (planned {self.dtype} {self._shapes[i]}); build a new plan")
+            self._bind(self.inputs)
         self._launch.run()
         return self.outputs
+
+    def _moved(self, tensors: Sequence[Tensor]) -> bool:
+        """True if any tensor's storage address or strides differ from the table's."""
+        return any(t.data_ptr() != p or t.stride() != st for t, (p, st) in zip(tensors, self._sig))
 
 
 class DequantPlan:
