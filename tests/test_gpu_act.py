@@ -160,7 +160,7 @@ def reference_forward(lin: nn.Linear, x: torch.Tensor, cfg: FP8Config) -> tuple:
     w_dq = T.dequantize_tensor(q, s16, 128).float()
     b = lin.bias.data.float().to(DEV) if lin.bias is not None else None
     y = F.linear(x_dq.to(DEV), w_dq.to(DEV), b)
-    return q, s16, y.reshape(*x.shape[:-1], lin.out_features).to(x.dtype)
+    return q, s16, y.to(x.dtype)  # [prod(leading), out_features] (fp8_rollout.py:56-78)
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
@@ -178,8 +178,26 @@ def test_fp8_linear_matches_reference(dtype, pow2, bias):
     assert torch.equal(mod.weight_scale.cpu().view(torch.int16), s16.view(torch.int16))
     with torch.no_grad():
         y = mod(x)
-    assert y.dtype == dtype and y.shape == (3, 17, 384)
+    assert y.dtype == dtype and y.shape == (51, 384)  # the reference's flattened shape
     assert torch.equal(y, y_ref)
+    keep = _FP8W8A8Linear(lin, WeightQuantizer(cfg), cfg, 128, keep_leading_dims=True)
+    with torch.no_grad():
+        yk = keep(x)
+    assert yk.shape == (3, 17, 384) and torch.equal(yk.reshape(51, 384), y_ref)
+
+
+def test_fp8_linear_float64_activations():
+    """x.to(float32) first, everything in float32, then y.to(float64) (fp8_rollout.py:53-78)."""
+    torch.manual_seed(5)
+    lin = nn.Linear(256, 128).to(DEV)
+    cfg = FP8Config(precision="fp8")
+    mod = _FP8W8A8Linear(lin, WeightQuantizer(cfg), cfg, 128)
+    x = torch.from_numpy(acts((2, 7, 256)).astype(np.float64) * (1 + 1e-9)).to(DEV)
+    with torch.no_grad():
+        y = mod(x)
+    _, _, y_ref = reference_forward(lin, x.float(), cfg)
+    assert y.dtype == torch.float64 and y.shape == (14, 128)
+    assert torch.equal(y, y_ref.double())
 
 
 def test_fp8_linear_errors_and_cpu_module():
@@ -232,7 +250,7 @@ def test_rollout_quantizer_patch_and_restore():
     off.quantize_model(net)
     assert isinstance(net.inp, nn.Linear)
     cfg = FP8Config(precision="fp8", num_first_layers_in_bf16=1, num_last_layers_in_bf16=1)
-    rq = FP8RolloutQuantizer(cfg)
+    rq = FP8RolloutQuantizer(cfg, keep_leading_dims=True)  # this model feeds 3-D activations
     assert rq.should_skip_layer("x", 0, 7) and rq.should_skip_layer("x", 6, 7)
     assert not rq.should_skip_layer("x", 1, 7) and not rq.should_skip_layer("x", 5, 7)
     originals = dict(net.named_modules())
@@ -253,3 +271,35 @@ def test_rollout_quantizer_patch_and_restore():
         assert net.get_submodule(n) is originals[n]
     with torch.no_grad():
         assert torch.equal(net(x), y0)
+
+
+def test_quantize_model_grouped_weights_equal_the_reference_ops():
+    """quantize_model's grouped launches give every patched module the buffers of
+    the reference's per-layer quantize_tensor (float32 upcast, bf16 scales), for
+    bf16, fp16, fp32 and float64 weights and a CPU-resident linear."""
+    torch.manual_seed(6)
+    shapes = [(384, 256), (128, 512), (1024, 256), (256, 1024), (640, 384)] * 5
+    net = nn.Sequential(*[nn.Linear(i, o, bias=(k % 2 == 0)) for k, (o, i) in enumerate(shapes)])
+    net = net.to(DEV, torch.bfloat16)
+    net[3].to(torch.float16)
+    net[7].to(torch.float32)
+    net[11].to(torch.float64)
+    cpu_lin = nn.Linear(256, 128)
+    net.append(cpu_lin)
+    want = {}
+    for name, m in net.named_modules():
+        if isinstance(m, nn.Linear):
+            q, s = T.quantize_tensor(m.weight.data.cpu().float(), 128, False)
+            want[name] = (q.view(torch.uint8), s.to(torch.bfloat16).view(torch.int16))
+    rq = FP8RolloutQuantizer(FP8Config(precision="fp8"))
+    rq.quantize_model(net)
+    patched = {n: m for n, m in net.named_modules() if isinstance(m, _FP8W8A8Linear)}
+    assert len(patched) == len(want)
+    for name, m in patched.items():
+        assert torch.equal(m.weight_fp8.cpu().view(torch.uint8), want[name][0]), name
+        assert torch.equal(m.weight_scale.cpu().view(torch.int16), want[name][1]), name
+    assert patched[str(len(shapes))].weight_fp8.device.type == "cpu"
+    x = torch.randn(9, 256, device=DEV, dtype=torch.bfloat16)
+    with torch.no_grad():
+        y = net[0](x)
+    assert y.shape == (9, 384)

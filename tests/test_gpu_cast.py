@@ -128,10 +128,14 @@ def test_dynamic_weight_loader_scaled_extension():
     and everything else keep their dtype and identity."""
     say("DynamicWeightLoader scaled")
     sd, eng = _mixed_state(), _Engine()
+    # a contiguous weight view 2 bytes into its buffer: not 16-byte aligned, so it
+    # cannot share the grouped launch (its own launch instead)
+    base = (torch.randn(64 * 256 + 1, device=DEV) * 0.02).to(torch.bfloat16)
+    sd["model.layers.1.self_attn.o_proj.weight"] = base[1:].view(64, 256)
     DynamicWeightLoader.load_weights(eng, sd, fp8_config={"enabled": True, "scaled": True})
     out = eng.sd
     quantized = {"model.layers.0.mlp.down_proj.weight", "model.layers.0.self_attn.q_proj.weight",
-                 "cpu.bf16.weight"}
+                 "cpu.bf16.weight", "model.layers.1.self_attn.o_proj.weight"}
     empty = out["empty.weight"], out["empty.weight_scale_inv"]
     assert empty[0].shape == (0, 128) and empty[1].shape == (0, 1)
     for k, t in sd.items():
