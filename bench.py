@@ -26,6 +26,11 @@ already resident in HBM:
   kv:  FP8KVCacheQuantizer scale recalibration: max(|W|.max(), FLT_MIN)/448 over
        the 108 q/k/v_proj weights of Qwen3-8B (c2's values), one grouped
        amax launch + one per-tensor finishing launch.
+  c2host / casthost: quantize_state_dict on the c2 weights / DynamicWeightLoader
+       on the whole Qwen3-8B state, both held in HOST memory: PCIe-inclusive
+       rates (the inputs are not resident in HBM), reported apart from the metric.
+  rollout: FP8RolloutQuantizer.quantize_model on a 36-layer Qwen3-8B-shaped
+       module of nn.Linear layers on the device (quantize, swap, restore).
   act: the W8A8 rollout linear's activation fake-quant (fp8_rollout.py:53-72)
        on the seven linear inputs of one Qwen3-8B layer for an 8192-token
        prefill chunk (bf16 in, float32 out), one launch per linear, every input
@@ -63,10 +68,11 @@ PROFILE_FOR = {"c1": "k_tile128_single_4096x4096_c1", "c2": "k_tile128_qwen3_8b_
                "c5": "k_mx_qwen3_8b_mxfp4", "c2d": "k_dequant_qwen3_8b_fp8_1x128_to_bf16",
                "act": "k_act_qdq_qwen3_8b_prefill_8192", "kv": "k_amax_qwen3_8b_qkv_scales",
                "cast": "k_cast_e4m3_qwen3_8b_state_dynamic_weight_loader",
-               "c4d": "k_mx_dequant_qwen3_8b_mxfp8_to_bf16", "c2sd": "k_row_qwen3_8b_state_dict_dropin"}
+               "c4d": "k_mx_dequant_qwen3_8b_mxfp8_to_bf16", "c2sd": "k_row_qwen3_8b_state_dict_dropin",
+               "rollout": "k_row_qwen3_8b_rollout_quantize_model"}
 KERNEL_FOR = {"c1": "k_tile128", "c2": "k_tile128", "c3": "k_tile128", "c4": "k_mx", "c5": "k_mx",
               "c2r": "k_row", "c2d": "k_dequant", "act": "k_act_qdq8", "kv": "k_amax", "c2sd": "k_row", "bucket": "k_tile128",
-              "cast": "k_cast_e4m3", "c4d": "k_mx_dequant"}
+              "cast": "k_cast_e4m3", "c4d": "k_mx_dequant", "rollout": "k_row"}
 PREFILL_TOKENS = 8192
 
 
@@ -156,8 +162,15 @@ def moe_layer(torch, dev, seed, layer, experts=128):
 # ---------------------------------------------------------------------------
 # CPU baseline: the reference's op sequence in torch on the host (bounded sample)
 # ---------------------------------------------------------------------------
-def cpu_baseline(torch, ws, fmt, fmt_block, seconds):
-    """Time the CPU path on the host over whole tensors until `seconds` elapse.
+def cpu_baseline(torch, ws, fmt, fmt_block, seconds, full_bytes=None):
+    """The CPU path on the host, timed as BASELINE.md section 3 asks: one warm-up
+    pass, then the median of 3 passes over the same bounded sample.
+
+    The sample is the first tensors of the workload, as many as fit in about
+    ``seconds / 4`` of 16-thread work (so the four passes take about ``seconds``);
+    the 1-thread leg does the same on a sample sized for 1 thread.  GB/s counts
+    algorithmic bytes, so a rate extrapolates linearly to the whole workload;
+    the extrapolated whole-set time is reported with it.
 
     FP8 blockwise: the reference's torch op sequence (oracle/torch_ref.py).
     MX formats have no reference CPU path: the C oracle's MX restatement.
@@ -169,11 +182,17 @@ def cpu_baseline(torch, ws, fmt, fmt_block, seconds):
 
     threads = max(1, min(os.cpu_count() or 1, 16))
     prev = torch.get_num_threads()
+    legs = {}
     try:
-        torch.set_num_threads(threads)
-        done_bytes, t_total, n = _cpu_pass(torch, O, torch_ref, np, ws, fmt, fmt_block, seconds, threads)
-        torch.set_num_threads(1)
-        one_bytes, one_t, one_n = _cpu_pass(torch, O, torch_ref, np, ws, fmt, fmt_block, seconds / 4, 1)
+        for nt, budget in ((threads, seconds / 4), (1, seconds / 8)):
+            torch.set_num_threads(nt)
+            sample = _cpu_sample(torch, O, torch_ref, np, ws, fmt, fmt_block, budget, nt)
+            _cpu_pass(torch, O, torch_ref, np, sample, fmt, fmt_block, nt)  # warm-up
+            times, nbytes = [], 0
+            for _ in range(3):
+                nbytes, t = _cpu_pass(torch, O, torch_ref, np, sample, fmt, fmt_block, nt)
+                times.append(t)
+            legs[nt] = (len(sample), nbytes, sorted(times)[1])
     finally:
         torch.set_num_threads(prev)
     what = {
@@ -185,18 +204,45 @@ def cpu_baseline(torch, ws, fmt, fmt_block, seconds):
         "cast": "torch's own tensor.to(float8_e4m3fn) per tensor, as weight_loader.py:19-43 runs it",
         "mx_dequant": "oracle/torch_ref.py mx_dequant (torch decode, E8M0 widen, product, bf16 cast)",
     }.get(fmt, f"the C oracle's {fmt} restatement (the reference has no MX CPU path)")
+    n, nb, t = legs[threads]
+    n1, nb1, t1 = legs[1]
+    rate, rate1 = nb / t / 1e9, nb1 / t1 / 1e9
+    whole = "" if not full_bytes else (
+        f"; extrapolated to the whole workload ({full_bytes / 1e9:.2f} GB): "
+        f"{full_bytes / 1e9 / rate:.1f} s at {threads} threads, {full_bytes / 1e9 / rate1:.1f} s at 1 thread")
     return {
-        "value": round(done_bytes / t_total / 1e9, 3),
+        "value": round(rate, 3),
         "unit": "GB/s",
         "cores": threads,
         "kind": "port",
-        "sample": (f"first {n} tensors of the same weight set ({done_bytes / 1e9:.2f} GB "
-                   f"algorithmic) through {what}, {threads} threads on {os.cpu_count()} "
-                   f"visible cores"),
-        "value_1thread": round(one_bytes / one_t / 1e9, 3),
-        "sample_1thread": f"first {one_n} tensors, 1 thread",
+        "sample": (f"first {n} tensors of the same weight set ({nb / 1e9:.2f} GB algorithmic) through "
+                   f"{what}; {threads} threads on {os.cpu_count()} visible cores; 1 warm-up pass, then the "
+                   f"median of 3 passes ({t:.2f} s){whole}"),
+        "value_1thread": round(rate1, 3),
+        "sample_1thread": (f"first {n1} tensors ({nb1 / 1e9:.2f} GB), 1 thread, 1 warm-up + median of 3 "
+                           f"({t1:.2f} s); GB/s extrapolates linearly to the whole set"),
         "cpu_model": _cpu_model(),
     }
+
+
+def _cpu_sample(torch, O, torch_ref, np, ws, fmt, fmt_block, budget, threads):
+    """The first tensors of ``ws`` whose CPU pass takes about ``budget`` seconds,
+    judged from a pass over the first tensor (at least one tensor)."""
+    _, t0 = _cpu_pass(torch, O, torch_ref, np, ws[:1], fmt, fmt_block, threads)
+    b0 = _item_bytes(ws[0])
+    total, out = 0, []
+    for w in ws:
+        if out and total * t0 / b0 >= budget:
+            break
+        out.append(w)
+        total += _item_bytes(w)
+    return out
+
+
+def _item_bytes(w) -> int:
+    if isinstance(w, (tuple, list)):
+        return sum(t.numel() * t.element_size() for t in w)
+    return w.numel() * w.element_size()
 
 
 def _cpu_model() -> str:
@@ -210,10 +256,9 @@ def _cpu_model() -> str:
     return "unknown"
 
 
-def _cpu_pass(torch, O, torch_ref, np, ws, fmt, fmt_block, seconds, threads):
-    """Whole tensors through the CPU path until `seconds` of timed work."""
+def _cpu_pass(torch, O, torch_ref, np, ws, fmt, fmt_block, threads):
+    """One pass over whole tensors through the CPU path: (algorithmic bytes, seconds)."""
     done_bytes = 0
-    n = 0
     t_total = 0.0
     for w in ws:
         if fmt == "mx_dequant":
@@ -222,9 +267,6 @@ def _cpu_pass(torch, O, torch_ref, np, ws, fmt, fmt_block, seconds, threads):
             out = torch_ref.mx_dequant(c, sc, 8, torch.bfloat16)
             t_total += time.perf_counter() - t0
             done_bytes += c.numel() + sc.numel() + out.numel() * 2
-            n += 1
-            if t_total >= seconds:
-                break
             continue
         if fmt == "fp8_dequant":
             c, sc = w[0].cpu(), w[1].cpu()
@@ -232,9 +274,6 @@ def _cpu_pass(torch, O, torch_ref, np, ws, fmt, fmt_block, seconds, threads):
             out = torch_ref.dequantize_tensor(c, sc, fmt_block[1]).to(torch.bfloat16)
             t_total += time.perf_counter() - t0
             done_bytes += c.numel() + sc.numel() * 2 + out.numel() * 2
-            n += 1
-            if t_total >= seconds:
-                break
             continue
         x = w.cpu()
         if fmt == "kv":
@@ -246,7 +285,7 @@ def _cpu_pass(torch, O, torch_ref, np, ws, fmt, fmt_block, seconds, threads):
             t0 = time.perf_counter()
             q = x.to(torch.float8_e4m3fn)  # weight_loader.py:33, the reference's own op
             t_total += time.perf_counter() - t0
-            done_bytes += x.numel() * 2 + q.numel()
+            done_bytes += x.numel() * x.element_size() + q.numel()
         elif fmt == "act":
             t0 = time.perf_counter()
             out = torch_ref.act_qdq(x, fmt_block[1])
@@ -266,10 +305,7 @@ def _cpu_pass(torch, O, torch_ref, np, ws, fmt, fmt_block, seconds, threads):
             q, s = O.mx_quant(xb, "bf16", 8 if fmt == "mxfp8" else 4, nthreads=threads)
             t_total += time.perf_counter() - t0
             done_bytes += x.numel() * 2 + q.size + s.size
-        n += 1
-        if t_total >= seconds:
-            break
-    return done_bytes, t_total, n
+    return done_bytes, t_total
 
 
 class _BucketFill:
@@ -314,6 +350,39 @@ class _LoaderCall:
 
     def run(self):
         self.loader.load_weights(self, self.sd, fp8_config={"enabled": True})
+
+
+class _RolloutCall:
+    """FP8RolloutQuantizer.quantize_model on a Qwen3-8B-shaped module (36 layers x
+    q,k,v,o,gate,up,down nn.Linear on the device), then restore_model: the
+    weight quantization of every linear plus the module swaps, host work
+    included."""
+
+    launch_timed_inside = True
+
+    def __init__(self, torch, ws, names):
+        import torch.nn as nn
+
+        from lumenrl_amd.quantization import FP8Config, FP8RolloutQuantizer
+
+        layers = nn.ModuleList()
+        it = iter(zip(names, ws))
+        for _ in range(36):
+            blk = nn.Module()
+            for _ in range(7):
+                name, w = next(it)
+                lin = nn.Linear(w.shape[1], w.shape[0], bias=False, device="meta")
+                lin.weight = nn.Parameter(w, requires_grad=False)
+                setattr(blk, name.split(".")[-1], lin)
+            layers.append(blk)
+        self.model = layers
+        self.rq = FP8RolloutQuantizer(FP8Config(precision="fp8"))
+        n = sum(w.numel() for w in ws)
+        self.algorithmic_bytes = n * 2 + n + (n // 128) * 2
+
+    def run(self):
+        self.rq.quantize_model(self.model)
+        self.rq.restore_model(self.model)
 
 
 class _ActLayer:
@@ -392,6 +461,14 @@ def run(args):
                  "format": "fp8_block_1x128_bf16_scales",
                  "launches_per_step": len(list(ops.launch_chunks(ws))),
                  "host_work_timed": True}
+    elif cfg == "rollout":
+        ws, names = qwen3_8b_set(torch, dev, args.seed, "normal")
+        plans = [_RolloutCall(torch, ws, names)]
+        workload = "qwen3-8b-module-fp8-rollout-quantize-model-1x128"
+        cpu_ws, cpu_blk, cpu_fmt = ws, (1, 128), "fp8_block"
+        extra = {"tensors": len(ws), "layers": 36, "elements": sum(w.numel() for w in ws),
+                 "format": "fp8_block_1x128_bf16_scales + module swap and restore",
+                 "launches_per_step": len(list(ops.launch_chunks(ws))), "host_work_timed": True}
     elif cfg == "bucket":
         from lumenrl_amd.quantization import QuantizedBucketWriter
 
@@ -572,8 +649,107 @@ def run(args):
     }
     if not args.no_cpu and cpu_ws:
         log("[bench] cpu baseline ...")
-        result["cpu_baseline"] = cpu_baseline(torch, cpu_ws, cpu_fmt, cpu_blk, args.cpu_seconds)
+        result["cpu_baseline"] = cpu_baseline(torch, cpu_ws, cpu_fmt, cpu_blk, args.cpu_seconds,
+                                              full_bytes=step_bytes)
     print(json.dumps(result), flush=True)
+
+
+def run_host(args):
+    """Host-resident workloads: the drop-in calls on state dicts held in host
+    memory, PCIe transfers included.  A step is one whole call; ``value`` is the
+    call's algorithmic bytes over its wall time.  These rates are bound by the
+    PCIe link, not by HBM, so they carry a ``pcie`` object instead of a kernel
+    roofline; the reference's CPU path is timed beside them."""
+    import torch
+
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    cfg = args.config
+    t0 = time.time()
+    if cfg == "c2host":
+        from lumenrl_amd.quantization import FP8Config, WeightQuantizer
+
+        ws, names = qwen3_8b_set(torch, dev, args.seed, "normal")
+        sd = {n: w.cpu() for n, w in zip(names, ws)}
+        del ws
+        wq = WeightQuantizer(FP8Config())
+        call = lambda: wq.quantize_state_dict(sd)  # noqa: E731
+        n = sum(w.numel() for w in sd.values())
+        h2d, d2h = 2 * n, n + (n // 128) * 2
+        workload = "qwen3-8b-linears-host-resident-quantize-state-dict-fp8-1x128"
+        cpu_ws, cpu_fmt, cpu_blk = list(sd.values()), "fp8_block", (1, 128)
+    else:  # casthost
+        from lumenrl_amd.engine.inference import DynamicWeightLoader
+
+        named = qwen3_8b_state(torch, dev, args.seed)
+        sd = {k: w.cpu() for k, w in named}
+        del named
+
+        class _Eng:
+            def update_weights(self, s):
+                self.sd = s
+
+        eng = _Eng()
+        call = lambda: DynamicWeightLoader.load_weights(eng, sd, fp8_config={"enabled": True})  # noqa: E731
+        n = sum(w.numel() for w in sd.values())
+        h2d, d2h = 2 * n, n
+        workload = "qwen3-8b-state-host-resident-dynamic-weight-loader-e4m3-cast"
+        cpu_ws, cpu_fmt, cpu_blk = list(sd.values()), "cast", (1, 1)
+    torch.cuda.synchronize()
+    alg = h2d + d2h
+    log(f"[bench] {workload}: {len(sd)} host tensors, {alg / 1e9:.3f} GB per call, "
+        f"setup {time.time() - t0:.1f}s")
+    for _ in range(args.warmup):
+        call()
+    torch.cuda.synchronize()
+    torch.cuda.reset_peak_memory_stats()
+    base = torch.cuda.memory_allocated()
+    times = []
+    for _ in range(args.steps):
+        torch.cuda.synchronize()
+        a = time.perf_counter()
+        call()
+        torch.cuda.synchronize()
+        times.append(time.perf_counter() - a)
+    peak = torch.cuda.max_memory_allocated() - base
+    ms = sum(times) / len(times) * 1e3
+    med = sorted(times)[len(times) // 2] * 1e3
+    value = alg / (ms * 1e-3) / 1e9
+    log(f"[bench] {ms:.1f} ms/call ({value:.1f} GB/s algorithmic, H2D {h2d / ms / 1e6:.1f} GB/s), "
+        f"device peak {peak / 2**20:.0f} MiB")
+    result = {
+        "metric": metric_name() + " [host-resident variant: PCIe-inclusive, not the HBM metric]",
+        "value": round(value, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 3),
+        "median_ms_per_step": round(med, 3),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (seeded on-device bf16 weights copied to host memory)",
+        "config": {"workload": workload, "tensors": len(sd), "elements": n, "host_resident": True,
+                   "algorithmic_bytes_per_step": alg,
+                   "window_bytes": _ops().HOST_WINDOW_BYTES, "window_depth": _ops().HOST_WINDOW_DEPTH},
+        "roofline": None,
+        "pcie": {"h2d_bytes": h2d, "d2h_bytes": d2h, "h2d_GBps": round(h2d / ms / 1e6, 2),
+                 "d2h_GBps": round(d2h / ms / 1e6, 2), "link_peak_GBps_per_direction": 64.0,
+                 "device_peak_bytes": int(peak)},
+    }
+    if not args.no_cpu:
+        log("[bench] cpu baseline ...")
+        result["cpu_baseline"] = cpu_baseline(torch, cpu_ws, cpu_fmt, cpu_blk, args.cpu_seconds,
+                                              full_bytes=alg)
+    print(json.dumps(result), flush=True)
+
+
+def _ops():
+    from lumenrl_amd.quantization import ops
+
+    return ops
 
 
 def run_copy(args):
@@ -603,7 +779,9 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--config", default="c2", choices=["c1", "c2", "c3", "c4", "c5", "c2r", "c2d", "c2sd", "bucket", "act", "kv", "cast", "c4d"])
+    ap.add_argument("--config", default="c2", choices=["c1", "c2", "c3", "c4", "c5", "c2r", "c2d", "c2sd", "bucket",
+                                                      "act", "kv", "cast", "c4d", "c2host", "casthost",
+                                                      "rollout"])
     ap.add_argument("--seed", type=int, default=1000)
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
@@ -617,6 +795,8 @@ def main():
         sys.exit(2)
     if args.mode == "copy":
         run_copy(args)
+    elif args.config in ("c2host", "casthost"):
+        run_host(args)
     else:
         run(args)
 

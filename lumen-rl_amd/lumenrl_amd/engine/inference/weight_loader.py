@@ -4,9 +4,11 @@ Same class, method, arguments, config keys and log texts.  With FP8 enabled the
 reference casts every floating tensor of the state dict with
 ``tensor.to(torch.float8_e4m3fn)`` (unscaled, :19-43) one tensor at a time;
 here the tensors of one dtype go through a few grouped liblrq launches (8, 16,
-32, then 64 tensors each, issued as each is planned) whose bytes equal torch's cast (round to nearest even; |x| rounding past 448,
-+-inf and NaN -> NaN 0x7F|sign).  CPU tensors are staged through the current
-HIP device and come back on the CPU, as the reference returns them.
+32, then 64 tensors each, issued as each is planned) whose bytes equal torch's
+cast (round to nearest even; |x| rounding past 448, +-inf and NaN -> NaN
+0x7F|sign).  CPU tensors go through the current HIP device in bounded
+pipelined windows and come back on the CPU (pinned), as the reference returns
+them; a process with no HIP device raises rather than casting on the CPU.
 
 Opt-in extension (no reference counterpart): ``fp8_config["scaled"] = True``
 replaces the unscaled cast by blockwise FP8 with float32 ``<name>_scale_inv``
@@ -66,61 +68,86 @@ def _kernel_input(t: torch.Tensor, device: torch.device) -> torch.Tensor:
 
 
 def _cast_all(tensors: dict[str, torch.Tensor]) -> dict[str, torch.Tensor]:
-    """e4m3fn casts of ``tensors``: chunked grouped launches per (device, dtype),
-    issued while the rest is still being staged."""
-    dev = None
-    host = any(not t.is_cuda for t in tensors.values())
-    launches = ops.ChunkedLaunches(lambda xs: ops.CastPlan(xs).run(), defer=host)
-    out = dict(tensors)
-    for name, t in tensors.items():
-        if t.dtype == torch.float8_e4m3fn:
-            continue  # tensor.to(its own dtype) is the tensor itself
-        if t.is_cuda:
+    """e4m3fn casts of ``tensors``: device tensors in chunked grouped launches
+    per (device, dtype); host tensors through bounded pipelined windows
+    (``ops.run_host_windows``), returned as (pinned) CPU tensors."""
+
+    def cast(xs: list[torch.Tensor]) -> list[torch.Tensor]:
+        launches = ops.ChunkedLaunches(lambda ys: ops.CastPlan(ys).run())
+        done: dict[int, torch.Tensor] = {}
+        for i, t in enumerate(xs):
             x = _kernel_input(t, t.device)
-        else:
-            dev = dev or ops.require_device()
-            x = _kernel_input(t, dev)
-        if x.numel():
-            launches.add((x.device, x.dtype), name, x)
-        else:
-            out[name] = torch.empty(t.shape, dtype=torch.float8_e4m3fn, device=t.device)
-    for n, q in launches.flush().items():
-        out[n] = q if tensors[n].is_cuda else q.to(tensors[n].device)
+            if x.numel():
+                launches.add((x.device, x.dtype), i, x)
+            else:
+                done[i] = torch.empty(t.shape, dtype=torch.float8_e4m3fn, device=t.device)
+        done.update(launches.flush())
+        return [done[i] for i in range(len(xs))]
+
+    out = dict(tensors)
+    # tensor.to(its own dtype) is the tensor itself
+    todo = {n: t for n, t in tensors.items() if t.dtype != torch.float8_e4m3fn}
+    on_dev = [n for n, t in todo.items() if t.is_cuda]
+    on_host = [n for n, t in todo.items() if not t.is_cuda]
+    out.update(zip(on_dev, cast([todo[n] for n in on_dev])))
+    if on_host:
+        dev = ops.require_device()
+        items = []
+        for n in on_host:
+            t = todo[n]
+            q = torch.empty(t.shape, dtype=torch.float8_e4m3fn, pin_memory=True)
+            out[n] = q
+            items += ops.host_items(n, (t.reshape(-1),), (q.view(-1),))  # elementwise: any split
+        ops.run_host_windows(items, lambda ins: [(q,) for q in cast([x for (x,) in ins])], dev)
     return out
 
 
 def _scaled(tensors: dict[str, torch.Tensor], block: tuple[int, int],
             quantize_if: Callable[[str, torch.Tensor], bool]) -> dict[str, torch.Tensor]:
     """Blockwise FP8 + ``<name>_scale_inv`` for accepted tensors, the rest kept."""
-    dev = None
-    host = any(not t.is_cuda for t in tensors.values() if isinstance(t, torch.Tensor))
-    launches = ops.ChunkedLaunches(lambda xs: ops.QuantPlan(xs, "fp8_block", block).run(),
-                                   defer=host)
-    results: dict[str, tuple[torch.Tensor, torch.Tensor]] = {}
-    for name, t in tensors.items():
-        if not quantize_if(name, t):
-            continue
-        if not t.is_cuda:
-            dev = dev or ops.require_device()
-        x = _kernel_input(t, t.device if t.is_cuda else dev)
-        if x.numel() and x.data_ptr() % 16 == 0:
-            launches.add((x.device, x.dtype), name, x)
-        elif x.numel():  # a view at an odd offset needs another kernel: its own launch
-            results[name] = ops.fp8_block_quant(x, block)
-        else:  # nothing to launch: empty codes and scales of the right shapes
-            *lead, r, c = x.shape
-            results[name] = (torch.empty(x.shape, dtype=torch.float8_e4m3fn, device=x.device),
-                             torch.empty((*lead, -(-r // block[0]), -(-c // block[1])),
-                                         dtype=torch.float32, device=x.device))
-    results.update(launches.flush())
+
+    def quantize(xs: list[torch.Tensor]) -> list[tuple[torch.Tensor, torch.Tensor]]:
+        launches = ops.ChunkedLaunches(lambda ys: ops.QuantPlan(ys, "fp8_block", block).run())
+        done: dict[int, tuple[torch.Tensor, torch.Tensor]] = {}
+        for i, t in enumerate(xs):
+            x = _kernel_input(t, t.device)
+            if x.numel() and x.data_ptr() % 16 == 0:
+                launches.add((x.device, x.dtype), i, x)
+            elif x.numel():  # a view at an odd offset needs another kernel: its own launch
+                done[i] = ops.fp8_block_quant(x, block)
+            else:  # nothing to launch: empty codes and scales of the right shapes
+                *lead, r, c = x.shape
+                done[i] = (torch.empty(x.shape, dtype=torch.float8_e4m3fn, device=x.device),
+                           torch.empty((*lead, -(-r // block[0]), -(-c // block[1])),
+                                       dtype=torch.float32, device=x.device))
+        done.update(launches.flush())
+        return [done[i] for i in range(len(xs))]
+
+    todo = [n for n, t in tensors.items() if quantize_if(n, t)]
+    on_dev = [n for n in todo if tensors[n].is_cuda]
+    on_host = [n for n in todo if not tensors[n].is_cuda]
+    results = dict(zip(on_dev, quantize([tensors[n] for n in on_dev])))
+    if on_host:
+        dev = ops.require_device()
+        items = []
+        for n in on_host:
+            t = tensors[n]
+            *lead, r, c = t.shape
+            outs = (torch.empty(t.shape, dtype=torch.float8_e4m3fn, pin_memory=True),
+                    torch.empty((*lead, -(-r // block[0]), -(-c // block[1])), dtype=torch.float32,
+                                pin_memory=True))
+            results[n] = outs
+            # 2-D: whole tile rows per chunk; 3-D: whole matrices (experts) per chunk
+            tiles = t.dim() == 2
+            items += ops.host_items(n, (t,), outs, multiple=block[0] if tiles else 1,
+                                    out_div=(1, block[0]) if tiles else (1, 1))
+        ops.run_host_windows(items, lambda ins: quantize([x for (x,) in ins]), dev)
     out: dict[str, torch.Tensor] = {}
     for name, t in tensors.items():
         if name not in results:
             out[name] = t
             continue
         codes, scales = results[name]
-        if not t.is_cuda:
-            codes, scales = codes.to(t.device), scales.to(t.device)
         out[name] = codes
         out[f"{name}_scale_inv"] = scales
     return out

@@ -406,14 +406,12 @@ class ChunkedLaunches:
     (dtype, device); a group calls ``run(items) -> outputs`` as soon as it holds
     the next chunk size (8, 16, 32, then 64), so the device starts on the first
     tensors of a state dict while the host still stages and plans the rest.
-    ``flush()`` runs what is left and returns ``{name: output}``.  With
-    ``defer`` every launch waits for ``flush()`` (same chunk sizes): callers that
-    stage host tensors use it, since a blocking host-to-device copy would
-    otherwise wait for the launches queued before it.
+    ``flush()`` runs what is left and returns ``{name: output}``.  Host tensors
+    are not staged here: ``run_host_windows`` moves them in bounded windows.
     """
 
-    def __init__(self, run, *, defer: bool = False, first: int = 8, most: int = 64) -> None:
-        self._run, self._defer, self._first, self._most = run, defer, first, most
+    def __init__(self, run, *, first: int = 8, most: int = 64) -> None:
+        self._run, self._first, self._most = run, first, most
         self._groups: dict = {}
         self.results: dict = {}
 
@@ -423,7 +421,7 @@ class ChunkedLaunches:
             g = self._groups[group] = {"names": [], "items": [], "next": self._first}
         g["names"].append(name)
         g["items"].append(item)
-        if not self._defer and len(g["names"]) == g["next"]:
+        if len(g["names"]) == g["next"]:
             self._launch(g["names"], g["items"])
             g["names"], g["items"] = [], []
             g["next"] = min(2 * g["next"], self._most)
@@ -440,6 +438,111 @@ class ChunkedLaunches:
                 i += len(chunk)
             g["names"], g["items"] = [], []
         return self.results
+
+
+HOST_WINDOW_BYTES = 512 << 20  # input bytes per staging window of run_host_windows
+HOST_WINDOW_DEPTH = 2          # windows holding device memory at once
+
+
+def run_host_windows(items: Sequence[tuple], launch, device: torch.device, *,
+                     window_bytes: Optional[int] = None, depth: Optional[int] = None) -> dict:
+    """Device launches over HOST-resident inputs, in bounded pipelined windows.
+
+    ``items``: ``[(key, (host tensor, ...)), ...]`` in order; an item may carry a
+    third element, a tuple of host tensors to receive its outputs (see
+    ``host_items``).  ``launch(ins)`` takes ``[(device tensor, ...), ...]`` for
+    one window, enqueues the work on the current stream and returns
+    ``[(device output, ...), ...]`` in the same order.  Returns
+    ``{key: (host output, ...)}``: pinned CPU tensors, complete when this returns.
+
+    Per window (inputs up to ``window_bytes``, or one larger item): the host
+    copies the inputs into pinned staging buffers (torch runs large copies on
+    several threads), a copy stream sends them, ``launch`` runs on the current
+    stream, and a second copy stream brings the outputs back into pinned host
+    tensors.  The host stages window i+1 while the device still copies and
+    computes window i; at most ``depth`` windows are in flight, so the device
+    holds about ``depth`` windows of inputs and outputs however large the
+    state.  Both copy streams keep the default priority.  The defaults are
+    the module's ``HOST_WINDOW_BYTES`` and ``HOST_WINDOW_DEPTH``.
+    """
+    window_bytes = HOST_WINDOW_BYTES if window_bytes is None else window_bytes
+    depth = HOST_WINDOW_DEPTH if depth is None else depth
+    cur = torch.cuda.current_stream(device)
+    s_in, s_out = torch.cuda.Stream(device), torch.cuda.Stream(device)
+    inflight: list = []
+    results: dict = {}
+    for window in _windows(items, window_bytes):
+        if len(inflight) >= depth:
+            inflight.pop(0).synchronize()
+        staged = [tuple(torch.empty(t.shape, dtype=t.dtype, pin_memory=True).copy_(t) for t in it[1])
+                  for it in window]
+        with torch.cuda.stream(s_in):
+            dev_in = [tuple(p.to(device, non_blocking=True) for p in ps) for ps in staged]
+        cur.wait_stream(s_in)
+        for ts in dev_in:
+            for d in ts:
+                d.record_stream(cur)
+        outs = launch(dev_in)
+        s_out.wait_stream(cur)
+        with torch.cuda.stream(s_out):
+            for it, os_ in zip(window, outs):
+                dests = it[2] if len(it) > 2 else [None] * len(os_)
+                host = []
+                for o, h in zip(os_, dests):
+                    if h is None:
+                        h = torch.empty(o.shape, dtype=o.dtype, pin_memory=True)
+                    elif tuple(h.shape) != tuple(o.shape) or h.dtype != o.dtype:
+                        raise ValueError(f"{it[0]}: output {tuple(o.shape)} {o.dtype} does not fit "
+                                         f"its destination {tuple(h.shape)} {h.dtype}")
+                    h.copy_(o, non_blocking=True)
+                    o.record_stream(s_out)
+                    host.append(h)
+                results[it[0]] = tuple(host)
+        inflight.append(s_out.record_event())
+        del staged, dev_in, outs
+    s_out.synchronize()
+    return results
+
+
+def host_items(key, ins: tuple, outs: tuple, *, window_bytes: Optional[int] = None,
+               multiple: int = 1, out_div: Optional[tuple] = None) -> list[tuple]:
+    """The run_host_windows items for one host work item whose results go to
+    ``outs`` (pinned host tensors of the full results).
+
+    Inputs that fit a window make one item.  Larger ones are split along dim 0
+    into chunks of a multiple of ``multiple`` rows, each chunk an item that
+    writes the matching rows of ``outs``, so the device never holds more than a
+    window of any tensor.  Every input has the same dim-0 length R, rows are
+    independent, and output j has ceil(R / out_div[j]) rows (default 1: the
+    same R; 128 for the scales of 128-row tiles, with ``multiple`` 128)."""
+    window_bytes = HOST_WINDOW_BYTES if window_bytes is None else window_bytes
+    out_div = out_div or (1,) * len(outs)
+    rows = ins[0].shape[0] if ins[0].dim() else 0
+    nbytes = sum(_nbytes(t) for t in ins)
+    if nbytes <= window_bytes or rows <= multiple:
+        return [(key, ins, outs)]
+    if any(multiple % d for d in out_div):
+        raise ValueError("host_items: multiple must be a multiple of every out_div")
+    per_row = max(1, nbytes // rows)
+    step = max(multiple, (window_bytes // per_row) // multiple * multiple)
+    return [((key, r0), tuple(t[r0:r0 + step] for t in ins),
+             tuple(o[r0 // d:-(-(r0 + step) // d)] for o, d in zip(outs, out_div)))
+            for r0 in range(0, rows, step)]
+
+
+def _windows(items: Sequence[tuple], window_bytes: int):
+    """Consecutive groups of items whose inputs total at most ``window_bytes``
+    (an item larger than that is a window of its own)."""
+    cur, size = [], 0
+    for it in items:
+        n = sum(_nbytes(t) for t in it[1])
+        if cur and size + n > window_bytes:
+            yield cur
+            cur, size = [], 0
+        cur.append(it)
+        size += n
+    if cur:
+        yield cur
 
 
 def launch_chunks(items: Sequence, first: int = 8, most: int = 64):

@@ -20,7 +20,9 @@ x86 CPU:
 
 Tensors on the CPU are staged through the current HIP device and the results
 copied back, so the reference's CPU-tensor call sites keep working; there is no
-CPU compute path.
+CPU compute path.  The state-dict calls move host tensors in bounded,
+pipelined windows (``ops.run_host_windows``), so device memory stays at a few
+hundred MB whatever the size of the state.
 """
 
 from __future__ import annotations
@@ -123,51 +125,55 @@ class WeightQuantizer:
         return True
 
     def quantize_state_dict(self, state_dict: dict[str, Tensor]) -> dict[str, Tensor | Any]:
-        """Return a new dict with 2-D float weights converted to FP8 + sidecar scales (:91-115)."""
+        """Return a new dict with 2-D float weights converted to FP8 + sidecar scales (:91-115).
+
+        Device weights go through chunked grouped launches; host weights go
+        through bounded pipelined windows (``ops.run_host_windows``) and come
+        back as (pinned) CPU tensors, as the reference returns them.
+        """
         pow2 = self._config.use_weight_pow2_scale
 
-        def run(xs: list[Tensor]) -> list[tuple[Tensor, Tensor]]:
-            plan = ops.QuantPlan(xs, "fp8_block", (1, 128), use_pow2_scale=pow2,
-                                 scale_dtype=torch.bfloat16)
-            plan.run()
-            return plan.outputs
+        def quantize(xs: list[Tensor]) -> list[tuple[Tensor, Tensor]]:
+            launches = ops.ChunkedLaunches(
+                lambda ys: ops.QuantPlan(ys, "fp8_block", (1, 128), use_pow2_scale=pow2,
+                                         scale_dtype=torch.bfloat16).run())
+            done: dict[int, tuple[Tensor, Tensor]] = {}
+            for i, x in enumerate(xs):
+                if x.dtype == torch.float64:
+                    x = x.to(torch.float32)  # the reference's own upcast (:109)
+                x = x if x.is_contiguous() else x.contiguous()
+                if x.data_ptr() % 16 == 0 and x.numel() > 0:
+                    launches.add((x.dtype, x.device), i, x)
+                else:  # empty, or a view at an odd offset: a launch of its own
+                    done[i] = ops.fp8_block_quant(x, (1, 128), pow2=pow2, scale_dtype=torch.bfloat16)
+            done.update(launches.flush())
+            return [done[i] for i in range(len(xs))]
 
-        # Grouped launches per (dtype, device) for 16-byte aligned weights,
-        # issued while the rest is still being staged; anything else is
-        # quantized by a single launch.
-        host = any(isinstance(v, Tensor) and not v.is_cuda and self._eligible(v)
-                   for v in state_dict.values())
-        launches = ops.ChunkedLaunches(run, defer=host)
-        staged: dict[str, tuple[Tensor, torch.device | None]] = {}
-        results: dict[str, tuple[Tensor, Tensor]] = {}
-        for key, value in state_dict.items():
-            if not self._eligible(value):
-                continue
-            x, home = _stage(value)
-            if x.dtype == torch.float64:
-                x = x.to(torch.float32)  # the reference's own upcast (:109)
-            x = x if x.is_contiguous() else x.contiguous()
-            staged[key] = (x, home)
-            if x.data_ptr() % 16 == 0 and x.numel() > 0:
-                launches.add((x.dtype, x.device), key, x)
-            else:
-                results[key] = ops.fp8_block_quant(x, (1, 128), pow2=pow2,
-                                                   scale_dtype=torch.bfloat16)
-        results.update(launches.flush())
+        keys = [k for k, v in state_dict.items() if self._eligible(v)]
+        on_dev = [k for k in keys if state_dict[k].is_cuda]
+        on_host = [k for k in keys if not state_dict[k].is_cuda]
+        results = dict(zip(on_dev, quantize([state_dict[k] for k in on_dev])))
+        if on_host:
+            dev = ops.require_device()
+            items = []
+            for k in on_host:
+                v = state_dict[k]
+                outs = (torch.empty(v.shape, dtype=torch.float8_e4m3fn, pin_memory=True),
+                        torch.empty((v.shape[0], v.shape[1] // 128), dtype=torch.bfloat16,
+                                    pin_memory=True))
+                results[k] = outs
+                items += ops.host_items(k, (v,), outs)
+            ops.run_host_windows(items, lambda ins: quantize([x for (x,) in ins]), dev)
 
         out: dict[str, Tensor | Any] = {}
         for key, value in state_dict.items():
-            if key not in staged:
+            if key not in results:
                 out[key] = value
                 continue
-            x, home = staged[key]
             q, s = results[key]
-            out_features, in_features = x.shape
-            s = s.reshape(out_features, in_features // 128)
-            if home is not None:
-                q, s = q.to(home), s.to(home)
+            out_features, in_features = value.shape
             out[key] = q
-            out[f"{key}_fp8_scales"] = s
+            out[f"{key}_fp8_scales"] = s.reshape(out_features, in_features // 128)
             out[f"{key}_fp8_meta"] = torch.tensor(
                 [out_features, in_features], dtype=torch.int64, device="cpu"
             )
@@ -178,44 +184,57 @@ class WeightQuantizer:
 
         The (codes, scales) pairs go through grouped kernel launches (chunked as in
         quantize_state_dict) that write bf16 directly (fp32 product, then the bf16
-        cast of :133).
+        cast of :133); host pairs go through bounded pipelined windows.
         """
         consumed_suffixes = {"_fp8_scales", "_fp8_meta"}
-        pending: dict[str, tuple[Tensor, Tensor, torch.device | None]] = {}
-        results: dict[str, Tensor] = {}
-        host = any(isinstance(v, Tensor) and not v.is_cuda for v in state_dict.values())
-        launches = ops.ChunkedLaunches(
-            lambda pairs: ops.DequantPlan(pairs, (1, 128), torch.bfloat16).run(), defer=host)
+        pairs: dict[str, tuple[Tensor, Tensor]] = {}
         for key, value in state_dict.items():
             if any(key.endswith(sfx) for sfx in consumed_suffixes) or not isinstance(value, Tensor):
                 continue
             scale_key = f"{key}_fp8_scales"
-            if scale_key not in state_dict:
-                continue
-            q, home = _stage(value)
-            s = state_dict[scale_key].to(q.device)
-            if s.dtype == torch.float64:
-                s = s.to(torch.float32)
-            last = value.shape[-1]
-            leading = 1
-            for d in value.shape[:-1]:
-                leading *= int(d)
-            q, s = q.contiguous().reshape(leading, last), s.contiguous().reshape(leading, last // 128)
-            pending[key] = (q, s, home)
-            if q.numel() > 0 and q.data_ptr() % 16 == 0:
-                launches.add((s.dtype, q.device), key, (q, s))
-            else:
-                results[key] = ops.fp8_block_dequant(q, s, (1, 128), torch.bfloat16)
-        results.update(launches.flush())
+            if scale_key in state_dict:
+                pairs[key] = (value, state_dict[scale_key])
+
+        def dequant(items: list[tuple[Tensor, Tensor]]) -> list[Tensor]:
+            launches = ops.ChunkedLaunches(
+                lambda ps: ops.DequantPlan(ps, (1, 128), torch.bfloat16).run())
+            done: dict[int, Tensor] = {}
+            for i, (q, s) in enumerate(items):
+                s = s.to(q.device)
+                if s.dtype == torch.float64:
+                    s = s.to(torch.float32)
+                last = q.shape[-1]
+                leading = 1
+                for d in q.shape[:-1]:
+                    leading *= int(d)
+                qm = q.contiguous().reshape(leading, last)
+                sm = s.contiguous().reshape(leading, last // 128)
+                if qm.numel() > 0 and qm.data_ptr() % 16 == 0:
+                    launches.add((sm.dtype, qm.device), i, (qm, sm))
+                else:
+                    done[i] = ops.fp8_block_dequant(qm, sm, (1, 128), torch.bfloat16)
+            done.update(launches.flush())
+            return [done[i].reshape(q.shape) for i, (q, _) in enumerate(items)]
+
+        on_dev = [k for k, (q, _) in pairs.items() if q.is_cuda]
+        on_host = [k for k, (q, _) in pairs.items() if not q.is_cuda]
+        results = dict(zip(on_dev, dequant([pairs[k] for k in on_dev])))
+        if on_host:
+            dev = ops.require_device()
+            items = []
+            for k in on_host:
+                q, s = pairs[k]
+                last = q.shape[-1]
+                qm = q.reshape(-1, last)
+                sm = s.cpu().reshape(qm.shape[0], last // 128)
+                out = torch.empty(qm.shape, dtype=torch.bfloat16, pin_memory=True)
+                results[k] = out.view(q.shape)
+                items += ops.host_items(k, (qm, sm), (out,))
+            ops.run_host_windows(items, lambda ins: [(d,) for d in dequant(ins)], dev)
 
         out: dict[str, Tensor | Any] = {}
         for key, value in state_dict.items():
             if any(key.endswith(sfx) for sfx in consumed_suffixes):
                 continue
-            if key not in pending:
-                out[key] = value
-                continue
-            dq = results[key].reshape(value.shape)
-            home = pending[key][2]
-            out[key] = dq.to(home) if home is not None else dq
+            out[key] = results.get(key, value)
         return out

@@ -257,3 +257,67 @@ def test_state_dict_calls_spanning_several_launches():
     assert list(back) == list(rback)
     for k, rv in rback.items():
         assert np.array_equal(bits(back[k]), bits(rv)), k
+
+
+def _same(a: torch.Tensor, b: torch.Tensor) -> bool:
+    return (a.dtype == b.dtype and a.shape == b.shape
+            and torch.equal(a.contiguous().view(torch.uint8), b.contiguous().view(torch.uint8)))
+
+
+@pytest.mark.parametrize("window", [100_000, 1 << 20, 64 << 20])
+def test_host_state_dicts_in_bounded_windows(monkeypatch, window):
+    """Host-resident state dicts through the pipelined windows (many small ones
+    at 1 MiB): every output equals the reference's ops run by torch on the CPU
+    and comes back on the CPU; with small windows the device never holds the
+    whole state."""
+    from lumenrl_amd.engine.inference import DynamicWeightLoader
+    from lumenrl_amd.quantization import ops
+
+    monkeypatch.setattr(ops, "HOST_WINDOW_BYTES", window)
+    g = torch.Generator().manual_seed(11)
+    sd = {f"layers.{i}.w": (torch.randn(256 + 128 * (i % 5), 512 * (1 + i % 3), generator=g) * 0.02
+                            ).to(torch.bfloat16 if i % 4 else torch.float32) for i in range(24)}
+    sd["f64.w"] = torch.randn(128, 256, generator=g, dtype=torch.float64) * 0.02
+    sd["empty.w"] = torch.empty(0, 128)
+    sd["norm"] = torch.ones(512)
+    sd["view.w"] = torch.randn(64, 384, generator=g)[:, 128:]  # non-contiguous host view
+    sd["big.w"] = torch.randn(2048, 1024, generator=g).to(torch.bfloat16)  # split into row chunks
+    wq = WeightQuantizer(FP8Config())
+    torch.cuda.synchronize()
+    torch.cuda.reset_peak_memory_stats()
+    base = torch.cuda.memory_allocated()
+    out = wq.quantize_state_dict(sd)
+    peak = torch.cuda.max_memory_allocated() - base
+    total = sum(t.numel() * t.element_size() for t in sd.values())
+    if window < total // 8:
+        assert peak < total // 2, (peak, total)
+    ref = T.quantize_state_dict(sd)
+    assert list(out) == list(ref)
+    for k, v in ref.items():
+        assert out[k].device.type == "cpu", k
+        assert _same(out[k], v), k
+    back = wq.dequantize_state_dict(out)
+    want = T.dequantize_state_dict(ref)
+    assert list(back) == list(want)
+    for k, v in want.items():
+        assert back[k].device.type == "cpu" and _same(back[k], v), k
+
+    class Eng:
+        def update_weights(self, s):
+            self.sd = s
+
+    eng = Eng()
+    DynamicWeightLoader.load_weights(eng, sd, fp8_config={"enabled": True})
+    for k, v in sd.items():
+        q = eng.sd[k]
+        assert q.device.type == "cpu", k
+        assert _same(q, v.to(torch.float8_e4m3fn)), k
+    # the scaled extension (128x128 tiles, row chunks of whole tile rows; 3-D by experts)
+    sd3 = {"layers.0.mlp.experts.w": (torch.randn(6, 256, 384, generator=g) * 0.02).to(torch.bfloat16),
+           "layers.0.q_proj.w": sd["big.w"], "norm": sd["norm"]}
+    DynamicWeightLoader.load_weights(eng, sd3, fp8_config={"enabled": True, "scaled": True})
+    for k in ("layers.0.mlp.experts.w", "layers.0.q_proj.w"):
+        q, s = T.quantize_tensor_tiles(sd3[k].float(), (128, 128))
+        assert eng.sd[k].device.type == "cpu"
+        assert _same(eng.sd[k], q) and _same(eng.sd[k + "_scale_inv"], s), k
+    assert eng.sd["norm"] is sd["norm"]

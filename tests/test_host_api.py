@@ -229,20 +229,19 @@ def test_launch_chunks_cover_every_item_once_in_order(n):
 from lumenrl_amd.quantization.ops import ChunkedLaunches  # noqa: E402
 
 
-@pytest.mark.parametrize("defer", [False, True])
-def test_chunked_launches_schedule_and_results(defer):
-    """Groups launch 8, 16, 32, then 64 items each (eagerly, or all at flush when
-    deferred); results map every name to its own output; groups never mix."""
+def test_chunked_launches_schedule_and_results():
+    """Groups launch 8, 16, 32, then 64 items each, as soon as a chunk is full;
+    results map every name to its own output; groups never mix."""
     calls = []
 
     def run(items):
         calls.append(list(items))
         return [x * 10 for x in items]
 
-    cl = ChunkedLaunches(run, defer=defer)
+    cl = ChunkedLaunches(run)
     for i in range(150):
         cl.add("a" if i % 3 else "b", f"n{i}", i)
-        if not defer and i == 30:
+        if i == 30:
             assert [len(c) for c in calls] == [8, 8]  # a: 8 of 20 so far; b: 8 of 11
     res = cl.flush()
     assert res == {f"n{i}": i * 10 for i in range(150)}
@@ -250,3 +249,48 @@ def test_chunked_launches_schedule_and_results(defer):
     b_sizes = [len(c) for c in calls if c[0] % 3 == 0]
     assert a_sizes == [8, 16, 32, 44] and b_sizes == [8, 16, 26]
     assert all(len({x % 3 == 0 for x in c}) == 1 for c in calls)
+
+
+def test_host_windows_split_in_order_and_keep_big_items_whole():
+    from lumenrl_amd.quantization.ops import _windows
+
+    t = {n: torch.empty(n, dtype=torch.uint8) for n in (10, 30, 60, 100, 5, 5)}
+    items = [(f"k{i}", (t[n],)) for i, n in enumerate([30, 60, 10, 100, 5, 5, 60, 30])]
+    wins = [[k for k, _ in w] for w in _windows(items, 100)]
+    assert wins == [["k0", "k1", "k2"], ["k3"], ["k4", "k5", "k6", "k7"]]
+    assert [k for w in wins for k in w] == [k for k, _ in items]
+    # an item larger than the window is a window of its own
+    big = [("a", (t[5],)), ("b", (torch.empty(500, dtype=torch.uint8),)), ("c", (t[5],))]
+    assert [[k for k, _ in w] for w in _windows(big, 100)] == [["a"], ["b"], ["c"]]
+    # several inputs per item count together
+    pairs = [("p", (t[60], t[30])), ("q", (t[10], t[5]))]
+    assert [[k for k, _ in w] for w in _windows(pairs, 100)] == [["p"], ["q"]]
+
+
+def test_host_items_split_rows_and_map_outputs():
+    from lumenrl_amd.quantization.ops import host_items
+
+    x = torch.zeros(1000, 64, dtype=torch.bfloat16)          # 128,000 bytes
+    codes = torch.zeros(1000, 64, dtype=torch.uint8)
+    sc = torch.zeros(1000, 1, dtype=torch.bfloat16)
+    whole = host_items("w", (x,), (codes, sc), window_bytes=1 << 20)
+    assert len(whole) == 1 and whole[0][0] == "w" and whole[0][2][0] is codes
+    parts = host_items("w", (x,), (codes, sc), window_bytes=16_000)  # 125 rows per window
+    assert [k for k, _, _ in parts] == [("w", r) for r in range(0, 1000, 125)]
+    for (_, r0), ins, outs in parts:
+        n = ins[0].shape[0]
+        assert n == min(125, 1000 - r0)
+        assert ins[0].data_ptr() == x[r0].data_ptr()
+        assert outs[0].data_ptr() == codes[r0].data_ptr() and outs[0].shape[0] == n
+        assert outs[1].data_ptr() == sc[r0].data_ptr() and outs[1].shape[0] == n
+    # 128-row tiles: chunks of whole tile rows; scales have ceil(rows / 128) rows
+    t = torch.zeros(1000, 256, dtype=torch.bfloat16)          # 512 bytes per row
+    tc = torch.zeros(1000, 256, dtype=torch.uint8)
+    ts = torch.zeros(8, 2, dtype=torch.float32)
+    parts = host_items("t", (t,), (tc, ts), window_bytes=300 * 512, multiple=128, out_div=(1, 128))
+    assert [k[1] for k, _, _ in parts] == [0, 256, 512, 768]
+    assert [o[1].shape[0] for _, _, o in parts] == [2, 2, 2, 2]
+    assert [i[0].shape[0] for _, i, _ in parts] == [256, 256, 256, 232]
+    assert parts[-1][2][1].data_ptr() == ts[6].data_ptr()
+    with pytest.raises(ValueError):
+        host_items("t", (t,), (tc, ts), window_bytes=300 * 512, multiple=100, out_div=(1, 128))
