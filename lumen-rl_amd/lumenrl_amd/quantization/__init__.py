@@ -1,6 +1,6 @@
 """Weight quantization for trainer -> rollout weight sync (lumenrl/quantization mirror)."""
 
-from lumenrl_amd.quantization.bucket import QuantizedBucketWriter
+from lumenrl_amd.quantization.bucket import QuantizedBucketWriter, encode_bucket
 from lumenrl_amd.quantization.fp8_config import (
     FP8Config,
     QuantizationConfig,
@@ -30,6 +30,7 @@ __all__ = [
     "QuantizationConfig",
     "QuantPlan",
     "QuantizedBucketWriter",
+    "encode_bucket",
     "RolloutQuantConfig",
     "TensorScalePlan",
     "TrainingQuantConfig",

@@ -23,6 +23,7 @@ vLLM/ATOM FP8 loader takes.
 
 from __future__ import annotations
 
+import json
 from typing import Callable, Iterator, Optional, Sequence
 
 import torch
@@ -264,6 +265,44 @@ class QuantizedBucketWriter:
 
     def __len__(self) -> int:
         return len(self.buckets)
+
+
+def encode_bucket(weights: Sequence[tuple[str, Tensor]], *, fmt: str = "fp8_block",
+                  block_size: tuple[int, int] = (128, 128),
+                  quantize_if: Callable[[str, Tensor], bool] = default_quantize_if,
+                  scale_suffix: str = "_scale_inv") -> tuple[Tensor, Tensor]:
+    """The RCCL sender's ``_encode_bucket`` (rdma_weight_transfer.py:22-57) with the
+    quantization fused into the payload fill.
+
+    Returns ``(metadata, payload)`` as the reference does: ``metadata`` is the
+    compact JSON of the entries ``{name, shape, dtype, offset, nbytes}`` as a
+    uint8 device tensor, ``payload`` the uint8 device bytes the entries point
+    into.  Weights ``quantize_if`` accepts arrive as codes plus
+    ``<name><scale_suffix>`` scales, written by one grouped launch per dtype;
+    the rest are copied unchanged.  Entries start on 256-byte boundaries (the
+    receiver reads offsets from the metadata, rdma_weight_transfer.py:176-180).
+    CPU tensors are moved to the current HIP device first, as the reference
+    does.  For a sync that repeats over the same weights, plan once with
+    ``QuantizedBucketWriter`` instead (this builds the plan on every call).
+    """
+    if not weights:
+        raise ValueError("cannot encode an empty weight bucket")
+    prepared = []
+    for name, tensor in weights:
+        value = tensor.detach()
+        if not value.is_cuda:
+            value = value.to(ops.require_device(), non_blocking=True)
+        prepared.append((name, value.contiguous()))
+    layouts = plan_layout([(n, tuple(v.shape), v.dtype, bool(quantize_if(n, v))) for n, v in prepared],
+                          1 << 62, fmt, block_size, scale_suffix)
+    writer = QuantizedBucketWriter(prepared, bucket_bytes=max(layouts[0].nbytes, 1), fmt=fmt,
+                                   block_size=block_size, quantize_if=quantize_if,
+                                   scale_suffix=scale_suffix)
+    bucket = writer.buckets[0].fill()
+    raw = json.dumps(bucket.rdma_entries(), separators=(",", ":")).encode("utf-8")
+    device = bucket.buffer.device
+    metadata = torch.tensor(list(raw), dtype=torch.uint8, device=device)
+    return metadata, bucket.buffer[:bucket.nbytes]
 
 
 def _align(n: int) -> int:

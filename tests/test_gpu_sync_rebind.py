@@ -19,7 +19,7 @@ import pytest
 import torch
 
 from oracle import oracle as O
-from lumenrl_amd.quantization import QuantizedBucketWriter, ops
+from lumenrl_amd.quantization import QuantizedBucketWriter, encode_bucket, ops
 
 pytestmark = pytest.mark.gpu
 
@@ -176,3 +176,42 @@ def test_mixed_dtype_bucket_decoded_like_the_reference_receivers():
         writer.rebind([("lm_head.weight", weight((512, 128)))])
     with pytest.raises(KeyError):
         writer.rebind([("nope", weight((512, 128)))])
+
+
+def test_encode_bucket_like_the_rccl_sender():
+    """encode_bucket mirrors _encode_bucket (rdma_weight_transfer.py:22-57): compact
+    JSON metadata as a uint8 device tensor, and a payload the receiver decodes with
+    its own expressions (rdma_weight_transfer.py:170-180) -- here with FP8 codes and
+    scales for the linear weights and the rest unchanged, CPU inputs included."""
+    named = [("model.embed_tokens.weight", weight((256, 256))),
+             ("model.layers.0.self_attn.o_proj.weight", weight((384, 512))),
+             ("model.layers.0.post_attention_layernorm.weight", torch.ones(512, dtype=torch.bfloat16)),
+             ("model.layers.0.mlp.experts.w2", weight((2, 256, 128)).cpu()),
+             ("model.layers.0.mlp.gate.weight", weight((64, 256), torch.float32))]
+    metadata, payload = encode_bucket(named)
+    torch.cuda.synchronize()
+    assert metadata.dtype == torch.uint8 and metadata.is_cuda and payload.dtype == torch.uint8
+    entries = json.loads(bytes(metadata.cpu().tolist()).decode("utf-8"))
+    raw = json.dumps(entries, separators=(",", ":")).encode("utf-8")
+    assert bytes(metadata.cpu().tolist()) == raw
+    src = {n: w.to(DEV) for n, w in named}
+    seen = set()
+    for entry in entries:
+        dtype = getattr(torch, entry["dtype"])
+        start = int(entry["offset"])
+        end = start + int(entry["nbytes"])
+        value = payload[start:end].view(dtype).view(entry["shape"])
+        name = entry["name"]
+        seen.add(name)
+        base = name[: -len("_scale_inv")] if name.endswith("_scale_inv") else name
+        w = src[base]
+        if name == base and value.dtype == w.dtype:
+            assert torch.equal(value, w), name
+            continue
+        oc, osc = oracle_tiles(w)
+        got = value.view(torch.uint8) if name == base else value
+        want = oc if name == base else osc
+        assert np.array_equal(got.cpu().numpy().reshape(-1).view(np.uint8 if name == base else np.uint32), want), name
+    assert seen == set(src) | {n + "_scale_inv" for n in src if "proj" in n or "experts" in n or "gate" in n}
+    with pytest.raises(ValueError, match="empty weight bucket"):
+        encode_bucket([])
