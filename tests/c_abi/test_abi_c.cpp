@@ -23,6 +23,9 @@ int lrqo_mx_quant(const void* in, int in_dtype, int64_t rows, int64_t cols, int6
 int lrqo_act_qdq(const void* in, int in_dtype, int64_t rows, int64_t cols, int64_t blk, int pow2,
                  float* out, int nthreads);
 uint32_t lrqo_tensor_scale(const void* in, int in_dtype, int64_t n);
+int lrqo_fp8_block_quant_f64(const double* in, int64_t batch, int64_t rows, int64_t cols,
+                             int64_t ld, int64_t bstride, int64_t blk_r, int64_t blk_c,
+                             int pow2, uint8_t* codes, double* scales, int nthreads);
 void lrqo_f32_to_e4m3_n(const float* in, uint8_t* out, int64_t n);
 }
 
@@ -204,9 +207,57 @@ int main() {
     const bool ok = got[0] == lrqo_tensor_scale(hw[0].data(), LRQ_DTYPE_BF16, R[0] * C[0]) &&
                     got[1] == lrqo_tensor_scale(hw[1].data(), LRQ_DTYPE_BF16, R[1] * C[1]);
     expect(ok, "lrq_tensor_scale_grouped");
+    // the same tables through the entry point that allocates nothing: the library's
+    // static workspace instead of dws, twice (the second call reuses its contents)
+    for (int rep = 0; rep < 2; ++rep) {
+      HIP(hipMemset(dsc, 0xFF, 2 * sizeof(float)));
+      LRQ(lrq_tensor_scale_grouped_static(ht.data(), dt, (lrq_stream_t)st));
+      HIP(hipStreamSynchronize(st));
+      uint32_t got2[2];
+      HIP(hipMemcpy(got2, dsc, sizeof(got2), hipMemcpyDeviceToHost));
+      expect(got2[0] == got[0] && got2[1] == got[1], "lrq_tensor_scale_grouped_static");
+    }
     HIP(hipFree(dws));
     HIP(hipFree(dt));
     HIP(hipFree(dsc));
+  }
+
+  // 5b. float64 input in float64 arithmetic (quantize_tensor on a float64 tensor):
+  //     tensor 0's values scaled off the bf16 grid, 1x128 blocks, float64 scales
+  {
+    const int64_t n = R[0] * C[0];
+    std::vector<double> hx((size_t)n);
+    for (int64_t i = 0; i < n; ++i) {
+      uint32_t b = (uint32_t)hw[0][(size_t)i] << 16;
+      float f;
+      memcpy(&f, &b, 4);
+      hx[(size_t)i] = (double)f * (1.0 + 1e-9 * (double)(i % 7));
+    }
+    for (int pow2 = 0; pow2 < 2; ++pow2) {
+      double* dx;
+      uint8_t* dq;
+      double* ds;
+      const int64_t ns = R[0] * (C[0] / 128);
+      HIP(hipMalloc(&dx, (size_t)n * 8));
+      HIP(hipMalloc(&dq, (size_t)n));
+      HIP(hipMalloc(&ds, (size_t)ns * 8));
+      HIP(hipMemcpy(dx, hx.data(), (size_t)n * 8, hipMemcpyHostToDevice));
+      const unsigned flags = LRQ_FLAG_NATIVE_ARITH | (pow2 ? LRQ_FLAG_POW2_SCALE : 0u);
+      LRQ(lrq_fp8_block_quant(dx, LRQ_DTYPE_F64, 1, R[0], C[0], C[0], R[0] * C[0], 1, 128, dq, ds, flags,
+                              (lrq_stream_t)st));
+      HIP(hipStreamSynchronize(st));
+      std::vector<uint8_t> gq((size_t)n), wq((size_t)n);
+      std::vector<double> gs((size_t)ns), wsc((size_t)ns);
+      HIP(hipMemcpy(gq.data(), dq, (size_t)n, hipMemcpyDeviceToHost));
+      HIP(hipMemcpy(gs.data(), ds, (size_t)ns * 8, hipMemcpyDeviceToHost));
+      lrqo_fp8_block_quant_f64(hx.data(), 1, R[0], C[0], C[0], R[0] * C[0], 1, 128, pow2, wq.data(),
+                               wsc.data(), 0);
+      expect(memcmp(gq.data(), wq.data(), (size_t)n) == 0 && memcmp(gs.data(), wsc.data(), (size_t)ns * 8) == 0,
+             pow2 ? "lrq_fp8_block_quant float64, pow2" : "lrq_fp8_block_quant float64");
+      HIP(hipFree(ds));
+      HIP(hipFree(dq));
+      HIP(hipFree(dx));
+    }
   }
 
   // 6. unscaled e4m3 cast of tensor 1 (x 300, so values pass 448 -> NaN) and of an
