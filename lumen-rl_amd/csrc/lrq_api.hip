@@ -110,7 +110,12 @@ bool fold_batch(Desc& d) {
 }
 
 int fp8_kernel_for(const Desc& d, int in_dtype, int64_t blk_r, int64_t blk_c) {
-  if (in_dtype == lrq::kF64) return lrq::kKernF64;
+  if (in_dtype == lrq::kF64) {
+    const bool row = blk_r == 1 && pow2_block(blk_c) && d.cols % blk_c == 0 && d.ld == d.cols &&
+                     (d.batch == 1 || d.bstride == d.rows * d.ld) && aligned(d.in, 16) &&
+                     aligned(d.codes, 2) && aligned(d.scales, 8);
+    return row ? lrq::kKernF64Row : lrq::kKernF64;
+  }
   const int64_t es = esize(in_dtype);
   const bool vec = aligned(d.in, 16) && (d.ld * es) % 16 == 0 &&
                    (d.batch == 1 || (d.bstride * es) % 16 == 0) && aligned(d.codes, 8) &&
@@ -151,6 +156,12 @@ bool plan_units(const LaunchCfg& cfg, Desc& d) {
       d.units_c = (d.cols + cfg.blk_c - 1) / cfg.blk_c;
       d.units = d.batch * d.units_r * d.units_c;
       return true;
+    case kKernF64Row: {  // 4 waves x kF64RowInstr instructions of 128 doubles
+      if (!fold_batch(d)) return false;
+      const int64_t per_wg = 4 * kF64RowInstr * 128;
+      d.units = (d.batch * d.rows * d.cols + per_wg - 1) / per_wg;
+      return true;
+    }
     case kKernF64:  // one wave per block, four per work-group
       d.units_r = (d.rows + cfg.blk_r - 1) / cfg.blk_r;
       d.units_c = (d.cols + cfg.blk_c - 1) / cfg.blk_c;
@@ -202,7 +213,8 @@ hipError_t launch(const LaunchCfg& cfg, const Desc& single, const Desc* descs_de
     return launch_mx(cfg, single, descs_dev, map_dev, total_units, stream);
   if (cfg.kernel == kKernDequant || cfg.kernel == kKernGenericDequant)
     return launch_dequant(cfg, single, descs_dev, map_dev, total_units, stream);
-  if (cfg.kernel == kKernF64) return launch_f64(cfg, single, descs_dev, map_dev, total_units, stream);
+  if (cfg.kernel == kKernF64 || cfg.kernel == kKernF64Row)
+    return launch_f64(cfg, single, descs_dev, map_dev, total_units, stream);
   return launch_fp8(cfg, single, descs_dev, map_dev, total_units, stream);
 }
 

@@ -38,6 +38,7 @@ enum Kernel : int {
   kKernCast = 9,           // grouped unscaled cast to float8_e4m3fn
   kKernMxDequant = 10,     // MXFP8 / MXFP4 dequant, 8 (bf16 out) or 4 (fp32) elements per lane-chunk
   kKernF64 = 11,           // FP8 blocks of a float64 tensor in float64 arithmetic, one wave per block
+  kKernF64Row = 12,        // dense 1xB float64 blocks (B = 32..512), 16-byte loads
 };
 
 // Work per lane of the streaming kernels, shared by the kernels and the
@@ -55,6 +56,7 @@ constexpr int64_t kXcdRunStream = 32;  // dequant, act, amax, copy, cast, generi
 constexpr int kCastLaneElems = 16;   // k_cast_e4m3: elements per lane
 constexpr int64_t kCastUnit = 256 * kCastLaneElems;  // k_cast_e4m3: elements per work-group
 constexpr int kAmaxLoads = 2;        // k_amax: 16-byte loads per lane (2 beat 1, 3, 4 and 8)
+constexpr int kF64RowInstr = 4;      // k_row_f64: 1 KiB wave instructions per wave (128 doubles each)
 
 // Descriptor and local work unit of this work-group: the single-tensor
 // descriptor (kernel argument) or, for a grouped launch, the one the device

@@ -66,15 +66,15 @@ def check(xd: torch.Tensor, blk, pow2):
 
 
 @pytest.mark.parametrize("pow2", [False, True])
-@pytest.mark.parametrize("blk", [(1, 128), (1, 32), (1, 96), (1, 384), (128, 128), (3, 40), (64, 96)])
+@pytest.mark.parametrize("blk", [(1, 128), (1, 32), (1, 64), (1, 256), (1, 512), (1, 96), (1, 384), (128, 128), (3, 40), (64, 96)])
 @pytest.mark.parametrize("data", ["weights", "edge"])
 def test_f64_blocks_vs_oracle(data, blk, pow2):
     say("f64", data, blk, pow2)
     if data == "weights":
-        x = RNG.normal(0, 0.02, (200, 384))
+        x = RNG.normal(0, 0.02, (200, 512) if blk[1] == 512 else (200, 384))
         x.flat[RNG.integers(0, x.size, 80)] *= 150
     else:
-        x = edge64()
+        x = edge64(cols=512 if blk[1] == 512 else 384)
     check(torch.from_numpy(x).to(DEV), blk, pow2)
 
 
@@ -139,3 +139,56 @@ def test_f64_full_4096x4096_vs_oracle():
     oc, osc = O.fp8_block_quant(x, "f64", "native", (1, 128), False, nthreads=16)
     assert np.array_equal(s.cpu().numpy().view(np.uint64).reshape(-1), osc.view(np.uint64).reshape(-1))
     assert np.array_equal(c.view(torch.uint8).cpu().numpy(), oc[0])
+
+
+def _e4m3_values() -> np.ndarray:
+    """All positive finite float8_e4m3fn values, ascending."""
+    codes = torch.arange(0, 0x7F, dtype=torch.uint8).view(torch.float8_e4m3fn)
+    return codes.float().numpy().astype(np.float64)
+
+
+def _division_regimes(n_blocks: int, rng) -> dict:
+    """float64 [n_blocks, 128] inputs whose quotients x/s stress the per-element division."""
+    out = {}
+    # (a) block amax anywhere in float64's range, elements 2^U(-80, 0) below it
+    amax = 2.0 ** rng.uniform(-1000, 1000, (n_blocks, 1))
+    x = amax * 2.0 ** rng.uniform(-80, 0, (n_blocks, 128)) * rng.choice([-1.0, 1.0], (n_blocks, 128))
+    x[:, 0] = amax[:, 0]
+    out["wide"] = x
+    # (b) quotients planted on e4m3 ties and float32 rounding boundaries, then nudged
+    v = _e4m3_values()
+    ties = (v[:-1] + v[1:]) / 2
+    s = 2.0 ** rng.uniform(-300, 300, (n_blocks, 1)) * rng.uniform(1, 2, (n_blocks, 1))
+    t = rng.choice(np.concatenate([ties, v]), (n_blocks, 128))
+    f32_half_ulp = np.ldexp(1.0, np.frexp(t)[1] - 25)
+    nudge = rng.choice([-2, -1, 0, 1, 2], (n_blocks, 128)) * rng.choice([1e-16, 1e-12, 1.0], (n_blocks, 128))
+    t = t + nudge * np.where(nudge == 0, 0, f32_half_ulp) * rng.uniform(0.5, 1.5, (n_blocks, 128))
+    x = t * s * rng.choice([-1.0, 1.0], (n_blocks, 128))
+    x[:, 0] = 448.0 * s[:, 0]
+    out["ties"] = x
+    # (c) tiny elements: near float64's underflow, subnormal, signed zeros, in blocks of any amax
+    amax = 2.0 ** rng.uniform(-1000, 1000, (n_blocks, 1))
+    x = 2.0 ** rng.uniform(-1074, -900, (n_blocks, 128)) * rng.choice([-1.0, 1.0], (n_blocks, 128))
+    x[:, 1::9] = rng.choice([0.0, -0.0], x[:, 1::9].shape)
+    x[:, 0] = amax[:, 0]
+    out["tiny"] = x
+    return out
+
+
+@pytest.mark.parametrize("pow2", [False, True])
+def test_f64_row_kernel_division_sweep_vs_oracle(pow2):
+    """The 1x128 float64 kernel (Markstein's correction per element, IEEE division
+    near underflow) against the oracle's IEEE division, bit for bit, on 3 x 64 K
+    blocks of adversarial quotients."""
+    rng = np.random.default_rng(1717 + int(pow2))
+    for name, x in _division_regimes(1 << 16, rng).items():
+        say("f64 division sweep", name, pow2)
+        xd = torch.from_numpy(x).to(DEV)
+        c, s = ops.fp8_block_quant(xd, (1, 128), native_arith=True, pow2=pow2)
+        torch.cuda.synchronize()
+        oc, osc = O.fp8_block_quant(x, "f64", "native", (1, 128), pow2, nthreads=16)
+        got_s = s.cpu().numpy().view(np.uint64).reshape(-1)
+        assert np.array_equal(got_s, osc.view(np.uint64).reshape(-1)), name
+        got_c = c.view(torch.uint8).cpu().numpy()
+        bad = np.flatnonzero(got_c.reshape(-1) != oc.reshape(-1))
+        assert bad.size == 0, (name, bad[:8], x.reshape(-1)[bad[:8]])
