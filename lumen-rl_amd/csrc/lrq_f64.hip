@@ -8,11 +8,12 @@
 // (f64 -> f32 -> e4m3) that this kernel keeps.  Scales are written as float64.
 //
 // k_row_f64 takes dense 1xB blocks (B = 32...512, the reference's layout) with
-// 16-byte loads; k_f64 takes every other shape, one wave per block (any block
-// shape), four blocks per 256-thread work-group, re-reading the block from L2
-// for the encode.  Both use the IEEE float64 division per element and the
-// software e4m3 encoder: float64 weights are a rare input, and exactness comes
-// first.
+// 16-byte loads.  Its quotients of finite blocks use one correctly rounded 1/s
+// per block and Markstein's correction per element (the IEEE division near
+// underflow) and the hardware e4m3 encoder.  k_f64 takes every other shape,
+// one wave per block (any block shape), four blocks per 256-thread work-group,
+// re-reading the block from L2 for the encode, with the IEEE float64 division
+// and the software encoder.
 #include "lrq_device.hpp"
 #include "lrq_internal.hpp"
 

@@ -669,7 +669,7 @@ class QuantPlan:
         self._launch = launch
         self._views = views
         self.inputs = tensors
-        self._sig = [(t.data_ptr(), t.stride()) for t in tensors]
+        self._sig = [(t.data_ptr(), t.stride(), tuple(t.shape)) for t in tensors]
         self.units = launch.units
 
     def run(self, inputs: Optional[Sequence[Tensor]] = None) -> list[tuple[Tensor, Tensor]]:
@@ -703,8 +703,10 @@ class QuantPlan:
         return self.outputs
 
     def _moved(self, tensors: Sequence[Tensor]) -> bool:
-        """True if any tensor's storage address or strides differ from the table's."""
-        return any(t.data_ptr() != p or t.stride() != st for t, (p, st) in zip(tensors, self._sig))
+        """True if any tensor's storage address, strides or shape differ from the
+        table's (a shape change then raises in ``run``)."""
+        return any(t.data_ptr() != p or t.stride() != st or tuple(t.shape) != sh
+                   for t, (p, st, sh) in zip(tensors, self._sig))
 
 
 class DequantPlan:

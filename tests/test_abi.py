@@ -398,12 +398,20 @@ def test_float64_input_needs_float64_arithmetic_and_the_fp8_block_format():
     rc = L().lrq_fp8_block_quant(odd, _lib.DTYPE_F64, 1, 4, 128, 128, 512, 1, 128, fake, fake,
                                  _lib.FLAG_NATIVE_ARITH, None)
     assert rc == _lib.ERR_ALIGN
-    # a table packs (host memory only) with the float64 kernel's one-wave-per-block geometry
-    t = (_lib.LrqTensor * 1)()
-    t[0].in_, t[0].codes, t[0].scales = 0x10000, 0x20000, 0x30000
-    t[0].batch, t[0].rows, t[0].cols, t[0].ld, t[0].batch_stride = 1, 5, 256, 256, 1280
-    need = L().lrq_group_table_bytes(_lib.FMT_FP8_BLOCK, t, 1, _lib.DTYPE_F64, 1, 128, _lib.FLAG_NATIVE_ARITH)
-    host = (ctypes.c_uint8 * need)()
-    assert L().lrq_group_pack(_lib.FMT_FP8_BLOCK, t, 1, _lib.DTYPE_F64, 1, 128, _lib.FLAG_NATIVE_ARITH,
-                              host, need) == 0
-    assert L().lrq_group_units(host) == (5 * 2 + 3) // 4
+    # tables pack (host memory only) with each float64 kernel's geometry: a dense
+    # 1x128 tensor takes the row kernel (2048 doubles per work-group), a padded
+    # row pitch the generic kernel (one wave per block, four per work-group)
+    def units(rows, cols, ld):
+        t = (_lib.LrqTensor * 1)()
+        t[0].in_, t[0].codes, t[0].scales = 0x10000, 0x20000, 0x30000
+        t[0].batch, t[0].rows, t[0].cols, t[0].ld, t[0].batch_stride = 1, rows, cols, ld, rows * ld
+        need = L().lrq_group_table_bytes(_lib.FMT_FP8_BLOCK, t, 1, _lib.DTYPE_F64, 1, 128,
+                                         _lib.FLAG_NATIVE_ARITH)
+        host = (ctypes.c_uint8 * need)()
+        assert L().lrq_group_pack(_lib.FMT_FP8_BLOCK, t, 1, _lib.DTYPE_F64, 1, 128,
+                                  _lib.FLAG_NATIVE_ARITH, host, need) == 0
+        return L().lrq_group_units(host)
+
+    assert units(5, 256, 256) == 1
+    assert units(40, 256, 256) == 5
+    assert units(5, 256, 384) == (5 * 2 + 3) // 4

@@ -96,6 +96,20 @@ def test_plan_follows_moved_storage_and_new_inputs():
         plan.run()
 
 
+def test_plan_refuses_an_input_resized_in_place():
+    """A shrink by ``resize_`` keeps the storage address and strides; the plan
+    must still notice that the planned shape is gone."""
+    w = weight((3, 128, 256))
+    plan = ops.QuantPlan([w], "fp8_block", (128, 128))
+    plan.run()
+    assert_plan_matches(plan, [w])
+    ptr = w.data_ptr()
+    w.resize_(2, 128, 256)
+    assert w.data_ptr() == ptr
+    with pytest.raises(ValueError, match="build a new plan"):
+        plan.run()
+
+
 def decode_zmq(bucket):
     """BucketedWeightReceiver's decode of one bucket (bucketed_weight_transfer.py:262-270)."""
     weights = []
