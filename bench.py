@@ -69,10 +69,11 @@ PROFILE_FOR = {"c1": "k_tile128_single_4096x4096_c1", "c2": "k_tile128_qwen3_8b_
                "act": "k_act_qdq_qwen3_8b_prefill_8192", "kv": "k_amax_qwen3_8b_qkv_scales",
                "cast": "k_cast_e4m3_qwen3_8b_state_dynamic_weight_loader",
                "c4d": "k_mx_dequant_qwen3_8b_mxfp8_to_bf16", "c2sd": "k_row_qwen3_8b_state_dict_dropin",
-               "rollout": "k_row_qwen3_8b_rollout_quantize_model"}
+               "rollout": "k_row_qwen3_8b_rollout_quantize_model",
+               "f64": "k_row_f64_qwen3_8b_4_layers_quantize_tensor"}
 KERNEL_FOR = {"c1": "k_tile128", "c2": "k_tile128", "c3": "k_tile128", "c4": "k_mx", "c5": "k_mx",
               "c2r": "k_row", "c2d": "k_dequant", "act": "k_act_qdq8", "kv": "k_amax", "c2sd": "k_row", "bucket": "k_tile128",
-              "cast": "k_cast_e4m3", "c4d": "k_mx_dequant", "rollout": "k_row"}
+              "cast": "k_cast_e4m3", "c4d": "k_mx_dequant", "rollout": "k_row", "f64": "k_row_f64"}
 PREFILL_TOKENS = 8192
 
 
@@ -195,9 +196,11 @@ def cpu_baseline(torch, ws, fmt, fmt_block, seconds, full_bytes=None):
             legs[nt] = (len(sample), nbytes, sorted(times)[1])
     finally:
         torch.set_num_threads(prev)
+    f64 = not isinstance(ws[0], (tuple, list)) and ws[0].dtype == torch.float64
     what = {
         "fp8_block": (f"oracle/torch_ref.py (weight_quantizer.py op order on "
-                      f"{fmt_block[0]}x{fmt_block[1]} blocks, fp32 upcast first)"),
+                      f"{fmt_block[0]}x{fmt_block[1]} blocks, "
+                      + ("float64 arithmetic, no upcast)" if f64 else "fp32 upcast first)")),
         "fp8_dequant": "oracle/torch_ref.py (weight_quantizer.py:79-89 then the bf16 cast of :133)",
         "act": "oracle/torch_ref.py (fp8_rollout.py:53-72 op order)",
         "kv": "oracle/torch_ref.py (fp8_kv_cache.py:52-54 op order, one tensor at a time)",
@@ -295,10 +298,11 @@ def _cpu_pass(torch, O, torch_ref, np, ws, fmt, fmt_block, threads):
             t0 = time.perf_counter()
             if fmt_block == (128, 128):
                 q, s = torch_ref.quantize_tensor_tiles(x.float(), (128, 128))
-            else:
-                q, s = torch_ref.quantize_tensor(x.float(), fmt_block[1])
+            else:  # float64 weights keep float64 arithmetic (weight_quantizer.py:40-77)
+                q, s = torch_ref.quantize_tensor(x if x.dtype == torch.float64 else x.float(),
+                                                 fmt_block[1])
             t_total += time.perf_counter() - t0
-            done_bytes += x.numel() * 2 + q.numel() + s.numel() * 4
+            done_bytes += x.numel() * x.element_size() + q.numel() + s.numel() * s.element_size()
         else:
             xb = x.view(torch.int16).numpy().view(np.uint16)
             t0 = time.perf_counter()
@@ -385,6 +389,23 @@ class _RolloutCall:
         self.rq.restore_model(self.model)
 
 
+class _F64Calls:
+    """WeightQuantizer.quantize_tensor on each float64 weight, one call per
+    tensor as the reference's callers make them: float64 arithmetic, float64
+    scales, new outputs per call.  One event pair brackets all the calls of a
+    step (the host enqueues them ahead of the device)."""
+
+    def __init__(self, torch, ws):
+        from lumenrl_amd.quantization import FP8Config, WeightQuantizer
+
+        self.wq, self.ws = WeightQuantizer(FP8Config()), ws
+        n = sum(w.numel() for w in ws)
+        self.algorithmic_bytes = n * 8 + n + (n // 128) * 8
+
+    def run(self):
+        self.out = [self.wq.quantize_tensor(w) for w in self.ws]
+
+
 class _ActLayer:
     """The activation fake-quant of one layer's linear inputs: one launch per
     input, back to back, each into a preallocated float32 output.  Timed as one
@@ -450,6 +471,15 @@ def run(args):
         cpu_ws, cpu_blk, cpu_fmt = ws, blk, fmt
         extra = {"tensors": len(ws), "layers": 36, "elements": sum(w.numel() for w in ws),
                  "format": fmt, "launches_per_step": 1}
+    elif cfg == "f64":
+        ws, _ = qwen3_8b_set(torch, dev, args.seed, "normal", layers=4)
+        ws = [w.double() for w in ws]  # bf16 values widened exactly
+        torch.cuda.synchronize()
+        plans = [_F64Calls(torch, ws)]
+        workload = "qwen3-8b-4-layers-float64-quantize-tensor-1x128"
+        cpu_ws, cpu_blk, cpu_fmt = ws, (1, 128), "fp8_block"
+        extra = {"tensors": len(ws), "layers": 4, "elements": sum(w.numel() for w in ws),
+                 "format": "fp8_block_1x128_float64_arithmetic", "launches_per_step": len(ws)}
     elif cfg == "c2sd":
         from lumenrl_amd.quantization import FP8Config, WeightQuantizer
 
@@ -633,8 +663,9 @@ def run(args):
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "f32",
-        "data": "synthetic (seeded on-device bf16 weights, BASELINE.json distribution)",
+        "dtype": "f64" if cfg == "f64" else "f32",
+        "data": "synthetic (seeded on-device bf16 weights, BASELINE.json distribution"
+                + ("; widened to float64)" if cfg == "f64" else ")"),
         "config": {"workload": workload, **extra, "algorithmic_bytes_per_step": step_bytes},
         "roofline": {
             "bound": "hbm",
@@ -781,7 +812,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--config", default="c2", choices=["c1", "c2", "c3", "c4", "c5", "c2r", "c2d", "c2sd", "bucket",
                                                       "act", "kv", "cast", "c4d", "c2host", "casthost",
-                                                      "rollout"])
+                                                      "rollout", "f64"])
     ap.add_argument("--seed", type=int, default=1000)
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
