@@ -48,17 +48,61 @@ __device__ __forceinline__ double pow2_f64(double s) {
   return u2d((e + up) << 52);  // e + up == 2047 gives +inf, as torch.pow(2, 1024.)
 }
 
-// Max over aligned groups of LPB lanes (LPB = 2..64) of 64-bit values.
+__device__ __forceinline__ uint64_t umax64(uint64_t a, uint64_t b) { return a > b ? a : b; }
+
+__device__ __forceinline__ uint64_t shfl_xor_u64(uint64_t v, int off) {
+  const uint32_t lo = (uint32_t)__shfl_xor((int)(uint32_t)v, off, 64);
+  const uint32_t hi = (uint32_t)__shfl_xor((int)(uint32_t)(v >> 32), off, 64);
+  return ((uint64_t)hi << 32) | lo;
+}
+
+template <int CTRL>
+__device__ __forceinline__ uint64_t dpp_u64(uint64_t v) {
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_mov_dpp((int)(uint32_t)v, CTRL, 0xF, 0xF, false);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_mov_dpp((int)(uint32_t)(v >> 32), CTRL, 0xF, 0xF, false);
+  return ((uint64_t)hi << 32) | lo;
+}
+
+// Max over aligned groups of LPB lanes (LPB = 2..64) of 64-bit values: DPP
+// within 16 lanes (quad_perm [1,0,3,2], [2,3,0,1], row_half_mirror,
+// row_mirror), shuffles beyond.
 template <int LPB>
 __device__ __forceinline__ uint64_t group_max_u64(uint64_t v) {
-#pragma unroll
-  for (int off = 1; off < LPB; off <<= 1) {
-    const uint32_t lo = (uint32_t)__shfl_xor((int)(uint32_t)v, off, 64);
-    const uint32_t hi = (uint32_t)__shfl_xor((int)(uint32_t)(v >> 32), off, 64);
-    const uint64_t o = ((uint64_t)hi << 32) | lo;
-    v = v > o ? v : o;
-  }
+  if constexpr (LPB >= 2) v = umax64(v, dpp_u64<0xB1>(v));
+  if constexpr (LPB >= 4) v = umax64(v, dpp_u64<0x4E>(v));
+  if constexpr (LPB >= 8) v = umax64(v, dpp_u64<0x141>(v));
+  if constexpr (LPB >= 16) v = umax64(v, dpp_u64<0x140>(v));
+  if constexpr (LPB >= 32) v = umax64(v, shfl_xor_u64(v, 16));
+  if constexpr (LPB >= 64) v = umax64(v, shfl_xor_u64(v, 32));
   return v;
+}
+
+// Wave-wide maxima of V per-lane values (V = 1, 2, 4, 8): halving exchanges
+// across lanes 32, 16, ... apart leave each lane one value, then a 64 / V lane
+// group reduction.  Lane l returns the maximum of value l / (64 / V) over the wave.
+template <int V>
+__device__ __forceinline__ uint64_t wave_max_split(const uint64_t (&p)[V], int lane) {
+  static_assert(V == 1 || V == 2 || V == 4 || V == 8, "1, 2, 4 or 8 values");
+  uint64_t c[V];
+#pragma unroll
+  for (int k = 0; k < V; ++k) c[k] = p[k];
+#pragma unroll
+  for (int nv = V, off = 32; nv > 1; nv /= 2, off /= 2) {
+    const bool up = lane & off;  // this lane keeps the upper half of its values
+#pragma unroll
+    for (int k = 0; k < nv / 2; ++k) {
+      const uint64_t keep = up ? c[nv / 2 + k] : c[k], send = up ? c[k] : c[nv / 2 + k];
+      c[k] = umax64(keep, shfl_xor_u64(send, off));
+    }
+  }
+  return group_max_u64<64 / V>(c[0]);
+}
+
+__device__ __forceinline__ double readlane_f64(double v, int lane) {
+  const uint64_t u = d2u(v);
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)u, lane);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(u >> 32), lane);
+  return u2d(((uint64_t)hi << 32) | lo);
 }
 
 // The block scale of weight_quantizer.py:60-65 in float64 from the block's
@@ -92,6 +136,36 @@ __device__ __forceinline__ uint32_t code_f64(double x, double s, int kind) {
     return sx;                    // finite / inf = +-0
   }
   return sw_e4m3((float)(x / s));  // IEEE float64 quotient, RNE to float32, RNE to e4m3
+}
+
+// Blocks whose quotients may take Markstein's correction (see code2_f64).
+__device__ __forceinline__ bool fast_block(double s, int kind) {
+  return kind == kScaleExact && s >= 0x1p-900;
+}
+
+// e4m3 codes of two elements (first in the low byte) of a block with scale s,
+// y = RN(1/s).  In a fast block the quotient is q0 = x y corrected once:
+// q = RN(q0 - (q0 s - x) y), Markstein's step, which gives RN(x / s) when the
+// residual q0 s - x is exact.  It is exact for |x| >= 2^-968 with a quotient
+// of at least 2^-900; with s >= 2^-900 every element whose quotient reaches
+// 2^-12 meets both bounds (|x| >= 2^-912).  A smaller quotient is within a
+// few ulps of x/s either way, so it stays below 2^-11 through the float32
+// rounding and encodes to +-0: the sign is x's (s > 0), set explicitly.
+// Other blocks take the IEEE division and the software encoder.
+__device__ __forceinline__ uint32_t code2_f64(uint64_t a, uint64_t b, double s, double y, int kind,
+                                              bool fast) {
+  if (!fast) return code_f64(u2d(a), s, kind) | (code_f64(u2d(b), s, kind) << 8);
+  const uint64_t xs[2] = {a, b};
+  float q[2];
+#pragma unroll
+  for (int k = 0; k < 2; ++k) {
+    const double x = u2d(xs[k]);
+    const double q0 = x * y;
+    const double t = __builtin_fma(q0, s, -x);
+    const float qf = (float)__builtin_fma(-t, y, q0);
+    q[k] = u2f((f2u(qf) & 0x7FFFFFFFu) | ((uint32_t)(xs[k] >> 32) & 0x80000000u));
+  }
+  return cvt_e4m3x2<false>(q[0], q[1], 0u) & 0xFFFFu;  // finite |q| <= 448 sqrt 2
 }
 
 }  // namespace
@@ -140,6 +214,9 @@ __global__ __launch_bounds__(256) void k_f64(Desc single, const Desc* __restrict
 // block spans B/2 lanes of one instruction (B < 128) or B/128 instructions of
 // all 64 lanes (B >= 128).  Each wave runs kF64RowInstr instructions; code
 // stores are 2 bytes per lane (128 contiguous bytes per wave instruction).
+// For B >= 128 a wave holds 4 / (B/128) whole blocks: each lane computes the
+// scale of one of them (wave_max_split) and the scales reach the whole wave
+// by readlane, so the quotient loop runs on wave-uniform s and 1/s.
 template <int B>
 __global__ __launch_bounds__(256) void k_row_f64(Desc single, const Desc* __restrict__ descs,
                                                  const uint32_t* __restrict__ map, int pow2) {
@@ -152,68 +229,69 @@ __global__ __launch_bounds__(256) void k_row_f64(Desc single, const Desc* __rest
   pick_desc<kXcdRunRow>(single, descs, map, d, u);
   const int lane = threadIdx.x & 63;
   const int64_t n = d.rows * d.cols;
-  const int64_t e0 = (u * 4 + (threadIdx.x >> 6)) * (NI * 128) + 2 * lane;  // first element, instruction 0
+  const int64_t w0 = (u * 4 + (threadIdx.x >> 6)) * (NI * 128);  // the wave's first element
+  const int64_t e0 = w0 + 2 * lane;                                // this lane's, instruction 0
   const double* in = static_cast<const double*>(d.in);
-  uint64_t x[NI][2];
+  // Every lane loads (a lane past the end re-reads the last two elements and
+  // drops them), so the loads issue back to back with no branch between.
+  // The scheduling barrier keeps the selects that read the first load from
+  // being hoisted above the later loads (which would wait on it).
+  v4u raw[NI];
+  bool ok[NI];
 #pragma unroll
   for (int i = 0; i < NI; ++i) {
     const int64_t e = e0 + i * 128;
-    x[i][0] = x[i][1] = 0;
-    if (e < n) {
-      const v4u v = load_nt(in + e);
-      x[i][0] = ((uint64_t)v.y << 32) | v.x;
-      x[i][1] = ((uint64_t)v.w << 32) | v.z;
-    }
+    ok[i] = e < n;  // n is a multiple of B >= 32: e < n covers e + 1
+    raw[i] = load_nt(in + (ok[i] ? e : n - 2));
   }
+  __builtin_amdgcn_sched_barrier(0);
+  uint64_t x[NI][2];
 #pragma unroll
-  for (int i = 0; i < NI; i += IPB) {
-    const int64_t eb = e0 + i * 128;  // this lane's first element of the block's first instruction
-    if (eb - 2 * lane >= n) break;     // wave-uniform: past the tensor's end (blocks are whole)
-    uint64_t a = 0;
+  for (int i = 0; i < NI; ++i) {
+    x[i][0] = ok[i] ? ((uint64_t)raw[i].y << 32) | raw[i].x : 0;
+    x[i][1] = ok[i] ? ((uint64_t)raw[i].w << 32) | raw[i].z : 0;
+  }
+  if constexpr (B >= 128) {
+    constexpr int V = NI / IPB;   // blocks per wave
+    constexpr int G = 64 / V;     // lanes holding one block's scale
+    uint64_t p[V];
 #pragma unroll
-    for (int j = i; j < i + IPB; ++j) {
-      const uint64_t a0 = x[j][0] & kAbs64, a1 = x[j][1] & kAbs64;
-      a = a0 > a ? a0 : a;
-      a = a1 > a ? a1 : a;
+    for (int v = 0; v < V; ++v) {
+      p[v] = 0;
+#pragma unroll
+      for (int j = v * IPB; j < (v + 1) * IPB; ++j)
+        p[v] = umax64(p[v], umax64(x[j][0] & kAbs64, x[j][1] & kAbs64));
     }
-    a = group_max_u64<LPB>(a);
     double s;
     int kind;
-    block_scale_f64(a, pow2 != 0, s, kind);
-    // Finite blocks use Markstein's correction of q0 = x * y with y = RN(1/s):
-    // q0 is within an ulp of x/s, the residual x - q0 s is then exact, and
-    // RN(q0 + residual * y) = RN(x/s).  The residual's last bit is about 2^-104
-    // |x|, so it is exact while |x| >= 2^-968; elements below that, or with a
-    // quotient below 2^-900, take the IEEE division.
-    const bool fast = kind == kScaleExact;
-    const double y = fast ? 1.0 / s : 0.0;
-    const int64_t blk = eb / B;
-    if (lane % LPB == 0 && eb < n) gst<double>(static_cast<double*>(d.scales) + blk, s);
+    block_scale_f64(wave_max_split<V>(p, lane), pow2 != 0, s, kind);
+    const double y = 1.0 / s;  // correctly rounded
+    const int64_t mine = w0 + (lane / G) * B;  // first element of this lane's block
+    if (lane % G == 0 && mine < n) gst<double>(static_cast<double*>(d.scales) + mine / B, s);
 #pragma unroll
-    for (int j = i; j < i + IPB; ++j) {
-      const int64_t e = e0 + j * 128;
-      if (e >= n) continue;
-      uint32_t c;
-      if (fast) {
-        float q[2];
+    for (int v = 0; v < V; ++v) {
+      if (w0 + v * B >= n) break;  // wave-uniform: blocks are whole
+      const double sv = readlane_f64(s, v * G), yv = readlane_f64(y, v * G);
+      const int kv = __builtin_amdgcn_readlane(kind, v * G);
+      const bool fast = fast_block(sv, kv);
 #pragma unroll
-        for (int k = 0; k < 2; ++k) {
-          const double xv = u2d(x[j][k]);
-          const double q0 = xv * y;
-          double qv;
-          if ((__builtin_fabs(xv) >= 0x1p-968 && __builtin_fabs(q0) >= 0x1p-900) || xv == 0.0) {
-            const double t = __builtin_fma(q0, s, -xv);
-            qv = __builtin_fma(-t, y, q0);  // -(q0 s - x): x = -0 keeps its sign
-          } else {
-            qv = xv / s;  // a quotient near underflow: the IEEE division
-          }
-          q[k] = (float)qv;
-        }
-        c = cvt_e4m3x2<false>(q[0], q[1], 0u) & 0xFFFFu;  // finite |q| <= 448 sqrt 2: the hardware encoder
-      } else {
-        c = code_f64(u2d(x[j][0]), s, kind) | (code_f64(u2d(x[j][1]), s, kind) << 8);
-      }
-      gst_nt<uint16_t>(d.codes + e, (uint16_t)c);
+      for (int j = v * IPB; j < (v + 1) * IPB; ++j)
+        gst_nt<uint16_t>(d.codes + e0 + j * 128,
+                         (uint16_t)code2_f64(x[j][0], x[j][1], sv, yv, kv, fast));
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < NI; ++i) {
+      const int64_t e = e0 + i * 128;  // this lane's elements of instruction i
+      if (w0 + i * 128 >= n) break;     // wave-uniform: past the tensor's end
+      const uint64_t a = group_max_u64<LPB>(umax64(x[i][0] & kAbs64, x[i][1] & kAbs64));
+      double s;
+      int kind;
+      block_scale_f64(a, pow2 != 0, s, kind);
+      const bool fast = fast_block(s, kind);
+      const double y = fast ? 1.0 / s : 0.0;
+      if (lane % LPB == 0 && e < n) gst<double>(static_cast<double*>(d.scales) + e / B, s);
+      if (e < n) gst_nt<uint16_t>(d.codes + e, (uint16_t)code2_f64(x[i][0], x[i][1], s, y, kind, fast));
     }
   }
 }

@@ -56,7 +56,9 @@ constexpr int64_t kXcdRunStream = 32;  // dequant, act, amax, copy, cast, generi
 constexpr int kCastLaneElems = 16;   // k_cast_e4m3: elements per lane
 constexpr int64_t kCastUnit = 256 * kCastLaneElems;  // k_cast_e4m3: elements per work-group
 constexpr int kAmaxLoads = 2;        // k_amax: 16-byte loads per lane (2 beat 1, 3, 4 and 8)
-constexpr int kF64RowInstr = 4;      // k_row_f64: 1 KiB wave instructions per wave (128 doubles each)
+// k_row_f64: 1 KiB wave instructions per wave (128 doubles each); 4 beats 8 by
+// 8-10% on 1x128 blocks
+constexpr int kF64RowInstr = 4;
 
 // Descriptor and local work unit of this work-group: the single-tensor
 // descriptor (kernel argument) or, for a grouped launch, the one the device

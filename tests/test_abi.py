@@ -399,8 +399,9 @@ def test_float64_input_needs_float64_arithmetic_and_the_fp8_block_format():
                                  _lib.FLAG_NATIVE_ARITH, None)
     assert rc == _lib.ERR_ALIGN
     # tables pack (host memory only) with each float64 kernel's geometry: a dense
-    # 1x128 tensor takes the row kernel (2048 doubles per work-group), a padded
-    # row pitch the generic kernel (one wave per block, four per work-group)
+    # 1x128 tensor takes the row kernel (4 waves x 4 instructions of 128 doubles
+    # per work-group), a padded row pitch the generic kernel (one wave per
+    # block, four per work-group)
     def units(rows, cols, ld):
         t = (_lib.LrqTensor * 1)()
         t[0].in_, t[0].codes, t[0].scales = 0x10000, 0x20000, 0x30000

@@ -172,21 +172,35 @@ def _division_regimes(n_blocks: int, rng) -> dict:
     x[:, 1::9] = rng.choice([0.0, -0.0], x[:, 1::9].shape)
     x[:, 0] = amax[:, 0]
     out["tiny"] = x
+    # (d) scales on both sides of 2^-900 (the kernel's Markstein / IEEE-division
+    # cut per block): quotients on e4m3 values and ties and around the
+    # subnormal edge (2^-13 ... 2^-9), nudged, and quotients below 2^-12
+    s = 2.0 ** rng.uniform(-902, -898, (n_blocks, 1)) * rng.uniform(1, 2, (n_blocks, 1))
+    edge = 2.0 ** rng.uniform(-13, -9, 4096)
+    t = rng.choice(np.concatenate([ties, v, edge, edge * 2.0 ** -20]), (n_blocks, 128))
+    nudge = rng.choice([-2, -1, 0, 1, 2], (n_blocks, 128)) * rng.choice([1e-16, 1e-12, 1.0], (n_blocks, 128))
+    t = t + nudge * np.where(nudge == 0, 0, np.ldexp(1.0, np.frexp(t)[1] - 25))
+    x = t * s * rng.choice([-1.0, 1.0], (n_blocks, 128))
+    x[:, 0] = 448.0 * s[:, 0]
+    out["guard"] = x
     return out
 
 
-@pytest.mark.parametrize("pow2", [False, True])
-def test_f64_row_kernel_division_sweep_vs_oracle(pow2):
-    """The 1x128 float64 kernel (Markstein's correction per element, IEEE division
-    near underflow) against the oracle's IEEE division, bit for bit, on 3 x 64 K
-    blocks of adversarial quotients."""
+@pytest.mark.parametrize("pow2,blk", [(False, 128), (True, 128), (False, 256), (False, 512)])
+def test_f64_row_kernel_division_sweep_vs_oracle(pow2, blk):
+    """The 1xB float64 kernel (Markstein's correction in blocks with s >= 2^-900,
+    the IEEE division below) against the oracle's IEEE division, bit for bit, on
+    4 x 64 K rows of adversarial quotients.  B = 256 and 512 (rows read as
+    [N/2, 256] and [N/4, 512]) take the same quotients through the layouts
+    whose scales reach the wave from other lanes."""
     rng = np.random.default_rng(1717 + int(pow2))
     for name, x in _division_regimes(1 << 16, rng).items():
-        say("f64 division sweep", name, pow2)
+        say("f64 division sweep", name, pow2, blk)
+        x = x.reshape(-1, blk)
         xd = torch.from_numpy(x).to(DEV)
-        c, s = ops.fp8_block_quant(xd, (1, 128), native_arith=True, pow2=pow2)
+        c, s = ops.fp8_block_quant(xd, (1, blk), native_arith=True, pow2=pow2)
         torch.cuda.synchronize()
-        oc, osc = O.fp8_block_quant(x, "f64", "native", (1, 128), pow2, nthreads=16)
+        oc, osc = O.fp8_block_quant(x, "f64", "native", (1, blk), pow2, nthreads=16)
         got_s = s.cpu().numpy().view(np.uint64).reshape(-1)
         assert np.array_equal(got_s, osc.view(np.uint64).reshape(-1)), name
         got_c = c.view(torch.uint8).cpu().numpy()
