@@ -77,17 +77,18 @@ __device__ __forceinline__ uint64_t group_max_u64(uint64_t v) {
   return v;
 }
 
-// Wave-wide maxima of V per-lane values (V = 1, 2, 4, 8): halving exchanges
-// across lanes 32, 16, ... apart leave each lane one value, then a 64 / V lane
-// group reduction.  Lane l returns the maximum of value l / (64 / V) over the wave.
-template <int V>
-__device__ __forceinline__ uint64_t wave_max_split(const uint64_t (&p)[V], int lane) {
-  static_assert(V == 1 || V == 2 || V == 4 || V == 8, "1, 2, 4 or 8 values");
+// Maxima of V per-lane values (V = 1, 2, 4, 8) over aligned groups of G lanes
+// (G = 16, 32, 64): halving exchanges across lanes G/2, G/4, ... apart leave
+// each lane one value, then a G / V lane group reduction.  Lane l returns the
+// maximum of value (l % G) / (G / V) over its group.
+template <int V, int G>
+__device__ __forceinline__ uint64_t split_max(const uint64_t (&p)[V], int lane) {
+  static_assert((V == 1 || V == 2 || V == 4 || V == 8) && V <= G, "1, 2, 4 or 8 values");
   uint64_t c[V];
 #pragma unroll
   for (int k = 0; k < V; ++k) c[k] = p[k];
 #pragma unroll
-  for (int nv = V, off = 32; nv > 1; nv /= 2, off /= 2) {
+  for (int nv = V, off = G / 2; nv > 1; nv /= 2, off /= 2) {
     const bool up = lane & off;  // this lane keeps the upper half of its values
 #pragma unroll
     for (int k = 0; k < nv / 2; ++k) {
@@ -95,7 +96,14 @@ __device__ __forceinline__ uint64_t wave_max_split(const uint64_t (&p)[V], int l
       c[k] = umax64(keep, shfl_xor_u64(send, off));
     }
   }
-  return group_max_u64<64 / V>(c[0]);
+  return group_max_u64<G / V>(c[0]);
+}
+
+__device__ __forceinline__ double shfl_f64(double v, int src) {
+  const uint64_t u = d2u(v);
+  const uint32_t lo = (uint32_t)__shfl((int)(uint32_t)u, src, 64);
+  const uint32_t hi = (uint32_t)__shfl((int)(uint32_t)(u >> 32), src, 64);
+  return u2d(((uint64_t)hi << 32) | lo);
 }
 
 __device__ __forceinline__ double readlane_f64(double v, int lane) {
@@ -215,8 +223,8 @@ __global__ __launch_bounds__(256) void k_f64(Desc single, const Desc* __restrict
 // all 64 lanes (B >= 128).  Each wave runs kF64RowInstr instructions; code
 // stores are 2 bytes per lane (128 contiguous bytes per wave instruction).
 // For B >= 128 a wave holds 4 / (B/128) whole blocks: each lane computes the
-// scale of one of them (wave_max_split) and the scales reach the whole wave
-// by readlane, so the quotient loop runs on wave-uniform s and 1/s.
+// scale of one of them (split_max) and the scales reach the whole wave by
+// readlane, so the quotient loop runs on wave-uniform s and 1/s.
 template <int B>
 __global__ __launch_bounds__(256) void k_row_f64(Desc single, const Desc* __restrict__ descs,
                                                  const uint32_t* __restrict__ map, int pow2) {
@@ -264,7 +272,7 @@ __global__ __launch_bounds__(256) void k_row_f64(Desc single, const Desc* __rest
     }
     double s;
     int kind;
-    block_scale_f64(wave_max_split<V>(p, lane), pow2 != 0, s, kind);
+    block_scale_f64(split_max<V, 64>(p, lane), pow2 != 0, s, kind);
     const double y = 1.0 / s;  // correctly rounded
     const int64_t mine = w0 + (lane / G) * B;  // first element of this lane's block
     if (lane % G == 0 && mine < n) gst<double>(static_cast<double*>(d.scales) + mine / B, s);
@@ -280,18 +288,29 @@ __global__ __launch_bounds__(256) void k_row_f64(Desc single, const Desc* __rest
                          (uint16_t)code2_f64(x[j][0], x[j][1], sv, yv, kv, fast));
     }
   } else {
+    // A block spans LPB lanes of one instruction: the NI partials of each
+    // LPB-lane group split so that each lane computes one scale (block
+    // (lane % LPB) / Q of its group's instructions), which the group's other
+    // lanes fetch by shuffle.
+    constexpr int Q = LPB / NI;  // lanes holding one block's scale
+    uint64_t p[NI];
+#pragma unroll
+    for (int i = 0; i < NI; ++i) p[i] = umax64(x[i][0] & kAbs64, x[i][1] & kAbs64);
+    double s;
+    int kind;
+    block_scale_f64(split_max<NI, LPB>(p, lane), pow2 != 0, s, kind);
+    const double y = 1.0 / s;  // correctly rounded
+    const int64_t mine = w0 + ((lane % LPB) / Q) * 128 + (lane / LPB) * B;  // this lane's block
+    if (lane % Q == 0 && mine < n) gst<double>(static_cast<double*>(d.scales) + mine / B, s);
 #pragma unroll
     for (int i = 0; i < NI; ++i) {
+      if (w0 + i * 128 >= n) break;  // wave-uniform: past the tensor's end
+      const int src = (lane / LPB) * LPB + i * Q;
+      const double si = shfl_f64(s, src), yi = shfl_f64(y, src);
+      const int ki = __shfl(kind, src, 64);
       const int64_t e = e0 + i * 128;  // this lane's elements of instruction i
-      if (w0 + i * 128 >= n) break;     // wave-uniform: past the tensor's end
-      const uint64_t a = group_max_u64<LPB>(umax64(x[i][0] & kAbs64, x[i][1] & kAbs64));
-      double s;
-      int kind;
-      block_scale_f64(a, pow2 != 0, s, kind);
-      const bool fast = fast_block(s, kind);
-      const double y = fast ? 1.0 / s : 0.0;
-      if (lane % LPB == 0 && e < n) gst<double>(static_cast<double*>(d.scales) + e / B, s);
-      if (e < n) gst_nt<uint16_t>(d.codes + e, (uint16_t)code2_f64(x[i][0], x[i][1], s, y, kind, fast));
+      if (e < n)
+        gst_nt<uint16_t>(d.codes + e, (uint16_t)code2_f64(x[i][0], x[i][1], si, yi, ki, fast_block(si, ki)));
     }
   }
 }

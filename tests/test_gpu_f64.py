@@ -186,13 +186,14 @@ def _division_regimes(n_blocks: int, rng) -> dict:
     return out
 
 
-@pytest.mark.parametrize("pow2,blk", [(False, 128), (True, 128), (False, 256), (False, 512)])
+@pytest.mark.parametrize("pow2,blk", [(False, 128), (True, 128), (False, 32), (False, 64),
+                                      (False, 256), (False, 512)])
 def test_f64_row_kernel_division_sweep_vs_oracle(pow2, blk):
     """The 1xB float64 kernel (Markstein's correction in blocks with s >= 2^-900,
     the IEEE division below) against the oracle's IEEE division, bit for bit, on
-    4 x 64 K rows of adversarial quotients.  B = 256 and 512 (rows read as
-    [N/2, 256] and [N/4, 512]) take the same quotients through the layouts
-    whose scales reach the wave from other lanes."""
+    4 x 64 K rows of adversarial quotients.  The same rows read as 1x32, 1x64,
+    1x256 and 1x512 blocks take the layouts whose scales reach each lane from
+    other lanes (shuffles within a block's lanes, or readlane)."""
     rng = np.random.default_rng(1717 + int(pow2))
     for name, x in _division_regimes(1 << 16, rng).items():
         say("f64 division sweep", name, pow2, blk)
