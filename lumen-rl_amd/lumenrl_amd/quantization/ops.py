@@ -580,7 +580,9 @@ class QuantPlan:
     outputs stay the same tensors across re-binds.
 
     Inputs must be device tensors with 16-byte aligned rows (every torch
-    allocation of a [N, K] weight with K % 8 == 0 qualifies).
+    allocation of a [N, K] weight with K % 8 == 0 qualifies).  float64 weights
+    take ``fmt="fp8_block"`` with ``native_arith=True`` (float64 arithmetic and
+    scales, as ``quantize_tensor`` on a float64 tensor).
     """
 
     def __init__(self, tensors: Sequence[Tensor], fmt: str = "fp8_block",
@@ -594,9 +596,12 @@ class QuantPlan:
         dt = tensors[0].dtype
         dev = tensors[0].device
         for t in tensors:
-            _check_input(t, "QuantPlan")
+            _check_input(t, "QuantPlan", allow_f64=True)
             if t.dtype != dt or t.device != dev:
                 raise ValueError("all tensors of a QuantPlan must share dtype and device")
+        if dt == torch.float64 and not (fmt == "fp8_block" and native_arith):
+            raise ValueError("QuantPlan: float64 weights are quantized to fp8_block in float64 "
+                             "arithmetic (native_arith=True); cast them to float32 otherwise")
         if outputs is not None and len(outputs) != len(tensors):
             raise ValueError("outputs must pair up with tensors")
         self.fmt = fmt
@@ -662,7 +667,8 @@ class QuantPlan:
             descs[i].scales = scales.data_ptr()
             descs[i].batch, descs[i].rows, descs[i].cols = batch, rows, cols
             descs[i].ld, descs[i].batch_stride = ld, bstride
-        launch = _GroupLaunch(self.fmt, descs, len(tensors), _IN_DTYPES[self.dtype], self._block,
+        launch = _GroupLaunch(self.fmt, descs, len(tensors),
+                              _IN_DTYPES.get(self.dtype, _lib.DTYPE_F64), self._block,
                               self._flags, self.device)
         if self._owned:
             launch.buffers += [t for pair in self.outputs for t in pair]
@@ -684,7 +690,7 @@ class QuantPlan:
             if len(inputs) != len(self._shapes):
                 raise ValueError(f"QuantPlan.run: {len(inputs)} inputs for a plan of {len(self._shapes)}")
             for i, t in enumerate(inputs):
-                _check_input(t, "QuantPlan.run")
+                _check_input(t, "QuantPlan.run", allow_f64=self.dtype == torch.float64)
                 if t.dtype != self.dtype or t.device != self.device or tuple(t.shape) != self._shapes[i]:
                     raise ValueError(f"QuantPlan.run: input {i} is {t.dtype} {tuple(t.shape)} on "
                                      f"{t.device}; the plan has {self.dtype} {self._shapes[i]} on "

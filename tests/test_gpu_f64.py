@@ -207,3 +207,55 @@ def test_f64_row_kernel_division_sweep_vs_oracle(pow2, blk):
         got_c = c.view(torch.uint8).cpu().numpy()
         bad = np.flatnonzero(got_c.reshape(-1) != oc.reshape(-1))
         assert bad.size == 0, (name, bad[:8], x.reshape(-1)[bad[:8]])
+
+
+def _grouped_inputs(shapes, rng):
+    xs = []
+    for shape in shapes:
+        x = rng.normal(0.0, 0.02, shape) * 2.0 ** rng.uniform(-40, 40)
+        flat = x.reshape(-1)
+        flat[rng.integers(0, flat.size, 4)] = rng.uniform(0.5, 4.0, 4)
+        xs.append(x)
+    xs[0].reshape(-1)[:40] = 0.0
+    xs[1].reshape(-1)[7] = np.inf
+    xs[-1].reshape(-1)[-3] = np.nan
+    return xs
+
+
+@pytest.mark.parametrize("blk,pow2", [((1, 128), False), ((1, 128), True), ((1, 32), False),
+                                      ((1, 512), False), ((128, 128), False), ((3, 40), False)])
+def test_f64_grouped_plan_vs_oracle(blk, pow2):
+    """float64 weights through one grouped launch (QuantPlan, float64 arithmetic):
+    the 1xB row kernel for dense 1xB blocks, the generic kernel otherwise; run
+    twice, the second time on new tensors (run(inputs=...))."""
+    say("f64 grouped plan", blk, pow2)
+    rng = np.random.default_rng(4242 + blk[1] + int(pow2))
+    if blk[0] == 1:
+        shapes = [(256, 1024), (1, 1024), (3, 64, 512), (640, 2048)]
+    else:
+        shapes = [(256, 384), (1, 200), (3, 130, 270), (640, 128)]
+    plan = None
+    for step in range(2):
+        xs = _grouped_inputs(shapes, rng)
+        ts = [torch.from_numpy(x).to(DEV) for x in xs]
+        if plan is None:
+            plan = ops.QuantPlan(ts, "fp8_block", blk, native_arith=True, use_pow2_scale=pow2)
+            outs = plan.run()
+        else:
+            outs = plan.run(inputs=ts)
+        torch.cuda.synchronize()
+        for x, (c, s) in zip(xs, outs):
+            assert s.dtype == torch.float64
+            oc, osc = O.fp8_block_quant(x, "f64", "native", blk, pow2, nthreads=16)
+            got_c = c.view(torch.uint8).cpu().numpy().reshape(oc.shape)
+            got_s = s.cpu().numpy().view(np.uint64).reshape(osc.shape)
+            assert np.array_equal(got_s, osc.view(np.uint64)), (blk, x.shape, step)
+            assert np.array_equal(got_c, oc), (blk, x.shape, step)
+
+
+def test_f64_plan_rules():
+    x = torch.zeros(128, 256, dtype=torch.float64, device=DEV)
+    with pytest.raises(ValueError, match="float64"):
+        ops.QuantPlan([x], "fp8_block", (1, 128))
+    with pytest.raises(ValueError, match="float64"):
+        ops.QuantPlan([x], "mxfp8", (1, 32), native_arith=True)
