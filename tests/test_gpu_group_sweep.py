@@ -3,7 +3,9 @@
 Each case is one plan over 1-12 tensors of random shape, dtype, row stride and
 magnitude (Student-t values, planted +-inf/NaN/zero/tiny/huge entries, zero
 rows): 128x128, 1x128 and odd-block FP8 (float32 or native arithmetic, pow2
-and bf16 scale options), MXFP8, MXFP4, the unscaled cast, per-tensor KV scales, FP8
+and bf16 scale options), float64 FP8 in float64 arithmetic (dense 1xB rows or
+any block over strided tensors, magnitudes across float64's range), MXFP8,
+MXFP4, the unscaled cast, per-tensor KV scales, FP8
 dequant of the 1x128 results and MX dequant of the MX results, to float32 and
 bf16.  Every code, scale and output bit is compared with the oracle (MX dequant
 with the torch restatement, NaN payloads aside: they depend on torch's loop
@@ -27,13 +29,14 @@ if not torch.cuda.is_available():  # pragma: no cover - CPU container
 
 DEV = torch.device("cuda", 0)
 DT = {"bf16": torch.bfloat16, "f16": torch.float16, "f32": torch.float32}
-KINDS = ["tile", "row", "mx8", "mx4", "cast", "kv", "deq", "mxdeq", "blk"]
+KINDS = ["tile", "row", "mx8", "mx4", "cast", "kv", "deq", "mxdeq", "blk", "f64"]
+F64_BLOCKS = [(1, 32), (1, 128), (1, 512), (128, 128), (3, 40), (1, 96)]
 BLOCKS = [(1, 32), (1, 64), (1, 256), (1, 512), (3, 40), (64, 96), (128, 64), (2, 128)]
 
 
 def host(t: torch.Tensor, dt: str) -> np.ndarray:
     t = t.detach().cpu().contiguous()
-    return t.numpy() if dt == "f32" else t.view(torch.int16).numpy().view(np.uint16)
+    return t.numpy() if dt in ("f32", "f64") else t.view(torch.int16).numpy().view(np.uint16)
 
 
 def u8(t: torch.Tensor) -> np.ndarray:
@@ -54,6 +57,16 @@ def _tensor(rng, rows, cols, dt, strided):
         r0 = int(rng.integers(0, rows))
         x[r0:r0 + 3, :] = 0.0
     t = torch.from_numpy(x).to(DT[dt]).to(DEV)
+    return t[:, :cols] if strided else t
+
+
+def _tensor64(rng, rows, cols, strided):
+    ld = cols + (int(rng.integers(1, 9)) if strided else 0)
+    x = rng.standard_t(4, (rows, ld)) * 2.0 ** rng.uniform(-1000, 1000)
+    for _ in range(int(rng.integers(0, 4))):
+        x[rng.integers(0, rows), rng.integers(0, ld)] = rng.choice(
+            [np.inf, -np.inf, np.nan, 0.0, -0.0, 5e-324, -2.5e-310, 1e300])
+    t = torch.from_numpy(x).to(DEV)
     return t[:, :cols] if strided else t
 
 
@@ -80,6 +93,9 @@ def test_grouped_plans_random_sweep(seed):
     rng = np.random.default_rng(seed)
     for case in range(60):
         kind = KINDS[rng.integers(0, len(KINDS))]
+        if kind == "f64":
+            _f64_case(rng, seed, case)
+            continue
         dt = ["bf16", "f16", "f32"][rng.integers(0, 3)]
         native = kind in ("tile", "row", "blk") and dt != "f32" and rng.random() < 0.3
         pow2 = kind in ("tile", "row", "blk") and rng.random() < 0.3
@@ -135,3 +151,24 @@ def test_grouped_plans_random_sweep(seed):
                                                (1, 128), oname)[0]
                     assert np.array_equal(fbits(back[i]), want.view(np.uint32) if oname == "f32" else want), \
                         (case, i, oname)
+
+
+def _f64_case(rng, seed, case):
+    """One grouped float64 plan: dense tensors with 1xB rows (the row kernel), or
+    any block over possibly strided tensors (the generic kernel)."""
+    blk = F64_BLOCKS[rng.integers(0, len(F64_BLOCKS))]
+    row = blk[0] == 1 and blk[1] in (32, 64, 128, 256, 512)
+    pow2 = bool(rng.random() < 0.3)
+    ts = []
+    for _ in range(int(rng.integers(1, 9))):
+        rows = int(rng.integers(1, 300))
+        cols = blk[1] * int(rng.integers(1, 9)) if row else int(rng.integers(1, 400))
+        ts.append(_tensor64(rng, rows, cols, strided=not row and rng.random() < 0.3))
+    print("group sweep", seed, case, "f64", blk, pow2, [tuple(t.shape) for t in ts], flush=True)
+    outs = ops.QuantPlan(ts, "fp8_block", blk, native_arith=True, use_pow2_scale=pow2).run()
+    torch.cuda.synchronize()
+    for i, t in enumerate(ts):
+        oc, osc = O.fp8_block_quant(host(t, "f64"), "f64", "native", blk, pow2)
+        assert np.array_equal(u8(outs[i][0]), oc[0]), (case, i)
+        got_s = outs[i][1].cpu().numpy().view(np.uint64).reshape(-1)
+        assert np.array_equal(got_s, osc[0].view(np.uint64).reshape(-1)), (case, i)
