@@ -44,7 +44,7 @@ constexpr uint32_t kTableVersion = 2u;
 // max_units() gives it per kernel.
 constexpr int64_t kMaxGrid = 0xFFFFFFFFll / 256;
 int64_t max_units(int kernel) {
-  return 0xFFFFFFFFll / (kernel == lrq::kKernTile128 ? lrq::kTileThreads : 256);
+  return 0xFFFFFFFFll / (kernel == lrq::kKernTile128 || kernel == lrq::kKernF64Tile ? lrq::kTileThreads : 256);
 }
 
 // Table layout, host and device alike: [header | n descriptors | map].  The
@@ -114,7 +114,11 @@ int fp8_kernel_for(const Desc& d, int in_dtype, int64_t blk_r, int64_t blk_c) {
     const bool row = blk_r == 1 && pow2_block(blk_c) && d.cols % blk_c == 0 && d.ld == d.cols &&
                      (d.batch == 1 || d.bstride == d.rows * d.ld) && aligned(d.in, 16) &&
                      aligned(d.codes, 2) && aligned(d.scales, 8);
-    return row ? lrq::kKernF64Row : lrq::kKernF64;
+    if (row) return lrq::kKernF64Row;
+    const bool tile = blk_r == 128 && blk_c == 128 && aligned(d.in, 16) && d.ld % 2 == 0 &&
+                      (d.batch == 1 || d.bstride % 2 == 0) && d.cols % 2 == 0 &&
+                      aligned(d.codes, 2) && aligned(d.scales, 8);
+    return tile ? lrq::kKernF64Tile : lrq::kKernF64;
   }
   const int64_t es = esize(in_dtype);
   const bool vec = aligned(d.in, 16) && (d.ld * es) % 16 == 0 &&
@@ -151,6 +155,7 @@ bool plan_units(const LaunchCfg& cfg, Desc& d) {
   }
   switch (cfg.kernel) {
     case kKernTile128:
+    case kKernF64Tile:
     case kKernGenericFp8:
       d.units_r = (d.rows + cfg.blk_r - 1) / cfg.blk_r;
       d.units_c = (d.cols + cfg.blk_c - 1) / cfg.blk_c;
@@ -213,7 +218,7 @@ hipError_t launch(const LaunchCfg& cfg, const Desc& single, const Desc* descs_de
     return launch_mx(cfg, single, descs_dev, map_dev, total_units, stream);
   if (cfg.kernel == kKernDequant || cfg.kernel == kKernGenericDequant)
     return launch_dequant(cfg, single, descs_dev, map_dev, total_units, stream);
-  if (cfg.kernel == kKernF64 || cfg.kernel == kKernF64Row)
+  if (cfg.kernel == kKernF64 || cfg.kernel == kKernF64Row || cfg.kernel == kKernF64Tile)
     return launch_f64(cfg, single, descs_dev, map_dev, total_units, stream);
   return launch_fp8(cfg, single, descs_dev, map_dev, total_units, stream);
 }

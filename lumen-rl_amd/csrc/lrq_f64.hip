@@ -7,13 +7,13 @@
 // rounded to float32 (:68) before the e4m3 cast (:71): a double rounding
 // (f64 -> f32 -> e4m3) that this kernel keeps.  Scales are written as float64.
 //
-// k_row_f64 takes dense 1xB blocks (B = 32...512, the reference's layout) with
-// 16-byte loads.  Its quotients of finite blocks use one correctly rounded 1/s
-// per block and Markstein's correction per element (the IEEE division near
-// underflow) and the hardware e4m3 encoder.  k_f64 takes every other shape,
-// one wave per block (any block shape), four blocks per 256-thread work-group,
-// re-reading the block from L2 for the encode, with the IEEE float64 division
-// and the software encoder.
+// k_row_f64 takes dense 1xB blocks (B = 32...512, the reference's layout) and
+// k_tile_f64 128x128 tiles, both with 16-byte loads.  Their quotients of finite
+// blocks use one correctly rounded 1/s per block and Markstein's correction per
+// element (the IEEE division in blocks with tiny scales) and the hardware e4m3
+// encoder.  k_f64 takes every other shape, one wave per block (any block
+// shape), four blocks per 256-thread work-group, re-reading the block from L2
+// for the encode, with the IEEE float64 division and the software encoder.
 #include "lrq_device.hpp"
 #include "lrq_internal.hpp"
 
@@ -315,6 +315,81 @@ __global__ __launch_bounds__(256) void k_row_f64(Desc single, const Desc* __rest
   }
 }
 
+// One 128x128 float64 tile held by 512 threads: thread t holds 16-byte chunk
+// t % 64 of rows t / 64 + 8 i (i < 16), so each wave instruction reads one whole
+// 1 KiB tile row.  FULL tiles load and store unconditionally; an edge tile's
+// lanes outside the matrix re-read its first two elements and drop them, so
+// the loads still issue back to back.
+template <bool FULL>
+__device__ __forceinline__ void tile_f64(const Desc& d, int64_t u, int64_t b, int64_t r0, int64_t col,
+                                         int pow2, uint64_t* red) {
+  constexpr int NL = 16, RS = 8;
+  const double* in = static_cast<const double*>(d.in) + b * d.bstride;
+  uint8_t* codes = d.codes + b * d.rows * d.cols;
+  const int lane = threadIdx.x & 63;
+  v4u v[NL];
+  if constexpr (FULL) {
+    const double* p = in + r0 * d.ld + col;
+#pragma unroll
+    for (int i = 0; i < NL; ++i) v[i] = load_nt(p + (int64_t)(RS * i) * d.ld);
+  } else {
+#pragma unroll
+    for (int i = 0; i < NL; ++i) {
+      const bool ok = col < d.cols && r0 + RS * i < d.rows;
+      v[i] = load_nt(in + (ok ? (r0 + RS * i) * d.ld + col : 0));
+    }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int i = 0; i < NL; ++i)
+      if (!(col < d.cols && r0 + RS * i < d.rows)) v[i] = v4u{0u, 0u, 0u, 0u};
+  }
+  uint64_t a = 0;
+#pragma unroll
+  for (int i = 0; i < NL; ++i)
+    a = umax64(a, umax64((((uint64_t)v[i].y << 32) | v[i].x) & kAbs64,
+                         (((uint64_t)v[i].w << 32) | v[i].z) & kAbs64));
+  a = group_max_u64<64>(a);
+  if (lane == 0) red[threadIdx.x >> 6] = a;
+  __syncthreads();
+  a = red[0];
+#pragma unroll
+  for (int w = 1; w < 8; ++w) a = umax64(a, red[w]);
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)a);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(a >> 32));
+  double s;
+  int kind;
+  block_scale_f64(((uint64_t)hi << 32) | lo, pow2 != 0, s, kind);
+  if (threadIdx.x == 0) gst<double>(static_cast<double*>(d.scales) + u, s);
+  const bool fast = fast_block(s, kind);
+  const double y = fast ? 1.0 / s : 0.0;
+  uint8_t* q = codes + r0 * d.cols + col;
+#pragma unroll
+  for (int i = 0; i < NL; ++i) {
+    const uint32_t c = code2_f64(((uint64_t)v[i].y << 32) | v[i].x, ((uint64_t)v[i].w << 32) | v[i].z,
+                                 s, y, kind, fast);
+    if (FULL || (col < d.cols && r0 + RS * i < d.rows)) gst_nt<uint16_t>(q + (int64_t)(RS * i) * d.cols, (uint16_t)c);
+  }
+}
+
+// 128x128 tiles of a float64 tensor (the vLLM/ATOM tile layout, in float64
+// arithmetic): one 512-thread work-group per tile; the tile stays in VGPRs,
+// one LDS step joins the eight waves' maxima, and s, 1/s are tile-uniform.
+__global__ __launch_bounds__(512) void k_tile_f64(Desc single, const Desc* __restrict__ descs,
+                                                  const uint32_t* __restrict__ map, int pow2) {
+  __shared__ uint64_t red[8];
+  Desc d;
+  int64_t u;
+  pick_desc<kXcdRunTile>(single, descs, map, d, u);
+  const int64_t per = d.units_r * d.units_c;
+  const int64_t b = u / per;
+  const int64_t rem = u - b * per;
+  const int64_t tr = rem / d.units_c, tc = rem - tr * d.units_c;
+  const int64_t r0 = tr * 128 + (threadIdx.x >> 6);
+  const int64_t col = tc * 128 + 2 * (threadIdx.x & 63);  // cols is even: col < cols covers col + 1
+  if (tr * 128 + 128 <= d.rows && tc * 128 + 128 <= d.cols) tile_f64<true>(d, u, b, r0, col, pow2, red);
+  else tile_f64<false>(d, u, b, r0, col, pow2, red);
+}
+
 hipError_t launch_f64(const LaunchCfg& cfg, const Desc& single, const Desc* descs,
                       const uint32_t* map, int64_t units, hipStream_t stream) {
   const dim3 grid((unsigned)units), block(256);
@@ -327,6 +402,10 @@ hipError_t launch_f64(const LaunchCfg& cfg, const Desc& single, const Desc* desc
       case 512: hipLaunchKernelGGL(k_row_f64<512>, grid, block, 0, stream, single, descs, map, cfg.pow2); break;
       default: return hipErrorInvalidValue;
     }
+    return hipGetLastError();
+  }
+  if (cfg.kernel == kKernF64Tile) {
+    hipLaunchKernelGGL(k_tile_f64, grid, dim3(512), 0, stream, single, descs, map, cfg.pow2);
     return hipGetLastError();
   }
   hipLaunchKernelGGL(k_f64, grid, block, 0, stream, single, descs, map, cfg.pow2, cfg.blk_r, cfg.blk_c);

@@ -39,6 +39,7 @@ enum Kernel : int {
   kKernMxDequant = 10,     // MXFP8 / MXFP4 dequant, 8 (bf16 out) or 4 (fp32) elements per lane-chunk
   kKernF64 = 11,           // FP8 blocks of a float64 tensor in float64 arithmetic, one wave per block
   kKernF64Row = 12,        // dense 1xB float64 blocks (B = 32..512), 16-byte loads
+  kKernF64Tile = 13,       // 128x128 float64 tiles, one 512-thread work-group per tile
 };
 
 // Work per lane of the streaming kernels, shared by the kernels and the

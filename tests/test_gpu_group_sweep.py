@@ -60,8 +60,8 @@ def _tensor(rng, rows, cols, dt, strided):
     return t[:, :cols] if strided else t
 
 
-def _tensor64(rng, rows, cols, strided):
-    ld = cols + (int(rng.integers(1, 9)) if strided else 0)
+def _tensor64(rng, rows, cols, strided, pitch_step=1):
+    ld = cols + (pitch_step * int(rng.integers(1, 9)) if strided else 0)
     x = rng.standard_t(4, (rows, ld)) * 2.0 ** rng.uniform(-1000, 1000)
     for _ in range(int(rng.integers(0, 4))):
         x[rng.integers(0, rows), rng.integers(0, ld)] = rng.choice(
@@ -154,16 +154,25 @@ def test_grouped_plans_random_sweep(seed):
 
 
 def _f64_case(rng, seed, case):
-    """One grouped float64 plan: dense tensors with 1xB rows (the row kernel), or
-    any block over possibly strided tensors (the generic kernel)."""
+    """One grouped float64 plan: dense tensors with 1xB rows (the row kernel);
+    128x128 tiles over even widths and row pitches (the tile kernel) or odd
+    widths (the generic kernel); any other block over possibly strided tensors
+    (the generic kernel).  One kernel per plan, as a grouped table requires."""
     blk = F64_BLOCKS[rng.integers(0, len(F64_BLOCKS))]
     row = blk[0] == 1 and blk[1] in (32, 64, 128, 256, 512)
+    even = blk == (128, 128) and rng.random() < 0.6
     pow2 = bool(rng.random() < 0.3)
     ts = []
     for _ in range(int(rng.integers(1, 9))):
         rows = int(rng.integers(1, 300))
-        cols = blk[1] * int(rng.integers(1, 9)) if row else int(rng.integers(1, 400))
-        ts.append(_tensor64(rng, rows, cols, strided=not row and rng.random() < 0.3))
+        if row:
+            cols = blk[1] * int(rng.integers(1, 9))
+        elif blk == (128, 128):
+            cols = 2 * int(rng.integers(1, 200)) + (0 if even else 1)
+        else:
+            cols = int(rng.integers(1, 400))
+        ts.append(_tensor64(rng, rows, cols, strided=not row and rng.random() < 0.3,
+                            pitch_step=2 if even else 1))
     print("group sweep", seed, case, "f64", blk, pow2, [tuple(t.shape) for t in ts], flush=True)
     outs = ops.QuantPlan(ts, "fp8_block", blk, native_arith=True, use_pow2_scale=pow2).run()
     torch.cuda.synchronize()
