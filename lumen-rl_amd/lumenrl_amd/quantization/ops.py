@@ -74,6 +74,9 @@ def matrix_view(x: Tensor) -> tuple[Tensor, int, int, int, int, int]:
     slice of a larger matrix costs no copy); otherwise a contiguous copy made
     on the device.
     """
+    if x.dim() == 2 and x.is_contiguous():  # the common case, without building a view
+        rows, cols = x.shape
+        return x, 1, rows, cols, cols, rows * cols
     if x.dim() == 1:
         x = x.reshape(1, -1)
     *lead, rows, cols = x.shape
@@ -132,17 +135,19 @@ def fp8_block_quant(x: Tensor, block: tuple[int, int], *, native_arith: bool = F
         sdt = torch.bfloat16
     else:
         raise ValueError(f"scale_dtype must be float32 or bfloat16, got {scale_dtype}")
-    codes = torch.empty(tuple(shape), dtype=torch.float8_e4m3fn, device=x.device)
+    codes = torch.empty(shape, dtype=torch.float8_e4m3fn, device=x.device)
     sshape = tuple(shape[:-2]) + (-(-rows // br), -(-cols // bc))
     scales = torch.empty(sshape, dtype=sdt, device=x.device)
-    if codes.numel() == 0:
-        return codes.reshape(x.shape), scales
+    if x.dim() < 2:
+        codes = codes.reshape(x.shape)
+    if batch * rows * cols == 0:
+        return codes, scales
     with _on(x.device):
         rc = _lib.lib().lrq_fp8_block_quant(
             xm.data_ptr(), _IN_DTYPES.get(x.dtype, _lib.DTYPE_F64), batch, rows, cols, ld, bstride,
             br, bc, codes.data_ptr(), scales.data_ptr(), flags, _stream(x.device))
     _lib.check(rc, "lrq_fp8_block_quant")
-    return codes.reshape(x.shape), scales
+    return codes, scales
 
 
 def fp8_block_dequant(codes: Tensor, scales: Tensor, block: tuple[int, int],

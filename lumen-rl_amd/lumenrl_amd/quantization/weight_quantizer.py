@@ -78,14 +78,17 @@ class WeightQuantizer:
         if last % block_size != 0:
             raise ValueError(f"Last dim {last} must be divisible by block_size={block_size}")
         x, home = _stage(tensor)
-        leading = 1
-        for d in tensor.shape[:-1]:
-            leading *= int(d)
-        flat = x.reshape(leading, last)
-        q, s = ops.fp8_block_quant(flat, (1, block_size), native_arith=True,
-                                   pow2=self._config.use_weight_pow2_scale)
-        q = q.reshape(tensor.shape)
-        s = s.reshape(tuple(tensor.shape[:-1]) + (last // block_size,))
+        pow2 = self._config.use_weight_pow2_scale
+        if x.dim() == 2:  # codes [N, K] and scales [N, K/B] as the kernel writes them
+            q, s = ops.fp8_block_quant(x, (1, block_size), native_arith=True, pow2=pow2)
+        else:
+            leading = 1
+            for d in tensor.shape[:-1]:
+                leading *= int(d)
+            q, s = ops.fp8_block_quant(x.reshape(leading, last), (1, block_size), native_arith=True,
+                                       pow2=pow2)
+            q = q.reshape(tensor.shape)
+            s = s.reshape(tuple(tensor.shape[:-1]) + (last // block_size,))
         if home is not None:
             q, s = q.to(home), s.to(home)
         return q, s
