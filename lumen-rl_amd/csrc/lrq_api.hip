@@ -128,6 +128,11 @@ int fp8_kernel_for(const Desc& d, int in_dtype, int64_t blk_r, int64_t blk_c) {
   if (blk_r == 1 && pow2_block(blk_c) && d.cols % blk_c == 0 && vec &&
       (d.batch == 1 || d.bstride == d.rows * d.ld))
     return lrq::kKernRowQuad;
+  // other widths of 8 G elements, G = 5..63 lanes per block (G >= kRowBlocks:
+  // a block's lanes share its kRowBlocks scale computations)
+  if (blk_r == 1 && blk_c % 8 == 0 && blk_c / 8 >= lrq::kRowBlocks && blk_c <= 512 &&
+      d.cols % blk_c == 0 && vec && (d.batch == 1 || d.bstride == d.rows * d.ld))
+    return lrq::kKernRowG;
   return lrq::kKernGenericFp8;
 }
 
@@ -178,6 +183,16 @@ bool plan_units(const LaunchCfg& cfg, Desc& d) {
       d.bpr = d.cols / cfg.blk_c;
       d.nblocks = d.rows * d.bpr;
       const int64_t per_wg = 4 * kRowBlocks * (512 / cfg.blk_c);  // 4 waves x kRowBlocks instructions
+      d.units = (d.nblocks + per_wg - 1) / per_wg;
+      return true;
+    }
+    case kKernRowG: {
+      if (!fold_batch(d)) return false;
+      d.bpr = d.cols / cfg.blk_c;
+      d.nblocks = d.rows * d.bpr;
+      int64_t lanes = 8;  // a block's lane group: the next power of two of blk_c / 8
+      while (lanes < cfg.blk_c / 8) lanes *= 2;
+      const int64_t per_wg = 4 * kRowBlocks * (64 / lanes);
       d.units = (d.nblocks + per_wg - 1) / per_wg;
       return true;
     }

@@ -197,12 +197,19 @@ __global__ __launch_bounds__(T) void k_tile128(Desc single, const Desc* __restri
 // beyond).  Each lane then computes the scale of ONE of its NJ blocks and
 // the NJ scales are exchanged by shuffles, so the IEEE divisions cost one
 // pair per lane instead of NJ.  Rows are folded over the batch by the host.
+// PAD takes widths that are not a power of two, 8 g elements with g = 5..63:
+// each block keeps the LPB-lane group of the next power of two and its last
+// LPB - g lanes idle, so the same DPP reductions apply (padding beat a
+// segmented reduction over exactly g lanes in 16 of 18 width x dtype cases).
 // ---------------------------------------------------------------------------
-template <int DT, int CDT, int LPB>
+template <int DT, int CDT, int LPB, bool PAD = false>
 __global__ __launch_bounds__(256) void k_row(Desc single, const Desc* __restrict__ descs,
                                              const uint32_t* __restrict__ map, int pow2,
-                                             int scale_bf16) {
-  constexpr int B = 8 * LPB;          // elements per block
+                                             int scale_bf16, int g = LPB) {
+  // PAD: blocks of 8 g elements, g < LPB, in LPB-lane groups whose last
+  // LPB - g lanes idle (widths that are not a power of two)
+  const int G = PAD ? g : LPB;        // lanes holding a chunk of the block
+  const int B = 8 * G;                // elements per block
   constexpr int BPI = 64 / LPB;       // blocks per wave instruction
   Desc d;
   int64_t u;
@@ -218,7 +225,7 @@ __global__ __launch_bounds__(256) void k_row(Desc single, const Desc* __restrict
 #pragma unroll
   for (int j = 0; j < NJ; ++j) {
     const int64_t gb = wb + j * BPI;
-    ok[j] = gb < d.nblocks;
+    ok[j] = (!PAD || c < G) && gb < d.nblocks;
     if (ok[j]) {
       int64_t off;
       if (d.ld == d.cols) {
@@ -338,6 +345,18 @@ static hipError_t launch_fp8_typed(const LaunchCfg& cfg, const Desc& single, con
         default: return hipErrorInvalidValue;
       }
       break;
+    case kKernRowG: {
+      const int g = cfg.blk_c / 8;  // 5..63, not a power of two
+      if (g < 8)
+        hipLaunchKernelGGL((k_row<DT, CDT, 8, true>), grid, block, 0, stream, single, descs, map, cfg.pow2, cfg.scale_bf16, g);
+      else if (g < 16)
+        hipLaunchKernelGGL((k_row<DT, CDT, 16, true>), grid, block, 0, stream, single, descs, map, cfg.pow2, cfg.scale_bf16, g);
+      else if (g < 32)
+        hipLaunchKernelGGL((k_row<DT, CDT, 32, true>), grid, block, 0, stream, single, descs, map, cfg.pow2, cfg.scale_bf16, g);
+      else
+        hipLaunchKernelGGL((k_row<DT, CDT, 64, true>), grid, block, 0, stream, single, descs, map, cfg.pow2, cfg.scale_bf16, g);
+      break;
+    }
     case kKernGenericFp8:
       hipLaunchKernelGGL((k_generic<DT, CDT>), grid, block, 0, stream, single, descs, map,
                          cfg.pow2, cfg.scale_bf16, cfg.blk_r, cfg.blk_c);

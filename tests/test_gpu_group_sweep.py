@@ -31,7 +31,7 @@ DEV = torch.device("cuda", 0)
 DT = {"bf16": torch.bfloat16, "f16": torch.float16, "f32": torch.float32}
 KINDS = ["tile", "row", "mx8", "mx4", "cast", "kv", "deq", "mxdeq", "blk", "f64"]
 F64_BLOCKS = [(1, 32), (1, 128), (1, 512), (128, 128), (3, 40), (1, 96)]
-BLOCKS = [(1, 32), (1, 64), (1, 256), (1, 512), (3, 40), (64, 96), (128, 64), (2, 128)]
+BLOCKS = [(1, 32), (1, 64), (1, 256), (1, 512), (3, 40), (64, 96), (128, 64), (2, 128), (1, 96), (1, 40)]
 
 
 def host(t: torch.Tensor, dt: str) -> np.ndarray:
@@ -103,6 +103,8 @@ def test_grouped_plans_random_sweep(seed):
         sbf16 = kind == "row" and not native and rng.random() < 0.3
         ts = []
         blk_cols = _shape(rng, "blk")[1]  # one width per odd-block plan: one kernel for all
+        if kind == "blk" and blk[0] == 1 and rng.random() < 0.7:
+            blk_cols = blk[1] * int(rng.integers(1, 8))  # whole 1xB blocks: the row kernels
         for _ in range(int(rng.integers(1, 13))):
             rows, cols = _shape(rng, kind)
             cols = blk_cols if kind == "blk" else cols

@@ -1,0 +1,99 @@
+"""1xB blocks of widths that are not a power of two, on an MI355X.
+
+``quantize_tensor(tensor, block_size=B)`` takes any B dividing the last dim
+(weight_quantizer.py:40-77).  Widths B = 8 G with G = 5..63 run on the row
+kernel with lane groups padded to the next power of two (the last lanes of
+each group idle); narrower or unaligned ones on the generic kernel.  Every
+code and scale bit is compared with the oracle, and the drop-in with the
+reference's torch op sequence.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle as O
+from oracle import torch_ref as TR
+from lumenrl_amd.quantization import FP8Config, WeightQuantizer, ops
+
+pytestmark = pytest.mark.gpu
+
+if not torch.cuda.is_available():  # pragma: no cover - CPU container
+    pytest.skip("needs a HIP device", allow_module_level=True)
+
+DEV = torch.device("cuda", 0)
+DT = {"bf16": torch.bfloat16, "f16": torch.float16, "f32": torch.float32}
+WIDTHS = [40, 48, 96, 120, 200, 248, 504, 24, 36]
+
+
+def host(t: torch.Tensor, dt: str) -> np.ndarray:
+    t = t.detach().cpu().contiguous()
+    return t.numpy() if dt == "f32" else t.view(torch.int16).numpy().view(np.uint16)
+
+
+def weights(rng, rows, cols, ld, dt):
+    x = (rng.standard_t(4, (rows, ld)) * 10.0 ** rng.uniform(-3, 0)).astype(np.float32)
+    for _ in range(3):
+        x[rng.integers(0, rows), rng.integers(0, cols)] = rng.choice([np.inf, -np.inf, np.nan, 0.0, 1e-30, 6e4])
+    x[rng.integers(0, rows), :] = 0.0
+    t = torch.from_numpy(x).to(DT[dt]).to(DEV)
+    return t[:, :cols] if ld != cols else t
+
+
+@pytest.mark.parametrize("B", WIDTHS)
+@pytest.mark.parametrize("dt,arith", [("bf16", "f32"), ("bf16", "native"), ("f16", "native"),
+                                      ("f16", "f32"), ("f32", "f32")])
+def test_width_vs_oracle(B, dt, arith):
+    print("rowg", B, dt, arith, flush=True)
+    rng = np.random.default_rng(B * 7 + len(dt) + len(arith))
+    for rows, mult, pitch, pow2, sbf16 in [(1, 1, 0, False, False), (37, 3, 0, True, False),
+                                          (200, 5, 16, False, arith == "f32"), (513, 2, 0, False, False),
+                                          (64, 11, 8, True, False)]:
+        cols = B * mult
+        ld = cols + pitch
+        if DT[dt].itemsize * ld % 16:
+            ld = cols
+        t = weights(rng, rows, cols, ld, dt)
+        c, s = ops.fp8_block_quant(t, (1, B), native_arith=arith == "native", pow2=pow2,
+                                   scale_dtype=torch.bfloat16 if sbf16 else None)
+        torch.cuda.synchronize()
+        oc, osc = O.fp8_block_quant(host(t, dt), dt, arith, (1, B), pow2)
+        assert np.array_equal(c.view(torch.uint8).cpu().numpy(), oc[0]), (B, rows, cols, ld)
+        want = O.bf16_from_f32(osc[0]) if sbf16 else osc[0]
+        want = want.view(np.uint32) if want.dtype == np.float32 else want
+        got = s.cpu().contiguous()
+        got = got.numpy().view(np.uint32) if got.dtype == torch.float32 else got.view(torch.int16).numpy().view(np.uint16)
+        assert np.array_equal(got.reshape(-1), want.reshape(-1)), (B, rows, cols, ld)
+
+
+@pytest.mark.parametrize("B", [96, 40, 200])
+def test_grouped_plan_and_expert_stacks(B):
+    print("rowg grouped", B, flush=True)
+    rng = np.random.default_rng(B)
+    ts = [weights(rng, r, B * m, B * m, "bf16") for r, m in [(100, 3), (1, 7), (333, 1), (64, 16)]]
+    ts.append(torch.from_numpy(rng.normal(0, 0.02, (3, 50, B * 2)).astype(np.float32)).to(torch.bfloat16).to(DEV))
+    plan = ops.QuantPlan(ts, "fp8_block", (1, B), scale_dtype=torch.bfloat16)
+    for step in range(2):
+        outs = plan.run()
+        torch.cuda.synchronize()
+        for t, (c, s) in zip(ts, outs):
+            x = host(t, "bf16")
+            oc, osc = O.fp8_block_quant(x.reshape(-1, x.shape[-1]), "bf16", "f32", (1, B), False)
+            assert np.array_equal(c.view(torch.uint8).cpu().numpy().reshape(-1), oc.reshape(-1)), (B, step)
+            want = O.bf16_from_f32(osc.reshape(-1))
+            assert np.array_equal(s.cpu().view(torch.int16).numpy().view(np.uint16).reshape(-1), want), (B, step)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_dropin_quantize_tensor_block_96_matches_reference_ops(dtype):
+    torch.manual_seed(5)
+    w = (torch.randn(300, 960) * 0.02).to(dtype)
+    wq = WeightQuantizer(FP8Config())
+    q, s = wq.quantize_tensor(w.to(DEV), block_size=96)
+    rq, rs = TR.quantize_tensor(w, 96)
+    assert q.shape == rq.shape and s.shape == rs.shape and s.dtype == rs.dtype
+    assert torch.equal(q.cpu().view(torch.uint8), rq.view(torch.uint8))
+    assert torch.equal(s.cpu().view(torch.int16 if s.element_size() == 2 else torch.int32),
+                       rs.view(torch.int16 if rs.element_size() == 2 else torch.int32))
