@@ -36,6 +36,8 @@ int64_t esize(int dt) { return dt == lrq::kF64 ? 8 : dt == lrq::kF32 ? 4 : 2; }
 bool aligned(const void* p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
 bool valid_dtype(int dt) { return dt == lrq::kBF16 || dt == lrq::kF16 || dt == lrq::kF32; }
 bool pow2_block(int64_t b) { return b == 32 || b == 64 || b == 128 || b == 256 || b == 512; }
+// widths k_row takes with whole lane groups: 4..64 lanes, or 2 / 4 wave instructions
+bool row_block(int64_t b) { return pow2_block(b) || b == 1024 || b == 2048; }
 
 constexpr uint32_t kMagic = 0x4C525154u;  // "LRQT"
 constexpr uint32_t kTableVersion = 2u;
@@ -125,13 +127,12 @@ int fp8_kernel_for(const Desc& d, int in_dtype, int64_t blk_r, int64_t blk_c) {
                    (d.batch == 1 || (d.bstride * es) % 16 == 0) && aligned(d.codes, 8) &&
                    d.cols % 8 == 0;
   if (blk_r == 128 && blk_c == 128 && vec) return lrq::kKernTile128;
-  if (blk_r == 1 && pow2_block(blk_c) && d.cols % blk_c == 0 && vec &&
+  if (blk_r == 1 && row_block(blk_c) && d.cols % blk_c == 0 && vec &&
       (d.batch == 1 || d.bstride == d.rows * d.ld))
     return lrq::kKernRowQuad;
-  // other widths of 8 G elements, G = 5..63 lanes per block (G >= kRowBlocks:
-  // a block's lanes share its kRowBlocks scale computations)
-  if (blk_r == 1 && blk_c % 8 == 0 && blk_c / 8 >= lrq::kRowBlocks && blk_c <= 512 &&
-      d.cols % blk_c == 0 && vec && (d.batch == 1 || d.bstride == d.rows * d.ld))
+  // other widths of 8 g elements up to 512 (g = 1..63): padded lane groups
+  if (blk_r == 1 && blk_c % 8 == 0 && blk_c <= 512 && d.cols % blk_c == 0 && vec &&
+      (d.batch == 1 || d.bstride == d.rows * d.ld))
     return lrq::kKernRowG;
   return lrq::kKernGenericFp8;
 }
@@ -182,7 +183,9 @@ bool plan_units(const LaunchCfg& cfg, Desc& d) {
       if (!fold_batch(d)) return false;
       d.bpr = d.cols / cfg.blk_c;
       d.nblocks = d.rows * d.bpr;
-      const int64_t per_wg = 4 * kRowBlocks * (512 / cfg.blk_c);  // 4 waves x kRowBlocks instructions
+      // 4 waves x kRowBlocks instructions of 512 elements
+      const int64_t per_wg = cfg.blk_c <= 512 ? 4 * kRowBlocks * (512 / cfg.blk_c)
+                                              : 4 * kRowBlocks / (cfg.blk_c / 512);
       d.units = (d.nblocks + per_wg - 1) / per_wg;
       return true;
     }
@@ -190,7 +193,7 @@ bool plan_units(const LaunchCfg& cfg, Desc& d) {
       if (!fold_batch(d)) return false;
       d.bpr = d.cols / cfg.blk_c;
       d.nblocks = d.rows * d.bpr;
-      int64_t lanes = 8;  // a block's lane group: the next power of two of blk_c / 8
+      int64_t lanes = 4;  // a block's lane group: the next power of two of blk_c / 8, 4 at least
       while (lanes < cfg.blk_c / 8) lanes *= 2;
       const int64_t per_wg = 4 * kRowBlocks * (64 / lanes);
       d.units = (d.nblocks + per_wg - 1) / per_wg;

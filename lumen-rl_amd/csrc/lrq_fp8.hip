@@ -197,74 +197,82 @@ __global__ __launch_bounds__(T) void k_tile128(Desc single, const Desc* __restri
 // beyond).  Each lane then computes the scale of ONE of its NJ blocks and
 // the NJ scales are exchanged by shuffles, so the IEEE divisions cost one
 // pair per lane instead of NJ.  Rows are folded over the batch by the host.
-// PAD takes widths that are not a power of two, 8 g elements with g = 5..63:
-// each block keeps the LPB-lane group of the next power of two and its last
-// LPB - g lanes idle, so the same DPP reductions apply (padding beat a
-// segmented reduction over exactly g lanes in 16 of 18 width x dtype cases).
+// PAD takes widths that are not a power of two, 8 g elements with g = 1..63
+// (the 4-lane group at least): each block keeps the LPB-lane group of the next
+// power of two and its last LPB - g lanes idle, so the same DPP reductions
+// apply (padding beat a segmented reduction over exactly g lanes in 16 of 18
+// width x dtype cases).  IPB = 2 or 4 takes 1x1024 and 1x2048 blocks, each
+// spanning IPB of a wave's instructions.
 // ---------------------------------------------------------------------------
-template <int DT, int CDT, int LPB, bool PAD = false>
+template <int DT, int CDT, int LPB, bool PAD = false, int IPB = 1>
 __global__ __launch_bounds__(256) void k_row(Desc single, const Desc* __restrict__ descs,
                                              const uint32_t* __restrict__ map, int pow2,
                                              int scale_bf16, int g = LPB) {
   // PAD: blocks of 8 g elements, g < LPB, in LPB-lane groups whose last
-  // LPB - g lanes idle (widths that are not a power of two)
+  // LPB - g lanes idle (widths that are not a power of two).  IPB > 1: blocks
+  // of 512 IPB elements spanning IPB consecutive wave instructions of all 64
+  // lanes (1x1024, 1x2048).
+  static_assert(IPB == 1 || (LPB == 64 && !PAD && kRowBlocks % IPB == 0), "whole blocks per wave");
   const int G = PAD ? g : LPB;        // lanes holding a chunk of the block
-  const int B = 8 * G;                // elements per block
+  const int B = 8 * G * IPB;          // elements per block
   constexpr int BPI = 64 / LPB;       // blocks per wave instruction
+  constexpr int NJ = kRowBlocks;      // wave instructions (chunks per lane)
+  constexpr int NB = NJ / IPB;        // blocks per lane
   Desc d;
   int64_t u;
   pick_desc<kXcdRunRow>(single, descs, map, d, u);
   const int tid = threadIdx.x, lane = tid & 63;
   const int c = lane & (LPB - 1);     // chunk of the block held by this lane
-  constexpr int NJ = kRowBlocks;      // blocks per lane
-  const int64_t wb = u * (4 * NJ * BPI) + (tid >> 6) * (NJ * BPI) + lane / LPB;  // block at j = 0
+  const int64_t wb = u * (4 * NB * BPI) + (tid >> 6) * (NB * BPI) + lane / LPB;  // block at j = 0
 
   Chunk<DT> ch[NJ];
   bool ok[NJ];
-  uint32_t am[NJ];
 #pragma unroll
   for (int j = 0; j < NJ; ++j) {
-    const int64_t gb = wb + j * BPI;
+    const int64_t gb = wb + (j / IPB) * BPI;
+    const int64_t part = (j % IPB) * 512 + c * 8;  // element of the block
     ok[j] = (!PAD || c < G) && gb < d.nblocks;
     if (ok[j]) {
       int64_t off;
       if (d.ld == d.cols) {
-        off = gb * B + c * 8;
+        off = gb * B + part;
       } else {
         const int64_t row = gb / d.bpr;
-        off = row * d.ld + (gb - row * d.bpr) * B + c * 8;
+        off = row * d.ld + (gb - row * d.bpr) * B + part;
       }
       load_chunk<DT>(ch[j], d.in, off);
     } else {
       zero_chunk<DT>(ch[j]);
     }
   }
+  uint32_t am[NB];
 #pragma unroll
-  for (int j = 0; j < NJ; ++j) {
+  for (int k = 0; k < NB; ++k) {
     Amax<DT> a;
     a.init();
-    a.add(ch[j]);
-    am[j] = group_max<LPB>(a.bits());  // every lane takes part: groups never straddle
+#pragma unroll
+    for (int j = k * IPB; j < (k + 1) * IPB; ++j) a.add(ch[j]);
+    am[k] = group_max<LPB>(a.bits());  // every lane takes part: groups never straddle
   }
-  // lane c computes the scale of block j = c % NJ of its group; gather all NJ
+  // lane c computes the scale of block k = c % NB of its group; gather all NB
   uint32_t mine = am[0];
 #pragma unroll
-  for (int j = 1; j < NJ; ++j) mine = (c % NJ) == j ? am[j] : mine;
+  for (int k = 1; k < NB; ++k) mine = (c % NB) == k ? am[k] : mine;
   const BlockScale own = block_scale<CDT>(mine, pow2 != 0);
-  BlockScale bs[NJ];
+  BlockScale bs[NB];
 #pragma unroll
-  for (int j = 0; j < NJ; ++j) {
-    const int src = (lane & ~(LPB - 1)) | j;
-    bs[j].s = __shfl(own.s, src, 64);
-    bs[j].y = __shfl(own.y, src, 64);
-    bs[j].kind = __shfl(own.kind, src, 64);
+  for (int k = 0; k < NB; ++k) {
+    const int src = (lane & ~(LPB - 1)) | k;  // idle PAD lanes hold the group max too
+    bs[k].s = __shfl(own.s, src, 64);
+    bs[k].y = __shfl(own.y, src, 64);
+    bs[k].kind = __shfl(own.kind, src, 64);
   }
 #pragma unroll
   for (int j = 0; j < NJ; ++j) {
     if (!ok[j]) continue;
-    const int64_t gb = wb + j * BPI;
-    if (c == 0) store_scale<CDT>(d.scales, gb, bs[j].s, scale_bf16);
-    store_nt(d.codes + gb * B + c * 8, encode_chunk<DT, CDT>(ch[j], bs[j]));
+    const int64_t gb = wb + (j / IPB) * BPI;
+    if (c == 0 && j % IPB == 0) store_scale<CDT>(d.scales, gb, bs[j / IPB].s, scale_bf16);
+    store_nt(d.codes + gb * B + (j % IPB) * 512 + c * 8, encode_chunk<DT, CDT>(ch[j], bs[j / IPB]));
   }
 }
 
@@ -342,12 +350,16 @@ static hipError_t launch_fp8_typed(const LaunchCfg& cfg, const Desc& single, con
         case 128: hipLaunchKernelGGL((k_row<DT, CDT, 16>), grid, block, 0, stream, single, descs, map, cfg.pow2, cfg.scale_bf16); break;
         case 256: hipLaunchKernelGGL((k_row<DT, CDT, 32>), grid, block, 0, stream, single, descs, map, cfg.pow2, cfg.scale_bf16); break;
         case 512: hipLaunchKernelGGL((k_row<DT, CDT, 64>), grid, block, 0, stream, single, descs, map, cfg.pow2, cfg.scale_bf16); break;
+        case 1024: hipLaunchKernelGGL((k_row<DT, CDT, 64, false, 2>), grid, block, 0, stream, single, descs, map, cfg.pow2, cfg.scale_bf16); break;
+        case 2048: hipLaunchKernelGGL((k_row<DT, CDT, 64, false, 4>), grid, block, 0, stream, single, descs, map, cfg.pow2, cfg.scale_bf16); break;
         default: return hipErrorInvalidValue;
       }
       break;
     case kKernRowG: {
-      const int g = cfg.blk_c / 8;  // 5..63, not a power of two
-      if (g < 8)
+      const int g = cfg.blk_c / 8;  // 1..63, not a power of two of 4..64 lanes
+      if (g < 4)
+        hipLaunchKernelGGL((k_row<DT, CDT, 4, true>), grid, block, 0, stream, single, descs, map, cfg.pow2, cfg.scale_bf16, g);
+      else if (g < 8)
         hipLaunchKernelGGL((k_row<DT, CDT, 8, true>), grid, block, 0, stream, single, descs, map, cfg.pow2, cfg.scale_bf16, g);
       else if (g < 16)
         hipLaunchKernelGGL((k_row<DT, CDT, 16, true>), grid, block, 0, stream, single, descs, map, cfg.pow2, cfg.scale_bf16, g);

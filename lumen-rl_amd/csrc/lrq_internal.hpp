@@ -40,8 +40,8 @@ enum Kernel : int {
   kKernF64 = 11,           // FP8 blocks of a float64 tensor in float64 arithmetic, one wave per block
   kKernF64Row = 12,        // dense 1xB float64 blocks (B = 32..512), 16-byte loads
   kKernF64Tile = 13,       // 128x128 float64 tiles, one 512-thread work-group per tile
-  kKernRowG = 14,          // 1xB FP8 blocks of 8 G elements, G = 5..63 not a power of two: k_row with
-                           // G of each next-power-of-two lane group active
+  kKernRowG = 14,          // 1xB FP8 blocks of 8 g elements, g = 1..63 not 4..64 a power of two: k_row
+                           // with g lanes of each next-power-of-two group (4 at least) active
 };
 
 // Work per lane of the streaming kernels, shared by the kernels and the

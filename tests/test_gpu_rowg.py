@@ -1,11 +1,12 @@
 """1xB blocks of widths that are not a power of two, on an MI355X.
 
 ``quantize_tensor(tensor, block_size=B)`` takes any B dividing the last dim
-(weight_quantizer.py:40-77).  Widths B = 8 G with G = 5..63 run on the row
-kernel with lane groups padded to the next power of two (the last lanes of
-each group idle); narrower or unaligned ones on the generic kernel.  Every
-code and scale bit is compared with the oracle, and the drop-in with the
-reference's torch op sequence.
+(weight_quantizer.py:40-77).  Widths B = 8 g up to 512 that are not 32..512
+powers of two run on the row kernel with lane groups padded to the next power
+of two (the last lanes of each group idle); 1024 and 2048 on the row kernel
+with a block spanning 2 or 4 wave instructions; the rest (36, 1536) on the
+generic kernel.  Every code and scale bit is compared with the oracle, and the
+drop-in with the reference's torch op sequence.
 """
 
 from __future__ import annotations
@@ -25,7 +26,7 @@ if not torch.cuda.is_available():  # pragma: no cover - CPU container
 
 DEV = torch.device("cuda", 0)
 DT = {"bf16": torch.bfloat16, "f16": torch.float16, "f32": torch.float32}
-WIDTHS = [40, 48, 96, 120, 200, 248, 504, 24, 36]
+WIDTHS = [40, 48, 96, 120, 200, 248, 504, 8, 16, 24, 36, 1024, 2048, 1536]
 
 
 def host(t: torch.Tensor, dt: str) -> np.ndarray:
