@@ -50,7 +50,8 @@ constexpr int64_t kCopyUnit = 4096;  // k_copy: bytes per work-group (one 16 B l
 constexpr int kDequantChunks = 2;    // k_dequant: 16-byte output chunks per lane (2 beat 1, 4 and 8)
 constexpr int kMxLoads = 2;          // k_mx: 32-element groups per quad of lanes (2 beat 1, 3 and 4)
 constexpr int kTileThreads = 512;    // k_tile128: threads per 128x128 tile (512 beat 256 and 1024)
-constexpr int kRowBlocks = 4;        // k_row: 1xB blocks per lane, sharing one scale computation (4: 2 is 7% slower with bf16 scales, 3 slower with both)
+constexpr int kRowBlocks = 4;        // k_row: wave instructions per lane, one 1xB block each up to B = 512, sharing
+                                     // one scale computation (4: 2 is 7% slower with bf16 scales, 3 slower with both)
 // XCD run length (xcd_unit) per kernel, in work units; sweeps over 8..128:
 constexpr int64_t kXcdRunTile = 32;    // k_tile128: 32 tiles = 1 MiB of bf16 (16 and 8 lose 6-7%, 64 and 128 1%)
 constexpr int64_t kXcdRunRow = 16;     // k_row: 256 KiB of bf16 (32 loses 2%)
