@@ -164,8 +164,8 @@ def moe_layer(torch, dev, seed, layer, experts=128):
 # CPU baseline: the reference's op sequence in torch on the host (bounded sample)
 # ---------------------------------------------------------------------------
 def cpu_baseline(torch, ws, fmt, fmt_block, seconds, full_bytes=None):
-    """The CPU path on the host, timed as BASELINE.md section 3 asks: one warm-up
-    pass, then the median of 3 passes over the same bounded sample.
+    """The CPU path on the host: one warm-up pass, then the median of 3 passes
+    over the same bounded sample.
 
     The sample is the first tensors of the workload, as many as fit in about
     ``seconds / 4`` of 16-thread work (so the four passes take about ``seconds``);
