@@ -742,6 +742,9 @@ class DequantPlan:
             raise ValueError(f"fmt must be fp8_block, mxfp8 or mxfp4, got {fmt!r}")
         sdt = pairs[0][1].dtype
         dev = pairs[0][0].device
+        if sdt not in _IN_DTYPES:
+            raise TypeError(f"DequantPlan: scales must be float32, bfloat16 or float16, got {sdt} "
+                            "(cast float64 scales to float32, as dequantize_tensor does)")
         br, bc = int(block_size[0]), int(block_size[1])
         descs = (_lib.LrqTensor * len(pairs))()
         self.inputs = []
