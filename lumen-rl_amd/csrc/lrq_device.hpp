@@ -32,6 +32,11 @@ __device__ __forceinline__ uint32_t bf16_bits(float f) {
   return (u + 0x7FFFu + ((u >> 16) & 1u)) >> 16;
 }
 __device__ __forceinline__ float bf16_round(float f) { return u2f(bf16_bits(f) << 16); }
+// bf16_round for a value known not to be NaN (RNE; inf and overflow to inf as IEEE)
+__device__ __forceinline__ float bf16_round_finite(float f) {
+  const uint32_t u = f2u(f);
+  return u2f((u + 0x7FFFu + ((u >> 16) & 1u)) & 0xFFFF0000u);
+}
 
 __device__ __forceinline__ float f16_to_f32(uint32_t h) {
   return (float)__builtin_bit_cast(_Float16, (unsigned short)h);
@@ -199,8 +204,9 @@ template <int CDT>
 __device__ __forceinline__ float block_quot(float x, const BlockScale& b) {
   if (CDT == kBF16) {
     // bf16 arithmetic: RN_bf16(RN_f32(x/s)); x*y lands on the same bf16 value
-    // for every bf16 x and every bf16 s (checked exhaustively).
-    return bf16_round(b.kind == kScaleFast ? x * b.y : x / b.s);
+    // for every bf16 x and every bf16 s (checked exhaustively).  x and s are
+    // finite here, so the quotient is never NaN.
+    return bf16_round_finite(b.kind == kScaleFast ? x * b.y : x / b.s);
   }
   if (CDT == kF16) return f16_round(x / b.s);
   if (b.kind == kScaleFast) {
