@@ -49,6 +49,8 @@ __device__ __forceinline__ uint32_t f16_bits(float f) {
   return (uint32_t)__builtin_bit_cast(unsigned short, (_Float16)f);  // IEEE RNE, keeps subnormals
 }
 __device__ __forceinline__ float f16_round(float f) { return f16_to_f32(f16_bits(f)); }
+// f16_round for a value known not to be NaN: IEEE RNE to binary16 and back
+__device__ __forceinline__ float f16_round_finite(float f) { return (float)(_Float16)f; }
 
 // ---------------------------------------------------------------------------
 // element encoders
@@ -192,7 +194,7 @@ __device__ __forceinline__ BlockScale block_scale(uint32_t amax_bits, bool pow2)
   r.y = 1.0f / s;  // IEEE division, correctly rounded
   // Blocks whose amax is below 2^-80 may hold subnormal x whose Markstein
   // residual underflows; they take the exact division (never real weights).
-  r.kind = (CDT == kF16 || amax < 0x1p-80f) ? kScaleExact : kScaleFast;
+  r.kind = amax < 0x1p-80f ? kScaleExact : kScaleFast;
   return r;
 }
 
@@ -200,21 +202,25 @@ __device__ __forceinline__ BlockScale block_scale(uint32_t amax_bits, bool pow2)
 // kScaleFast: Markstein's correction of x*y with y = RN(1/s): with y correctly
 // rounded and the residual exact, RN(q0 + (x - q0*s)*y) = RN(x/s).  The
 // residual is formed as -(q0*s - x) so that x = -0 keeps its sign.
+// x and s are finite here, so the quotient is never NaN.
 template <int CDT>
 __device__ __forceinline__ float block_quot(float x, const BlockScale& b) {
   if (CDT == kBF16) {
     // bf16 arithmetic: RN_bf16(RN_f32(x/s)); x*y lands on the same bf16 value
-    // for every bf16 x and every bf16 s (checked exhaustively).  x and s are
-    // finite here, so the quotient is never NaN.
+    // for every bf16 x and every bf16 s (checked exhaustively).
     return bf16_round_finite(b.kind == kScaleFast ? x * b.y : x / b.s);
   }
-  if (CDT == kF16) return f16_round(x / b.s);
+  float q;
   if (b.kind == kScaleFast) {
-    float q0 = x * b.y;
-    float t = __builtin_fmaf(q0, b.s, -x);
-    return __builtin_fmaf(-t, b.y, q0);
+    const float q0 = x * b.y;
+    const float t = __builtin_fmaf(q0, b.s, -x);
+    q = __builtin_fmaf(-t, b.y, q0);
+  } else {
+    q = x / b.s;
   }
-  return x / b.s;
+  // fp16 arithmetic: RN_f16(RN_f32(x/s)); every nonzero fp16 x has |x| >= 2^-24,
+  // so the residual never underflows (checked exhaustively over fp16 pairs)
+  return CDT == kF16 ? f16_round_finite(q) : q;
 }
 
 // e4m3 byte of x in a block whose scale is inf or NaN (torch on x86):

@@ -468,11 +468,11 @@ def test_grouped_expert_stacks_single_launch():
 # ----------------------------------------------------------------------------
 # exhaustive (x, amax): every bf16 x against every finite bf16 amax
 # ----------------------------------------------------------------------------
-def exhaustive_blocks(per_block: int) -> np.ndarray:
-    """Rows of `per_block` bf16 patterns: slot 0 holds amax a, the rest every
-    bf16 x with |x| <= a (both signs), for every finite positive a."""
+def exhaustive_blocks(per_block: int, dt: str = "bf16") -> np.ndarray:
+    """Rows of `per_block` bf16 (or fp16) patterns: slot 0 holds amax a, the
+    rest every x with |x| <= a (both signs), for every finite positive a."""
     rows = []
-    for a in range(1, 0x7F80):
+    for a in range(1, 0x7F80 if dt == "bf16" else 0x7C00):
         xs = np.concatenate([np.arange(0, a + 1, dtype=np.uint16),
                              np.arange(0x8000, 0x8000 + a + 1, dtype=np.uint16)])
         k = per_block - 1
@@ -498,6 +498,26 @@ def test_exhaustive_pairs_row_kernel(arith):
     sb = scale_bits(s).reshape(-1)
     want = osc.view(np.uint32).reshape(-1) if osc.dtype == np.float32 else osc.reshape(-1)
     assert np.array_equal(sb, want)
+
+
+@pytest.mark.slow
+@pytest.mark.parametrize("arith", ["f32", "native"])
+def test_exhaustive_pairs_f16_row_and_tile_kernels(arith):
+    """Every fp16 x against every finite fp16 amax (1.0 G pairs) through the 1x128
+    row kernel and the 128x128 tile kernel: the Markstein quotient, rounded to
+    fp16 in native arithmetic, equals the oracle's IEEE division everywhere."""
+    for blk in ((1, 128), (128, 128)):
+        xb = exhaustive_blocks(blk[0] * 128, "f16").reshape(-1, 128)
+        say("exhaustive f16", arith, blk, xb.shape)
+        xd = dev_from_bits(xb, "f16")
+        c, s = ops.fp8_block_quant(xd, blk, native_arith=arith == "native")
+        torch.cuda.synchronize()
+        oc, osc = O.fp8_block_quant(xb, "f16", arith, blk)
+        assert int((u8(c).reshape(oc.shape) != oc).sum()) == 0, blk
+        sb = scale_bits(s).reshape(-1)
+        want = osc.view(np.uint32).reshape(-1) if osc.dtype == np.float32 else osc.reshape(-1)
+        assert np.array_equal(sb, want), blk
+        del xb, xd, c, s, oc, osc
 
 
 @pytest.mark.slow
