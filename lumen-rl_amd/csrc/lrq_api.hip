@@ -127,6 +127,9 @@ int fp8_kernel_for(const Desc& d, int in_dtype, int64_t blk_r, int64_t blk_c) {
                    (d.batch == 1 || (d.bstride * es) % 16 == 0) && aligned(d.codes, 8) &&
                    d.cols % 8 == 0;
   if (blk_r == 128 && blk_c == 128 && vec) return lrq::kKernTile128;
+  if (in_dtype == lrq::kF32 && blk_r == 1 && (pow2_block(blk_c) || blk_c == 1024) &&
+      d.cols % blk_c == 0 && vec && aligned(d.codes, 4) && (d.batch == 1 || d.bstride == d.rows * d.ld))
+    return lrq::kKernRowF32;  // float32 input: 4-float chunks, 1 KiB per wave instruction
   if (blk_r == 1 && row_block(blk_c) && d.cols % blk_c == 0 && vec &&
       (d.batch == 1 || d.bstride == d.rows * d.ld))
     return lrq::kKernRowQuad;
@@ -186,6 +189,15 @@ bool plan_units(const LaunchCfg& cfg, Desc& d) {
       // 4 waves x kRowBlocks instructions of 512 elements
       const int64_t per_wg = cfg.blk_c <= 512 ? 4 * kRowBlocks * (512 / cfg.blk_c)
                                               : 4 * kRowBlocks / (cfg.blk_c / 512);
+      d.units = (d.nblocks + per_wg - 1) / per_wg;
+      return true;
+    }
+    case kKernRowF32: {  // 4 waves x kRowBlocks instructions of 256 floats
+      if (!fold_batch(d)) return false;
+      d.bpr = d.cols / cfg.blk_c;
+      d.nblocks = d.rows * d.bpr;
+      const int64_t per_wg = cfg.blk_c <= 256 ? 4 * kRowBlocks * (256 / cfg.blk_c)
+                                              : 4 * kRowBlocks / (cfg.blk_c / 256);
       d.units = (d.nblocks + per_wg - 1) / per_wg;
       return true;
     }

@@ -277,6 +277,99 @@ __global__ __launch_bounds__(256) void k_row(Desc single, const Desc* __restrict
 }
 
 // ---------------------------------------------------------------------------
+// 1xB row blocks of float32 input (B = 32...1024): a lane's chunk is one
+// 16-byte load of 4 floats, so each wave instruction reads 1 KiB contiguous
+// (k_row's 8-element chunks of float32 take two loads at a 32-byte stride,
+// each instruction covering a 2 KiB span at half density).  A block spans
+// LPB = B/4 lanes of one instruction (B <= 256) or all 64 lanes of IPB
+// instructions (B = 512, 1024); NJ = kRowBlocks instructions per wave, one
+// scale computation per lane as in k_row.
+// ---------------------------------------------------------------------------
+template <int LPB, int IPB>
+__global__ __launch_bounds__(256) void k_row_f32(Desc single, const Desc* __restrict__ descs,
+                                                 const uint32_t* __restrict__ map, int pow2,
+                                                 int scale_bf16) {
+  static_assert(IPB == 1 || LPB == 64, "multi-instruction blocks span the whole wave");
+  constexpr int NJ = kRowBlocks;      // wave instructions (chunks per lane)
+  static_assert(NJ % IPB == 0, "whole blocks per wave");
+  constexpr int B = 4 * LPB * IPB;    // elements per block
+  constexpr int BPI = 64 / LPB;       // blocks per wave instruction
+  constexpr int NB = NJ / IPB;        // blocks per lane
+  Desc d;
+  int64_t u;
+  pick_desc<kXcdRunRow>(single, descs, map, d, u);
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int c = lane & (LPB - 1);     // chunk of the block held by this lane
+  const int64_t wb = u * (4 * NB * BPI) + (tid >> 6) * (NB * BPI) + lane / LPB;  // block at j = 0
+  const float* in = static_cast<const float*>(d.in);
+
+  v4u v[NJ];
+  bool ok[NJ];
+#pragma unroll
+  for (int j = 0; j < NJ; ++j) {
+    const int64_t gb = wb + (j / IPB) * BPI;
+    const int64_t part = (j % IPB) * 256 + c * 4;  // element of the block
+    ok[j] = gb < d.nblocks;
+    if (ok[j]) {
+      int64_t off;
+      if (d.ld == d.cols) {
+        off = gb * B + part;
+      } else {
+        const int64_t row = gb / d.bpr;
+        off = row * d.ld + (gb - row * d.bpr) * B + part;
+      }
+      v[j] = load_nt(in + off);
+    } else {
+      v[j] = v4u{0u, 0u, 0u, 0u};
+    }
+  }
+  uint32_t am[NB];
+#pragma unroll
+  for (int k = 0; k < NB; ++k) {
+    uint32_t a = 0u;
+#pragma unroll
+    for (int j = k * IPB; j < (k + 1) * IPB; ++j) {
+      const uint32_t w[4] = {v[j].x, v[j].y, v[j].z, v[j].w};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const uint32_t m = w[i] & 0x7FFFFFFFu;
+        a = m > a ? m : a;
+      }
+    }
+    am[k] = group_max<LPB>(a);
+  }
+  uint32_t mine = am[0];
+#pragma unroll
+  for (int k = 1; k < NB; ++k) mine = (c % NB) == k ? am[k] : mine;
+  const BlockScale own = block_scale<kF32>(mine, pow2 != 0);
+  BlockScale bs[NB];
+#pragma unroll
+  for (int k = 0; k < NB; ++k) {
+    const int src = (lane & ~(LPB - 1)) | k;
+    bs[k].s = __shfl(own.s, src, 64);
+    bs[k].y = __shfl(own.y, src, 64);
+    bs[k].kind = __shfl(own.kind, src, 64);
+  }
+#pragma unroll
+  for (int j = 0; j < NJ; ++j) {
+    if (!ok[j]) continue;
+    const int64_t gb = wb + (j / IPB) * BPI;
+    const BlockScale& b = bs[j / IPB];
+    const float x[4] = {u2f(v[j].x), u2f(v[j].y), u2f(v[j].z), u2f(v[j].w)};
+    uint32_t code;
+    if (b.kind <= kScaleExact) {
+      code = cvt_e4m3x4(block_quot<kF32>(x[0], b), block_quot<kF32>(x[1], b),
+                        block_quot<kF32>(x[2], b), block_quot<kF32>(x[3], b));
+    } else {
+      code = special_code<kF32>(x[0], b) | (special_code<kF32>(x[1], b) << 8) |
+             (special_code<kF32>(x[2], b) << 16) | (special_code<kF32>(x[3], b) << 24);
+    }
+    if (c == 0 && j % IPB == 0) store_scale<kF32>(d.scales, gb, b.s, scale_bf16);
+    store_nt(d.codes + gb * B + (j % IPB) * 256 + c * 4, code);
+  }
+}
+
+// ---------------------------------------------------------------------------
 // Generic: one work-group per block of any shape; scalar loads; edge blocks
 // partial.  Unit u = (b, tile row, tile col) row-major = the scale index.
 // ---------------------------------------------------------------------------
@@ -355,6 +448,20 @@ static hipError_t launch_fp8_typed(const LaunchCfg& cfg, const Desc& single, con
         default: return hipErrorInvalidValue;
       }
       break;
+    case kKernRowF32:
+      if constexpr (DT == kF32) {
+        switch (cfg.blk_c) {
+          case 32: hipLaunchKernelGGL((k_row_f32<8, 1>), grid, block, 0, stream, single, descs, map, cfg.pow2, cfg.scale_bf16); break;
+          case 64: hipLaunchKernelGGL((k_row_f32<16, 1>), grid, block, 0, stream, single, descs, map, cfg.pow2, cfg.scale_bf16); break;
+          case 128: hipLaunchKernelGGL((k_row_f32<32, 1>), grid, block, 0, stream, single, descs, map, cfg.pow2, cfg.scale_bf16); break;
+          case 256: hipLaunchKernelGGL((k_row_f32<64, 1>), grid, block, 0, stream, single, descs, map, cfg.pow2, cfg.scale_bf16); break;
+          case 512: hipLaunchKernelGGL((k_row_f32<64, 2>), grid, block, 0, stream, single, descs, map, cfg.pow2, cfg.scale_bf16); break;
+          case 1024: hipLaunchKernelGGL((k_row_f32<64, 4>), grid, block, 0, stream, single, descs, map, cfg.pow2, cfg.scale_bf16); break;
+          default: return hipErrorInvalidValue;
+        }
+        break;
+      }
+      return hipErrorInvalidValue;
     case kKernRowG: {
       const int g = cfg.blk_c / 8;  // 1..63, not a power of two of 4..64 lanes
       if (g < 4)
