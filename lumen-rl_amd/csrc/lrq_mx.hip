@@ -9,71 +9,60 @@
 // nearest even, saturating (E4M3 +-448, E2M1 +-6).  E2M1 uses gfx950's scaled
 // FP4 pack-convert; E4M3 scales, clamps and uses the FP8 pack-convert.
 //
-// k_mx: a quad of lanes per group (8 elements per lane); wave w of the
-// work-group takes groups 256u + 64w + 16j + (lane>>2), j = 0..3, so each load
-// instruction of a wave reads 16 whole groups = 1 KiB contiguous.
+// k_mx (bf16/f16): a quad of lanes per group (8 elements per lane); wave w of
+// work-group u takes groups 64*kMxLoads*u + 16*kMxLoads*w + 16j + (lane>>2),
+// j < kMxLoads, so each load instruction of a wave reads 16 whole groups =
+// 1 KiB contiguous.  k_mx_f32: 8 lanes per group, the same 1 KiB per load.
 #include "lrq_device.hpp"
 #include "lrq_internal.hpp"
 
 namespace lrq {
 
-template <int DT>
-__device__ __forceinline__ void mx_load8(const void* base, int64_t off, uint32_t (&w)[8]) {
-  if constexpr (DT == kF32) {
-    const float* p = static_cast<const float*>(base) + off;
-    const v4u a = load_nt(p), b = load_nt(p + 4);
-    w[0] = a.x; w[1] = a.y; w[2] = a.z; w[3] = a.w;
-    w[4] = b.x; w[5] = b.y; w[6] = b.z; w[7] = b.w;
-  } else {
-    const v4u a = load_nt(static_cast<const uint16_t*>(base) + off);
-    w[0] = a.x; w[1] = a.y; w[2] = a.z; w[3] = a.w;
-  }
+// 8 bf16/f16 elements (16 bytes) -> w[0..3]
+__device__ __forceinline__ void mx_load8(const void* base, int64_t off, uint32_t (&w)[4]) {
+  const v4u a = load_nt(static_cast<const uint16_t*>(base) + off);
+  w[0] = a.x; w[1] = a.y; w[2] = a.z; w[3] = a.w;
 }
 
-template <int DT>
-__device__ __forceinline__ float mx_elem(const uint32_t (&w)[8], int i) {
+template <int DT, int N>
+__device__ __forceinline__ float mx_elem(const uint32_t (&w)[N], int i) {
   if constexpr (DT == kF32) return u2f(w[i]);
   else if constexpr (DT == kBF16) return (i & 1) ? bf16_hi(w[i >> 1]) : bf16_lo(w[i >> 1]);
   else return f16_to_f32((i & 1) ? (w[i >> 1] >> 16) : (w[i >> 1] & 0xFFFFu));
 }
 
+// amax of 8 bf16/f16 elements, as float32 bits
 template <int DT>
-__device__ __forceinline__ uint32_t mx_amax8(const uint32_t (&w)[8]) {
-  if constexpr (DT == kF32) {
-    uint32_t m = 0u;
+__device__ __forceinline__ uint32_t mx_amax8(const uint32_t (&w)[4]) {
+  u16x2 m = u16x2{0, 0};
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const uint32_t a = w[i] & 0x7FFFFFFFu;
-      m = a > m ? a : m;
-    }
-    return m;
-  } else {
-    u16x2 m = u16x2{0, 0};
-#pragma unroll
-    for (int i = 0; i < 4; ++i) m = amax_bf16x2(m, w[i]);
-    const uint32_t a = m.x > m.y ? m.x : m.y;
-    if constexpr (DT == kBF16) return a << 16;
-    return f2u(f16_to_f32(a));
-  }
+  for (int i = 0; i < 4; ++i) m = amax_bf16x2(m, w[i]);
+  const uint32_t a = m.x > m.y ? m.x : m.y;
+  if constexpr (DT == kBF16) return a << 16;
+  return f2u(f16_to_f32(a));
 }
 
-// 8 elements of a finite group -> E4M3 bytes (8) or E2M1 nibbles (8 in a dword).
-template <int DT, int FMT>
-__device__ __forceinline__ v2u mx_encode8(const uint32_t (&w)[8], uint32_t e8m0) {
+// E (4 or 8) elements of a group -> E4M3 bytes (E) or E2M1 nibbles (E, in the
+// low E/2 bytes of r.x).
+template <int DT, int FMT, int E = 8, int N>
+__device__ __forceinline__ v2u mx_encode(const uint32_t (&w)[N], uint32_t e8m0) {
   v2u r;
   if (e8m0 != 0xFFu) {
     if constexpr (FMT == 8) {
       const float mult = mx_mult(e8m0);
       float v[8];
 #pragma unroll
-      for (int i = 0; i < 8; ++i) v[i] = __builtin_amdgcn_fmed3f(mx_elem<DT>(w, i) * mult, -448.0f, 448.0f);
+      for (int i = 0; i < E; ++i) v[i] = __builtin_amdgcn_fmed3f(mx_elem<DT>(w, i) * mult, -448.0f, 448.0f);
       r.x = cvt_e4m3x4(v[0], v[1], v[2], v[3]);
-      r.y = cvt_e4m3x4(v[4], v[5], v[6], v[7]);
+      r.y = 0u;
+      if constexpr (E == 8) r.y = cvt_e4m3x4(v[4], v[5], v[6], v[7]);
     } else {
       uint32_t n = mx_fp4x2<0>(0u, mx_elem<DT>(w, 0), mx_elem<DT>(w, 1), e8m0);
       n = mx_fp4x2<1>(n, mx_elem<DT>(w, 2), mx_elem<DT>(w, 3), e8m0);
-      n = mx_fp4x2<2>(n, mx_elem<DT>(w, 4), mx_elem<DT>(w, 5), e8m0);
-      n = mx_fp4x2<3>(n, mx_elem<DT>(w, 6), mx_elem<DT>(w, 7), e8m0);
+      if constexpr (E == 8) {
+        n = mx_fp4x2<2>(n, mx_elem<DT>(w, 4), mx_elem<DT>(w, 5), e8m0);
+        n = mx_fp4x2<3>(n, mx_elem<DT>(w, 6), mx_elem<DT>(w, 7), e8m0);
+      }
       r.x = n;
       r.y = 0u;
     }
@@ -82,7 +71,7 @@ __device__ __forceinline__ v2u mx_encode8(const uint32_t (&w)[8], uint32_t e8m0)
     // E2M1 has no NaN: +-0 for every element.
     uint32_t lo = 0u, hi = 0u;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
+    for (int i = 0; i < E; ++i) {
       const uint32_t u = f2u(mx_elem<DT>(w, i));
       uint32_t c;
       if constexpr (FMT == 8) {
@@ -112,7 +101,7 @@ __global__ __launch_bounds__(256) void k_mx(Desc single, const Desc* __restrict_
   const int p = lane & 3;
   const int64_t g0 = u * (64 * kMxLoads) + (tid >> 6) * (16 * kMxLoads) + (lane >> 2);
 
-  uint32_t w[kMxLoads][8];
+  uint32_t w[kMxLoads][4];
   bool ok[kMxLoads];
 #pragma unroll
   for (int j = 0; j < kMxLoads; ++j) {
@@ -126,10 +115,10 @@ __global__ __launch_bounds__(256) void k_mx(Desc single, const Desc* __restrict_
         const int64_t row = g / d.bpr;
         off = row * d.ld + (g - row * d.bpr) * 32 + p * 8;
       }
-      mx_load8<DT>(d.in, off, w[j]);
+      mx_load8(d.in, off, w[j]);
     } else {
 #pragma unroll
-      for (int i = 0; i < 8; ++i) w[j][i] = 0u;
+      for (int i = 0; i < 4; ++i) w[j][i] = 0u;
     }
   }
 
@@ -140,11 +129,72 @@ __global__ __launch_bounds__(256) void k_mx(Desc single, const Desc* __restrict_
     const uint32_t e = mx_e8m0<kEmax>(a);
     if (!ok[j]) continue;
     const int64_t g = g0 + 16 * j;
-    const v2u c = mx_encode8<DT, FMT>(w[j], e);
+    const v2u c = mx_encode<DT, FMT>(w[j], e);
     if constexpr (FMT == 8) {
       store_nt(d.codes + g * 32 + p * 8, c);
     } else {
       store_nt(d.codes + g * 16 + p * 4, (uint32_t)c.x);
+    }
+    if (p == 0) gst<uint8_t>(static_cast<uint8_t*>(d.scales) + g, (uint8_t)e);
+  }
+}
+
+// Float32 input: 8 lanes per group and 4 elements per lane, so each lane makes
+// one 16-byte load per group and each wave load instruction reads 8 whole
+// groups = 1 KiB contiguous (k_mx's 8 elements per lane would take two loads
+// at a 32-byte lane stride).  A work-group covers the same 64 * kMxLoads groups
+// as k_mx: wave w takes groups 64*kMxLoads*u + 16*kMxLoads*w + 8j + (lane>>3).
+// Lanes past the last group load the last group (in bounds) and store nothing.
+template <int FMT>
+__global__ __launch_bounds__(256) void k_mx_f32(Desc single, const Desc* __restrict__ descs,
+                                                const uint32_t* __restrict__ map) {
+  constexpr int kEmax = FMT == 8 ? 8 : 2;
+  constexpr int J = 2 * kMxLoads;
+  Desc d;
+  int64_t u;
+  pick_desc<kXcdRunMx>(single, descs, map, d, u);
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int p = lane & 7;
+  const int64_t g0 = u * (64 * kMxLoads) + (tid >> 6) * (16 * kMxLoads) + (lane >> 3);
+  const float* in = static_cast<const float*>(d.in);
+
+  uint32_t w[J][4];
+  bool ok[J];
+#pragma unroll
+  for (int j = 0; j < J; ++j) {
+    const int64_t g = g0 + 8 * j;
+    ok[j] = g < d.nblocks;
+    const int64_t gc = ok[j] ? g : d.nblocks - 1;
+    int64_t off;
+    if (d.ld == d.cols) {
+      off = gc * 32 + p * 4;
+    } else {
+      const int64_t row = gc / d.bpr;
+      off = row * d.ld + (gc - row * d.bpr) * 32 + p * 4;
+    }
+    const v4u a = load_nt(in + off);
+    w[j][0] = a.x; w[j][1] = a.y; w[j][2] = a.z; w[j][3] = a.w;
+  }
+  __builtin_amdgcn_sched_barrier(0);
+
+#pragma unroll
+  for (int j = 0; j < J; ++j) {
+    uint32_t a = 0u;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint32_t m = w[j][i] & 0x7FFFFFFFu;
+      a = m > a ? m : a;
+    }
+    // the 8 lanes of a group share g: wholly in range or wholly out
+    const uint32_t e = mx_e8m0<kEmax>(group_max<8>(a));
+    if (!ok[j]) continue;
+    const int64_t g = g0 + 8 * j;
+    const v2u c = mx_encode<kF32, FMT, 4>(w[j], e);
+    if constexpr (FMT == 8) {
+      store_nt(d.codes + g * 32 + p * 4, (uint32_t)c.x);
+    } else {
+      gst_nt<uint16_t>(d.codes + g * 16 + p * 2, (uint16_t)c.x);
     }
     if (p == 0) gst<uint8_t>(static_cast<uint8_t*>(d.scales) + g, (uint8_t)e);
   }
@@ -213,7 +263,7 @@ __global__ __launch_bounds__(256) void k_diag_mx(const float* __restrict__ in,
   w[1] = f2u(in[2 * k + 1]);
 #pragma unroll
   for (int i = 2; i < 8; ++i) w[i] = 0u;
-  const v2u c = mx_encode8<kF32, FMT>(w, e8m0[k]);
+  const v2u c = mx_encode<kF32, FMT>(w, e8m0[k]);
   if constexpr (FMT == 8) {
     out[2 * k] = (uint8_t)(c.x & 0xFFu);
     out[2 * k + 1] = (uint8_t)((c.x >> 8) & 0xFFu);
@@ -239,9 +289,11 @@ static hipError_t launch_mx_typed(const LaunchCfg& cfg, const Desc& single, cons
   const bool gen = cfg.kernel == kKernGenericMx;
   if (cfg.mx_fmt == 8) {
     if (gen) hipLaunchKernelGGL((k_mx_generic<DT, 8>), grid, block, 0, stream, single, descs, map);
+    else if constexpr (DT == kF32) hipLaunchKernelGGL((k_mx_f32<8>), grid, block, 0, stream, single, descs, map);
     else hipLaunchKernelGGL((k_mx<DT, 8>), grid, block, 0, stream, single, descs, map);
   } else {
     if (gen) hipLaunchKernelGGL((k_mx_generic<DT, 4>), grid, block, 0, stream, single, descs, map);
+    else if constexpr (DT == kF32) hipLaunchKernelGGL((k_mx_f32<4>), grid, block, 0, stream, single, descs, map);
     else hipLaunchKernelGGL((k_mx<DT, 4>), grid, block, 0, stream, single, descs, map);
   }
   return hipGetLastError();
