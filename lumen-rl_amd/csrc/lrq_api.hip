@@ -127,13 +127,14 @@ int fp8_kernel_for(const Desc& d, int in_dtype, int64_t blk_r, int64_t blk_c) {
                    (d.batch == 1 || (d.bstride * es) % 16 == 0) && aligned(d.codes, 8) &&
                    d.cols % 8 == 0;
   if (blk_r == 128 && blk_c == 128 && vec) return lrq::kKernTile128;
-  if (in_dtype == lrq::kF32 && blk_r == 1 && (pow2_block(blk_c) || blk_c == 1024) &&
+  if (in_dtype == lrq::kF32 && blk_r == 1 && (pow2_block(blk_c) || blk_c == 8 || blk_c == 16 || blk_c == 1024) &&
       d.cols % blk_c == 0 && vec && aligned(d.codes, 4) && (d.batch == 1 || d.bstride == d.rows * d.ld))
     return lrq::kKernRowF32;  // float32 input: 4-float chunks, 1 KiB per wave instruction
   if (blk_r == 1 && row_block(blk_c) && d.cols % blk_c == 0 && vec &&
       (d.batch == 1 || d.bstride == d.rows * d.ld))
     return lrq::kKernRowQuad;
-  // other widths of 8 g elements up to 512 (g = 1..63): padded lane groups
+  // other widths of 8 g elements up to 512 (g = 1..63): 1- and 2-lane groups,
+  // padded lane groups beyond
   if (blk_r == 1 && blk_c % 8 == 0 && blk_c <= 512 && d.cols % blk_c == 0 && vec &&
       (d.batch == 1 || d.bstride == d.rows * d.ld))
     return lrq::kKernRowG;
@@ -205,7 +206,7 @@ bool plan_units(const LaunchCfg& cfg, Desc& d) {
       if (!fold_batch(d)) return false;
       d.bpr = d.cols / cfg.blk_c;
       d.nblocks = d.rows * d.bpr;
-      int64_t lanes = 4;  // a block's lane group: the next power of two of blk_c / 8, 4 at least
+      int64_t lanes = 1;  // a block's lane group: 1, 2, or the next power of two of blk_c / 8
       while (lanes < cfg.blk_c / 8) lanes *= 2;
       const int64_t per_wg = 4 * kRowBlocks * (64 / lanes);
       d.units = (d.nblocks + per_wg - 1) / per_wg;

@@ -187,7 +187,7 @@ __global__ __launch_bounds__(T) void k_tile128(Desc single, const Desc* __restri
 }
 
 // ---------------------------------------------------------------------------
-// 1xB row blocks (B = 8*LPB, LPB = 4..64 lanes per block).  The 64 lanes of a
+// 1xB row blocks (B = 8*LPB, LPB = 1..64 lanes per block).  The 64 lanes of a
 // wave cover 64 consecutive 8-element chunks, so each load instruction reads
 // one contiguous span (1 KiB of bf16) and each store writes whole 128-byte
 // code lines; lane c of a block holds chunk c of it.  Instruction j of wave w
@@ -197,7 +197,8 @@ __global__ __launch_bounds__(T) void k_tile128(Desc single, const Desc* __restri
 // beyond).  Each lane then computes the scale of ONE of its NJ blocks and
 // the NJ scales are exchanged by shuffles, so the IEEE divisions cost one
 // pair per lane instead of NJ.  Rows are folded over the batch by the host.
-// PAD takes widths that are not a power of two, 8 g elements with g = 1..63
+// LPB = 1 or 2 (1x8, 1x16) gives every lane its own blocks' scales.
+// PAD takes widths that are not a power of two, 8 g elements with g = 3..63
 // (the 4-lane group at least): each block keeps the LPB-lane group of the next
 // power of two and its last LPB - g lanes idle, so the same DPP reductions
 // apply (padding beat a segmented reduction over exactly g lanes in 16 of 18
@@ -254,18 +255,25 @@ __global__ __launch_bounds__(256) void k_row(Desc single, const Desc* __restrict
     for (int j = k * IPB; j < (k + 1) * IPB; ++j) a.add(ch[j]);
     am[k] = group_max<LPB>(a.bits());  // every lane takes part: groups never straddle
   }
-  // lane c computes the scale of block k = c % NB of its group; gather all NB
-  uint32_t mine = am[0];
-#pragma unroll
-  for (int k = 1; k < NB; ++k) mine = (c % NB) == k ? am[k] : mine;
-  const BlockScale own = block_scale<CDT>(mine, pow2 != 0);
   BlockScale bs[NB];
+  if constexpr (LPB < NB) {
+    // 1x8 / 1x16: fewer lanes per block than blocks per lane; each lane
+    // computes its own NB scales
 #pragma unroll
-  for (int k = 0; k < NB; ++k) {
-    const int src = (lane & ~(LPB - 1)) | k;  // idle PAD lanes hold the group max too
-    bs[k].s = __shfl(own.s, src, 64);
-    bs[k].y = __shfl(own.y, src, 64);
-    bs[k].kind = __shfl(own.kind, src, 64);
+    for (int k = 0; k < NB; ++k) bs[k] = block_scale<CDT>(am[k], pow2 != 0);
+  } else {
+    // lane c computes the scale of block k = c % NB of its group; gather all NB
+    uint32_t mine = am[0];
+#pragma unroll
+    for (int k = 1; k < NB; ++k) mine = (c % NB) == k ? am[k] : mine;
+    const BlockScale own = block_scale<CDT>(mine, pow2 != 0);
+#pragma unroll
+    for (int k = 0; k < NB; ++k) {
+      const int src = (lane & ~(LPB - 1)) | k;  // idle PAD lanes hold the group max too
+      bs[k].s = __shfl(own.s, src, 64);
+      bs[k].y = __shfl(own.y, src, 64);
+      bs[k].kind = __shfl(own.kind, src, 64);
+    }
   }
 #pragma unroll
   for (int j = 0; j < NJ; ++j) {
@@ -277,7 +285,7 @@ __global__ __launch_bounds__(256) void k_row(Desc single, const Desc* __restrict
 }
 
 // ---------------------------------------------------------------------------
-// 1xB row blocks of float32 input (B = 32...1024): a lane's chunk is one
+// 1xB row blocks of float32 input (B = 8...1024): a lane's chunk is one
 // 16-byte load of 4 floats, so each wave instruction reads 1 KiB contiguous
 // (k_row's 8-element chunks of float32 take two loads at a 32-byte stride,
 // each instruction covering a 2 KiB span at half density).  A block spans
@@ -338,17 +346,23 @@ __global__ __launch_bounds__(256) void k_row_f32(Desc single, const Desc* __rest
     }
     am[k] = group_max<LPB>(a);
   }
-  uint32_t mine = am[0];
-#pragma unroll
-  for (int k = 1; k < NB; ++k) mine = (c % NB) == k ? am[k] : mine;
-  const BlockScale own = block_scale<kF32>(mine, pow2 != 0);
   BlockScale bs[NB];
+  if constexpr (LPB < NB) {
+    // 1x8: two lanes per block, each lane computes its own NB scales
 #pragma unroll
-  for (int k = 0; k < NB; ++k) {
-    const int src = (lane & ~(LPB - 1)) | k;
-    bs[k].s = __shfl(own.s, src, 64);
-    bs[k].y = __shfl(own.y, src, 64);
-    bs[k].kind = __shfl(own.kind, src, 64);
+    for (int k = 0; k < NB; ++k) bs[k] = block_scale<kF32>(am[k], pow2 != 0);
+  } else {
+    uint32_t mine = am[0];
+#pragma unroll
+    for (int k = 1; k < NB; ++k) mine = (c % NB) == k ? am[k] : mine;
+    const BlockScale own = block_scale<kF32>(mine, pow2 != 0);
+#pragma unroll
+    for (int k = 0; k < NB; ++k) {
+      const int src = (lane & ~(LPB - 1)) | k;
+      bs[k].s = __shfl(own.s, src, 64);
+      bs[k].y = __shfl(own.y, src, 64);
+      bs[k].kind = __shfl(own.kind, src, 64);
+    }
   }
 #pragma unroll
   for (int j = 0; j < NJ; ++j) {
@@ -451,6 +465,8 @@ static hipError_t launch_fp8_typed(const LaunchCfg& cfg, const Desc& single, con
     case kKernRowF32:
       if constexpr (DT == kF32) {
         switch (cfg.blk_c) {
+          case 8: hipLaunchKernelGGL((k_row_f32<2, 1>), grid, block, 0, stream, single, descs, map, cfg.pow2, cfg.scale_bf16); break;
+          case 16: hipLaunchKernelGGL((k_row_f32<4, 1>), grid, block, 0, stream, single, descs, map, cfg.pow2, cfg.scale_bf16); break;
           case 32: hipLaunchKernelGGL((k_row_f32<8, 1>), grid, block, 0, stream, single, descs, map, cfg.pow2, cfg.scale_bf16); break;
           case 64: hipLaunchKernelGGL((k_row_f32<16, 1>), grid, block, 0, stream, single, descs, map, cfg.pow2, cfg.scale_bf16); break;
           case 128: hipLaunchKernelGGL((k_row_f32<32, 1>), grid, block, 0, stream, single, descs, map, cfg.pow2, cfg.scale_bf16); break;
@@ -464,7 +480,11 @@ static hipError_t launch_fp8_typed(const LaunchCfg& cfg, const Desc& single, con
       return hipErrorInvalidValue;
     case kKernRowG: {
       const int g = cfg.blk_c / 8;  // 1..63, not a power of two of 4..64 lanes
-      if (g < 4)
+      if (g == 1)
+        hipLaunchKernelGGL((k_row<DT, CDT, 1>), grid, block, 0, stream, single, descs, map, cfg.pow2, cfg.scale_bf16, g);
+      else if (g == 2)
+        hipLaunchKernelGGL((k_row<DT, CDT, 2>), grid, block, 0, stream, single, descs, map, cfg.pow2, cfg.scale_bf16, g);
+      else if (g < 4)
         hipLaunchKernelGGL((k_row<DT, CDT, 4, true>), grid, block, 0, stream, single, descs, map, cfg.pow2, cfg.scale_bf16, g);
       else if (g < 8)
         hipLaunchKernelGGL((k_row<DT, CDT, 8, true>), grid, block, 0, stream, single, descs, map, cfg.pow2, cfg.scale_bf16, g);

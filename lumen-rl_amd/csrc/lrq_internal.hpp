@@ -40,9 +40,10 @@ enum Kernel : int {
   kKernF64 = 11,           // FP8 blocks of a float64 tensor in float64 arithmetic, one wave per block
   kKernF64Row = 12,        // dense 1xB float64 blocks (B = 32..512), 16-byte loads
   kKernF64Tile = 13,       // 128x128 float64 tiles, one 512-thread work-group per tile
-  kKernRowF32 = 15,        // 1xB FP8 blocks of float32 input (B = 32..1024), one 16-byte load per lane chunk
+  kKernRowF32 = 15,        // 1xB FP8 blocks of float32 input (B = 8..1024, a power of two), one 16-byte load per lane chunk
   kKernRowG = 14,          // 1xB FP8 blocks of 8 g elements, g = 1..63 not 4..64 a power of two: k_row
-                           // with g lanes of each next-power-of-two group (4 at least) active
+                           // with 1- or 2-lane groups (g = 1, 2), else g lanes of each
+                           // next-power-of-two group (4 at least) active
 };
 
 // Work per lane of the streaming kernels, shared by the kernels and the

@@ -143,6 +143,13 @@ def test_group_pack_rows_and_mx_units():
     # MX: 64 lanes of a wave, a quad per group, 2 groups per quad -> 128 groups per work-group
     assert L().lrq_group_units(buf.ctypes.data) == -(-256 * 128 // 128) + -(-64 * 384 // 128)
     del blocks
+    # other widths: 1x8 and 1x16 take 1- and 2-lane groups, wider ones the next
+    # power of two of B/8 lanes (4 at least); 4 waves x 4 instructions per work-group
+    for B, lanes in ((8, 1), (16, 2), (24, 4), (40, 8), (96, 16), (200, 32), (504, 64)):
+        shapes = [(1, 256, 16 * B), (1, 63, 3 * B)]
+        buf = _pack(_lib.FMT_FP8_BLOCK, shapes, (1, B))
+        per_wg = 4 * 4 * (64 // lanes)
+        assert L().lrq_group_units(buf.ctypes.data) == -(-256 * 16 // per_wg) + -(-63 * 3 // per_wg), B
 
 
 def test_group_pack_expert_stack_single_descriptor():
