@@ -138,6 +138,10 @@ int fp8_kernel_for(const Desc& d, int in_dtype, int64_t blk_r, int64_t blk_c) {
   if (blk_r == 1 && blk_c % 8 == 0 && blk_c <= 512 && d.cols % blk_c == 0 && vec &&
       (d.batch == 1 || d.bstride == d.rows * d.ld))
     return lrq::kKernRowG;
+  // wider blocks of 8 g elements: one wave per block up to 4096, four up to 16384
+  if (blk_r == 1 && blk_c % 8 == 0 && blk_c > 512 && blk_c <= 4 * 512 * lrq::kWideChunks &&
+      d.cols % blk_c == 0 && vec && (d.batch == 1 || d.bstride == d.rows * d.ld))
+    return lrq::kKernRowWide;
   return lrq::kKernGenericFp8;
 }
 
@@ -199,6 +203,15 @@ bool plan_units(const LaunchCfg& cfg, Desc& d) {
       d.nblocks = d.rows * d.bpr;
       const int64_t per_wg = cfg.blk_c <= 256 ? 4 * kRowBlocks * (256 / cfg.blk_c)
                                               : 4 * kRowBlocks / (cfg.blk_c / 256);
+      d.units = (d.nblocks + per_wg - 1) / per_wg;
+      return true;
+    }
+    case kKernRowWide: {  // 4 waves of P blocks each (B <= 4096), or one block of 4 waves
+      if (!fold_batch(d)) return false;
+      d.bpr = d.cols / cfg.blk_c;
+      d.nblocks = d.rows * d.bpr;
+      const int P = wide_blocks_per_wave(cfg.blk_c);
+      const int64_t per_wg = P > 0 ? 4 * P : 1;
       d.units = (d.nblocks + per_wg - 1) / per_wg;
       return true;
     }

@@ -3,13 +3,15 @@
 // Restates WeightQuantizer.quantize_tensor
 // (lumenrl/quantization/weight_quantizer.py:40-77): per block amax -> /448 ->
 // clamp(tiny) -> [pow2] -> x/s -> float8_e4m3fn, in one HBM pass (bf16 in,
-// e4m3 + scale out).  Three kernels:
+// e4m3 + scale out).  Four kernels:
 //   k_tile128  : 128x128 tiles (the vLLM/ATOM `weight_scale_inv` layout), one
 //                512-thread work-group per tile, the tile held in VGPRs;
 //                tiles handed to XCDs in runs of kXcdRunTile (xcd_unit).
 //   k_row      : 1xB row blocks (the reference's own layout), B/8 consecutive
 //                lanes per block so every wave instruction is one contiguous
 //                span; one scale computation per lane, shared by shuffles.
+//   k_row_wide : 1xB row blocks wider than 512 (but 1024 and 2048), one or
+//                four waves per block, the block held in VGPRs.
 //   k_generic  : any block shape, stride or alignment (one work-group per
 //                block, scalar loads); the fallback for odd inputs.
 // All of them share lrq_device.hpp's block_scale / block_quot / special_code.
@@ -384,6 +386,88 @@ __global__ __launch_bounds__(256) void k_row_f32(Desc single, const Desc* __rest
 }
 
 // ---------------------------------------------------------------------------
+// Wide 1xB row blocks, B = 8 g elements with 512 < B <= 16384 (other than
+// 1024 and 2048, which k_row takes): a block belongs to W waves of the
+// work-group (W = 1 up to B = 4096, else 4), whose lane l of wave w holds
+// chunks c = 64 w + l + 64 W k for k < K = ceil(g / 64W).  With W = 1 a wave
+// takes P consecutive blocks (P = 4, 2, 1 for K <= 2, 4, 8), so it keeps
+// about kWideChunks loads in flight per lane whatever the width.  Every wave
+// instruction of a block reads 1 KiB contiguous (of bf16), except the last
+// when 64 W does not divide g: its lanes past the end re-load chunk 0 of their
+// block (in bounds) and drop out of the amax.  The W waves' maxima meet in
+// LDS; the scale math then runs once per block.
+// ---------------------------------------------------------------------------
+template <int DT, int CDT, int W, int P>
+__global__ __launch_bounds__(256) void k_row_wide(Desc single, const Desc* __restrict__ descs,
+                                                  const uint32_t* __restrict__ map, int pow2,
+                                                  int scale_bf16, int g) {
+  static_assert(W == 1 || P == 1, "blocks of several waves: one block per wave group");
+  constexpr int KP = kWideChunks / P;  // chunk slots per block
+  __shared__ uint32_t red[4];
+  Desc d;
+  int64_t u;
+  pick_desc<kXcdRunRow>(single, descs, map, d, u);
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int K = (g + 64 * W - 1) / (64 * W);  // <= KP
+  const int64_t blk0 = (u * (4 / W) + wave / W) * P;
+  const int64_t B = 8 * (int64_t)g;
+  const int c0 = 64 * (wave % W) + lane;
+
+  bool live[P];
+  int64_t gb[P];
+  Chunk<DT> ch[P][KP];
+#pragma unroll
+  for (int p = 0; p < P; ++p) {
+    live[p] = blk0 + p < d.nblocks;  // the same for the W waves of a block
+    gb[p] = live[p] ? blk0 + p : d.nblocks - 1;
+    int64_t base;
+    if (d.ld == d.cols) {
+      base = gb[p] * B;
+    } else {
+      const int64_t row = gb[p] / d.bpr;
+      base = row * d.ld + (gb[p] - row * d.bpr) * B;
+    }
+#pragma unroll
+    for (int k = 0; k < KP; ++k) {
+      if (k < K) {
+        const int c = c0 + 64 * W * k;
+        load_chunk<DT>(ch[p][k], d.in, base + 8 * (c < g ? c : 0));
+      }
+    }
+  }
+  BlockScale bs[P];
+#pragma unroll
+  for (int p = 0; p < P; ++p) {
+    Amax<DT> am;
+    am.init();
+#pragma unroll
+    for (int k = 0; k < KP; ++k) {
+      if (k < K && c0 + 64 * W * k < g) am.add(ch[p][k]);
+    }
+    uint32_t a = group_max<64>(am.bits());
+    if constexpr (W > 1) {
+      if (lane == 0) red[wave] = a;
+      __syncthreads();
+      const int w0 = wave & ~(W - 1);
+#pragma unroll
+      for (int w = 0; w < W; ++w) a = red[w0 + w] > a ? red[w0 + w] : a;
+    }
+    a = __builtin_amdgcn_readfirstlane(a);  // block-uniform: scalar scale math
+    bs[p] = block_scale<CDT>(a, pow2 != 0);
+  }
+#pragma unroll
+  for (int p = 0; p < P; ++p) {
+    if (!live[p]) continue;
+    if (c0 == 0) store_scale<CDT>(d.scales, gb[p], bs[p].s, scale_bf16);
+#pragma unroll
+    for (int k = 0; k < KP; ++k) {
+      const int c = c0 + 64 * W * k;
+      if (k < K && c < g) store_nt(d.codes + gb[p] * B + 8 * c, encode_chunk<DT, CDT>(ch[p][k], bs[p]));
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
 // Generic: one work-group per block of any shape; scalar loads; edge blocks
 // partial.  Unit u = (b, tile row, tile col) row-major = the scale index.
 // ---------------------------------------------------------------------------
@@ -494,6 +578,16 @@ static hipError_t launch_fp8_typed(const LaunchCfg& cfg, const Desc& single, con
         hipLaunchKernelGGL((k_row<DT, CDT, 32, true>), grid, block, 0, stream, single, descs, map, cfg.pow2, cfg.scale_bf16, g);
       else
         hipLaunchKernelGGL((k_row<DT, CDT, 64, true>), grid, block, 0, stream, single, descs, map, cfg.pow2, cfg.scale_bf16, g);
+      break;
+    }
+    case kKernRowWide: {
+      const int g = (int)(cfg.blk_c / 8);
+      switch (wide_blocks_per_wave(cfg.blk_c)) {
+        case 4: hipLaunchKernelGGL((k_row_wide<DT, CDT, 1, 4>), grid, block, 0, stream, single, descs, map, cfg.pow2, cfg.scale_bf16, g); break;
+        case 2: hipLaunchKernelGGL((k_row_wide<DT, CDT, 1, 2>), grid, block, 0, stream, single, descs, map, cfg.pow2, cfg.scale_bf16, g); break;
+        case 1: hipLaunchKernelGGL((k_row_wide<DT, CDT, 1, 1>), grid, block, 0, stream, single, descs, map, cfg.pow2, cfg.scale_bf16, g); break;
+        default: hipLaunchKernelGGL((k_row_wide<DT, CDT, 4, 1>), grid, block, 0, stream, single, descs, map, cfg.pow2, cfg.scale_bf16, g); break;
+      }
       break;
     }
     case kKernGenericFp8:

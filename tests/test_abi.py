@@ -150,6 +150,12 @@ def test_group_pack_rows_and_mx_units():
         buf = _pack(_lib.FMT_FP8_BLOCK, shapes, (1, B))
         per_wg = 4 * 4 * (64 // lanes)
         assert L().lrq_group_units(buf.ctypes.data) == -(-256 * 16 // per_wg) + -(-63 * 3 // per_wg), B
+    # wider blocks: 4 waves of 4, 2 or 1 blocks (B <= 1024, 2048, 4096), or one
+    # block of 4 waves (B <= 16384); 1024 and 2048 stay on the row kernel
+    for B, per_wg in ((640, 16), (1032, 8), (1536, 8), (3072, 4), (4096, 4), (4104, 1), (16384, 1),
+                      (1024, 16 // 2), (2048, 16 // 4)):
+        buf = _pack(_lib.FMT_FP8_BLOCK, [(1, 256, 16 * B), (1, 63, 3 * B)], (1, B))
+        assert L().lrq_group_units(buf.ctypes.data) == -(-256 * 16 // per_wg) + -(-63 * 3 // per_wg), B
 
 
 def test_group_pack_expert_stack_single_descriptor():

@@ -1,12 +1,14 @@
-"""1xB blocks of widths that are not a power of two, on an MI355X.
+"""1xB blocks of widths that are not 32..512 powers of two, on an MI355X.
 
 ``quantize_tensor(tensor, block_size=B)`` takes any B dividing the last dim
-(weight_quantizer.py:40-77).  Widths B = 8 g up to 512 that are not 32..512
-powers of two run on the row kernel with lane groups padded to the next power
-of two (the last lanes of each group idle); 1024 and 2048 on the row kernel
-with a block spanning 2 or 4 wave instructions; the rest (36, 1536) on the
-generic kernel.  Every code and scale bit is compared with the oracle, and the
-drop-in with the reference's torch op sequence.
+(weight_quantizer.py:40-77).  Widths B = 8 g up to 512 run on the row kernel
+with 1- or 2-lane groups (8, 16) or lane groups padded to the next power of
+two (the last lanes of each group idle); 1024 and 2048 on the row kernel with
+a block spanning 2 or 4 wave instructions; other widths up to 16384 on the
+wide-row kernel, one wave per block up to 4096 (640, 1032, 1536, 4096) and
+four beyond (4104, 12288, 16384); the rest (36, 16392) on the generic kernel.
+Every code and scale bit is compared with the oracle, and the drop-in with the
+reference's torch op sequence.
 """
 
 from __future__ import annotations
@@ -26,7 +28,13 @@ if not torch.cuda.is_available():  # pragma: no cover - CPU container
 
 DEV = torch.device("cuda", 0)
 DT = {"bf16": torch.bfloat16, "f16": torch.float16, "f32": torch.float32}
-WIDTHS = [40, 48, 96, 120, 200, 248, 504, 8, 16, 24, 36, 1024, 2048, 1536]
+WIDTHS = [40, 48, 96, 120, 200, 248, 504, 8, 16, 24, 36, 1024, 2048, 1536,
+          640, 1032, 4096, 4104, 12288, 16384, 16392]
+# (rows, blocks per row, row pitch padding, pow2, bf16 scales when arith is f32)
+CASES = [(1, 1, 0, False, False), (37, 3, 0, True, False), (200, 5, 16, False, True),
+         (513, 2, 0, False, False), (64, 11, 8, True, False)]
+CASES_WIDE = [(1, 1, 0, False, False), (37, 3, 0, True, False), (90, 1, 16, False, True),
+              (129, 2, 0, False, False), (16, 5, 8, True, False)]
 
 
 def host(t: torch.Tensor, dt: str) -> np.ndarray:
@@ -49,9 +57,8 @@ def weights(rng, rows, cols, ld, dt):
 def test_width_vs_oracle(B, dt, arith):
     print("rowg", B, dt, arith, flush=True)
     rng = np.random.default_rng(B * 7 + len(dt) + len(arith))
-    for rows, mult, pitch, pow2, sbf16 in [(1, 1, 0, False, False), (37, 3, 0, True, False),
-                                          (200, 5, 16, False, arith == "f32"), (513, 2, 0, False, False),
-                                          (64, 11, 8, True, False)]:
+    for rows, mult, pitch, pow2, sbf16 in CASES if B <= 2048 else CASES_WIDE:
+        sbf16 = sbf16 and arith == "f32"
         cols = B * mult
         ld = cols + pitch
         if DT[dt].itemsize * ld % 16:
@@ -69,7 +76,7 @@ def test_width_vs_oracle(B, dt, arith):
         assert np.array_equal(got.reshape(-1), want.reshape(-1)), (B, rows, cols, ld)
 
 
-@pytest.mark.parametrize("B", [96, 40, 200])
+@pytest.mark.parametrize("B", [96, 40, 200, 8, 1536, 4104])
 def test_grouped_plan_and_expert_stacks(B):
     print("rowg grouped", B, flush=True)
     rng = np.random.default_rng(B)
