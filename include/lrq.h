@@ -136,7 +136,7 @@ int lrq_mxfp4_quant(const void* in, int in_dtype, int64_t rows, int64_t cols, in
  * pow2 (LRQ_FLAG_POW2_SCALE = FP8Config.use_activation_pow2_scale), and
  * out = float32(x / s) * s.  Replaces the activation ops of
  * _FP8W8A8Linear.forward (lumenrl/quantization/fp8_rollout.py:53-72).
- *   in  : [rows, cols] in_dtype, row stride ld (4-element aligned);
+ *   in  : [rows, cols] in_dtype, element-aligned, any row stride ld;
  *   out : [rows, cols] float32, dense, 16-byte aligned;  blk in {32,64,128,256}.
  */
 int lrq_act_qdq(const void* in, int in_dtype, int64_t rows, int64_t cols, int64_t ld, int64_t blk,
@@ -148,8 +148,9 @@ int lrq_act_qdq(const void* in, int in_dtype, int64_t rows, int64_t cols, int64_
  * 448, +-inf and NaN -> NaN (0x7F | sign).  Replaces the FP8 path of
  * DynamicWeightLoader (lumenrl/engine/inference/weight_loader.py:19-43,
  * `_maybe_fp8_quantize_tensor`); a whole state dict goes through one grouped
- * launch with LRQ_FMT_CAST_E4M3.  Any alignment; a 16-byte aligned input with
- * codes aligned to 8 bytes (4 for float32 input) takes the vector path.
+ * launch with LRQ_FMT_CAST_E4M3.  Any alignment; codes aligned to 8 bytes (4
+ * for float32 input) take the vector path, whose 16-byte loads take any
+ * element-aligned input.
  */
 int lrq_cast_e4m3(const void* in, int in_dtype, int64_t n, uint8_t* out, lrq_stream_t stream);
 

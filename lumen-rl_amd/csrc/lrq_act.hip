@@ -28,20 +28,10 @@ __device__ __forceinline__ float x86_div(float x, float s) {
   return x / s;
 }
 
-template <int DT>
+// 4 float32 elements (one 16-byte load; 4-byte alignment suffices)
 __device__ __forceinline__ void load4(const void* base, int64_t off, float (&x)[4]) {
-  if constexpr (DT == kF32) {
-    const v4u v = load_nt(static_cast<const float*>(base) + off);
-    x[0] = u2f(v.x); x[1] = u2f(v.y); x[2] = u2f(v.z); x[3] = u2f(v.w);
-  } else {
-    const v2u v = __builtin_nontemporal_load(reinterpret_cast<const v2u*>(static_cast<const uint16_t*>(base) + off));
-    if constexpr (DT == kBF16) {
-      x[0] = bf16_lo(v.x); x[1] = bf16_hi(v.x); x[2] = bf16_lo(v.y); x[3] = bf16_hi(v.y);
-    } else {
-      x[0] = f16_to_f32(v.x & 0xFFFFu); x[1] = f16_to_f32(v.x >> 16);
-      x[2] = f16_to_f32(v.y & 0xFFFFu); x[3] = f16_to_f32(v.y >> 16);
-    }
-  }
+  const v4u v = load_nt(static_cast<const float*>(base) + off);
+  x[0] = u2f(v.x); x[1] = u2f(v.y); x[2] = u2f(v.z); x[3] = u2f(v.w);
 }
 
 // Shared by both kernels: the [rows, cols] matrix is walked as its row-major
@@ -93,7 +83,7 @@ __global__ __launch_bounds__(256) void k_act_qdq8(const uint16_t* __restrict__ i
   const int64_t span = xcd_unit<kXcdRunStream>(blockIdx.x, gridDim.x) * 2048 + (threadIdx.x >> 6) * 512;
   const int64_t e = span + 8 * lane;
   v4u v = {0u, 0u, 0u, 0u};
-  if (e < n) v = __builtin_nontemporal_load(reinterpret_cast<const v4u*>(in + act_offset(e, cols, ld, DENSE)));
+  if (e < n) v = load_nt(in + act_offset(e, cols, ld, DENSE));
   const uint32_t w[4] = {v.x, v.y, v.z, v.w};
   float x[8];
 #pragma unroll
@@ -125,11 +115,11 @@ __global__ __launch_bounds__(256) void k_act_qdq8(const uint16_t* __restrict__ i
   }
 }
 
-// Any input dtype, 4 elements per lane, NCH 1024-element chunks per
+// Float32 input, 4 elements per lane, NCH 1024-element chunks per
 // work-group: in chunk j lane t holds elements 1024j + 4t .. +3, so each wave
 // load reads one contiguous span and each store writes 1 KiB.  All NCH loads
 // are issued before the first reduction.
-template <int DT, int LPB, int NCH, bool DENSE>
+template <int LPB, int NCH, bool DENSE>
 __global__ __launch_bounds__(256) void k_act_qdq(const void* __restrict__ in, int64_t rows, int64_t cols,
                                                  int64_t ld, float* __restrict__ out, int pow2) {
   const int64_t n = rows * cols;
@@ -139,7 +129,7 @@ __global__ __launch_bounds__(256) void k_act_qdq(const void* __restrict__ in, in
   for (int j = 0; j < NCH; ++j) {
     const int64_t e = base + 1024 * j;
     x[j][0] = x[j][1] = x[j][2] = x[j][3] = 0.0f;
-    if (e < n) load4<DT>(in, act_offset(e, cols, ld, DENSE), x[j]);
+    if (e < n) load4(in, act_offset(e, cols, ld, DENSE), x[j]);
   }
 #pragma unroll
   for (int j = 0; j < NCH; ++j) {
@@ -154,14 +144,13 @@ __global__ __launch_bounds__(256) void k_act_qdq(const void* __restrict__ in, in
 
 constexpr int kActChunks = 2;
 
-// True when the 8-per-lane kernel applies: 16-bit input whose rows start on
-// 16-byte boundaries.
-static bool act_wide(const void* in, int dtype, int64_t rows, int64_t ld) {
-  return dtype != kF32 && ((uintptr_t)in % 16u) == 0 && (rows == 1 || ld % 8 == 0);
-}
-
+// 16-bit input takes the 8-per-lane kernel (any element alignment and row
+// pitch: its 16-byte loads take 2-byte-aligned addresses), float32 the
+// 4-per-lane one.
 int64_t act_grid(const void* in, int dtype, int64_t rows, int64_t cols, int64_t ld) {
-  const int64_t per_wg = act_wide(in, dtype, rows, ld) ? 2048 : 1024 * kActChunks;
+  (void)in;
+  (void)ld;
+  const int64_t per_wg = dtype != kF32 ? 2048 : 1024 * kActChunks;
   return (rows * cols + per_wg - 1) / per_wg;
 }
 
@@ -171,23 +160,21 @@ static hipError_t launch_act_typed(const void* in, int64_t rows, int64_t cols, i
   const dim3 grid((unsigned)act_grid(in, DT, rows, cols, ld)), block(256);
   const uint16_t* in16 = static_cast<const uint16_t*>(in);
   if constexpr (DT != kF32) {
-    if (act_wide(in, DT, rows, ld)) {
-      switch (blk) {
-        case 32: hipLaunchKernelGGL((k_act_qdq8<DT, 4, DENSE>), grid, block, 0, stream, in16, rows, cols, ld, out, pow2); break;
-        case 64: hipLaunchKernelGGL((k_act_qdq8<DT, 8, DENSE>), grid, block, 0, stream, in16, rows, cols, ld, out, pow2); break;
-        case 128: hipLaunchKernelGGL((k_act_qdq8<DT, 16, DENSE>), grid, block, 0, stream, in16, rows, cols, ld, out, pow2); break;
-        case 256: hipLaunchKernelGGL((k_act_qdq8<DT, 32, DENSE>), grid, block, 0, stream, in16, rows, cols, ld, out, pow2); break;
-        default: return hipErrorInvalidValue;
-      }
-      return hipGetLastError();
+    switch (blk) {
+      case 32: hipLaunchKernelGGL((k_act_qdq8<DT, 4, DENSE>), grid, block, 0, stream, in16, rows, cols, ld, out, pow2); break;
+      case 64: hipLaunchKernelGGL((k_act_qdq8<DT, 8, DENSE>), grid, block, 0, stream, in16, rows, cols, ld, out, pow2); break;
+      case 128: hipLaunchKernelGGL((k_act_qdq8<DT, 16, DENSE>), grid, block, 0, stream, in16, rows, cols, ld, out, pow2); break;
+      case 256: hipLaunchKernelGGL((k_act_qdq8<DT, 32, DENSE>), grid, block, 0, stream, in16, rows, cols, ld, out, pow2); break;
+      default: return hipErrorInvalidValue;
     }
-  }
-  switch (blk) {
-    case 32: hipLaunchKernelGGL((k_act_qdq<DT, 8, kActChunks, DENSE>), grid, block, 0, stream, in, rows, cols, ld, out, pow2); break;
-    case 64: hipLaunchKernelGGL((k_act_qdq<DT, 16, kActChunks, DENSE>), grid, block, 0, stream, in, rows, cols, ld, out, pow2); break;
-    case 128: hipLaunchKernelGGL((k_act_qdq<DT, 32, kActChunks, DENSE>), grid, block, 0, stream, in, rows, cols, ld, out, pow2); break;
-    case 256: hipLaunchKernelGGL((k_act_qdq<DT, 64, kActChunks, DENSE>), grid, block, 0, stream, in, rows, cols, ld, out, pow2); break;
-    default: return hipErrorInvalidValue;
+  } else {
+    switch (blk) {
+      case 32: hipLaunchKernelGGL((k_act_qdq<8, kActChunks, DENSE>), grid, block, 0, stream, in, rows, cols, ld, out, pow2); break;
+      case 64: hipLaunchKernelGGL((k_act_qdq<16, kActChunks, DENSE>), grid, block, 0, stream, in, rows, cols, ld, out, pow2); break;
+      case 128: hipLaunchKernelGGL((k_act_qdq<32, kActChunks, DENSE>), grid, block, 0, stream, in, rows, cols, ld, out, pow2); break;
+      case 256: hipLaunchKernelGGL((k_act_qdq<64, kActChunks, DENSE>), grid, block, 0, stream, in, rows, cols, ld, out, pow2); break;
+      default: return hipErrorInvalidValue;
+    }
   }
   return hipGetLastError();
 }

@@ -114,18 +114,17 @@ bool fold_batch(Desc& d) {
 int fp8_kernel_for(const Desc& d, int in_dtype, int64_t blk_r, int64_t blk_c) {
   if (in_dtype == lrq::kF64) {
     const bool row = blk_r == 1 && pow2_block(blk_c) && d.cols % blk_c == 0 && d.ld == d.cols &&
-                     (d.batch == 1 || d.bstride == d.rows * d.ld) && aligned(d.in, 16) &&
+                     (d.batch == 1 || d.bstride == d.rows * d.ld) && aligned(d.in, 8) &&
                      aligned(d.codes, 2) && aligned(d.scales, 8);
     if (row) return lrq::kKernF64Row;
-    const bool tile = blk_r == 128 && blk_c == 128 && aligned(d.in, 16) && d.ld % 2 == 0 &&
-                      (d.batch == 1 || d.bstride % 2 == 0) && d.cols % 2 == 0 &&
+    const bool tile = blk_r == 128 && blk_c == 128 && aligned(d.in, 8) && d.cols % 2 == 0 &&
                       aligned(d.codes, 2) && aligned(d.scales, 8);
     return tile ? lrq::kKernF64Tile : lrq::kKernF64;
   }
   const int64_t es = esize(in_dtype);
-  const bool vec = aligned(d.in, 16) && (d.ld * es) % 16 == 0 &&
-                   (d.batch == 1 || (d.bstride * es) % 16 == 0) && aligned(d.codes, 8) &&
-                   d.cols % 8 == 0;
+  // input loads take element-aligned addresses (any row pitch); chunks of 8
+  // elements stay inside a row
+  const bool vec = aligned(d.in, (uintptr_t)es) && aligned(d.codes, 8) && d.cols % 8 == 0;
   if (blk_r == 128 && blk_c == 128 && vec) return lrq::kKernTile128;
   if (in_dtype == lrq::kF32 && blk_r == 1 && (pow2_block(blk_c) || blk_c == 8 || blk_c == 16 || blk_c == 1024) &&
       d.cols % blk_c == 0 && vec && aligned(d.codes, 4) && (d.batch == 1 || d.bstride == d.rows * d.ld))
@@ -152,8 +151,7 @@ int dequant_kernel_for(const Desc& d, int64_t blk_c) {
 
 int mx_kernel_for(const Desc& d, int in_dtype, int fmt) {
   const int64_t es = esize(in_dtype);
-  const bool vec = aligned(d.in, 16) && (d.ld * es) % 16 == 0 &&
-                   (d.batch == 1 || d.bstride == d.rows * d.ld) &&
+  const bool vec = aligned(d.in, (uintptr_t)es) && (d.batch == 1 || d.bstride == d.rows * d.ld) &&
                    aligned(d.codes, fmt == 8 ? 8 : 4);
   return vec ? lrq::kKernMx : lrq::kKernGenericMx;
 }
@@ -401,7 +399,7 @@ int plan_group(int fmt, const lrq_tensor* ts, int64_t n, int in_dtype, int64_t b
       if (d.batch > 1 || d.rows > 1 || (d.cols > 0 && d.ld != d.cols))
         return fail(LRQ_ERR_ARG, "tensor %lld: a cast entry is one contiguous run (batch = rows = 1)", (long long)i);
       const int64_t es = esize(in_dtype);
-      d.units_c = aligned(d.in, 16) && aligned(d.codes, es == 4 ? 4 : 8) ? 1 : 0;
+      d.units_c = aligned(d.in, (uintptr_t)es) && aligned(d.codes, es == 4 ? 4 : 8) ? 1 : 0;
       d.units = (d.cols + lrq::kCastUnit - 1) / lrq::kCastUnit;
       d.unit0 = units;
       units += d.units;
@@ -424,8 +422,7 @@ int plan_group(int fmt, const lrq_tensor* ts, int64_t n, int in_dtype, int64_t b
         return fail(LRQ_ERR_ARG, "tensor %lld is empty: a max over no elements is undefined", (long long)i);
       if (!aligned(d.scales, 4)) return fail(LRQ_ERR_ALIGN, "tensor %lld: scale not 4-byte aligned", (long long)i);
       const int64_t es = esize(in_dtype);
-      const bool vec = aligned(d.in, 16) && (d.ld * es) % 16 == 0 && d.cols % (16 / es) == 0 &&
-                       (d.batch == 1 || (d.bstride * es) % 16 == 0);
+      const bool vec = aligned(d.in, (uintptr_t)es) && d.cols % (16 / es) == 0;
       const bool dense = d.ld == d.cols && (d.batch == 1 || d.bstride == d.rows * d.cols);
       d.units_c = vec ? 1 : 0;
       d.units_r = dense ? 1 : 0;
@@ -541,8 +538,8 @@ int lrq_act_qdq(const void* in, int in_dtype, int64_t rows, int64_t cols, int64_
   if (ld < cols) return fail(LRQ_ERR_ARG, "ld < cols");
   if (!in || !out) return fail(LRQ_ERR_ARG, "null pointer");
   const int64_t es = esize(in_dtype);
-  if (!aligned(in, (uintptr_t)(4 * es)) || (ld * es) % (4 * es) != 0 || !aligned(out, 16))
-    return fail(LRQ_ERR_ALIGN, "activation rows must be aligned to 4 elements, out to 16 bytes");
+  if (!aligned(in, (uintptr_t)es) || !aligned(out, 16))
+    return fail(LRQ_ERR_ALIGN, "activation input must be element-aligned, out 16-byte aligned");
   if (lrq::act_grid(in, in_dtype, rows, cols, ld) > kMaxGrid) return fail(LRQ_ERR_ARG, "tensor too large for one launch");
   return check_hip(lrq::launch_act(in, in_dtype, rows, cols, ld, blk, out,
                                    (flags & LRQ_FLAG_POW2_SCALE) ? 1 : 0, (hipStream_t)stream),

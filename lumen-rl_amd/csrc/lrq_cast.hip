@@ -12,9 +12,9 @@
 // A work-group converts one unit of kCastUnit elements of one tensor: 16
 // elements per lane in 16-byte nontemporal loads, lane-interleaved so every
 // wave instruction reads one contiguous span and writes whole code lines.
-// Tensors whose input is not 16-byte aligned or whose codes are not aligned
-// to one chunk of codes (8 bytes for 16-bit inputs, 4 for float32) take an
-// element-wise walk of the same unit; the last n % (elements per load) of a
+// The 16-byte loads take any element-aligned input; tensors whose codes are
+// not aligned to one chunk of codes (8 bytes for 16-bit inputs, 4 for
+// float32) take an element-wise walk of the same unit; the last n % (elements per load) of a
 // tensor are converted element-wise by the unit that holds them.
 #include <string.h>
 

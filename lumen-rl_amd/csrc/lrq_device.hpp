@@ -284,7 +284,16 @@ template <class T>
 __device__ __forceinline__ void gst_nt(void* p, T v) {
   __builtin_nontemporal_store(v, (LRQ_GLOBAL T*)p);
 }
-__device__ __forceinline__ v4u load_nt(const void* p) { return gld_nt<v4u>(p); }
+// Input loads take element-aligned addresses (2 bytes suffice): under the HSA
+// ABI the hardware runs in unaligned-access mode (LLVM enables
+// unaligned-access-mode for amdhsa targets), so a 16-byte load from a 2-byte
+// aligned address is still one global_load_dwordx4, split by the memory
+// pipeline where it crosses a cache line.  Aligned addresses compile to the
+// same instruction as a 16-byte-aligned type would.
+typedef unsigned int v4u_in __attribute__((ext_vector_type(4), aligned(2)));
+__device__ __forceinline__ v4u load_nt(const void* p) {
+  return __builtin_nontemporal_load((const LRQ_GLOBAL v4u_in*)p);
+}
 __device__ __forceinline__ void store_nt(void* p, v2u v) { gst_nt<v2u>(p, v); }
 __device__ __forceinline__ void store_nt(void* p, uint32_t v) { gst_nt<uint32_t>(p, v); }
 

@@ -92,9 +92,9 @@ __device__ __forceinline__ uint32_t block_reduce_max(uint32_t v, uint32_t* lds) 
 }
 
 // Max |x| bit pattern (float32 order) over this lane's part of unit u.
-// VEC: 16-byte loads (16-byte aligned rows and cols a multiple of the 16-byte
-// element count); DENSE: the tensor is one contiguous run.  Otherwise the
-// lane walks single elements.
+// VEC: 16-byte loads (element-aligned input, any row pitch, cols a multiple of
+// the 16-byte element count); DENSE: the tensor is one contiguous run.
+// Otherwise the lane walks single elements.
 template <int DT, bool VEC, bool DENSE>
 __device__ __forceinline__ uint32_t lane_amax(const Desc& d, int64_t u) {
   const int64_t n = d.batch * d.rows * d.cols;

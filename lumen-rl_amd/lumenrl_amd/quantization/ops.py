@@ -195,7 +195,7 @@ def act_qdq(x: Tensor, block: int = 128, *, pow2: bool = False,
     last = x.shape[-1]
     rows = x.numel() // last if last else 0
     xm = x.reshape(rows, last)
-    if xm.stride(-1) != 1 or (rows > 1 and xm.stride(0) % 4 != 0) or xm.data_ptr() % (4 * x.element_size()):
+    if xm.stride(-1) != 1:  # any row pitch and element alignment, but unit-stride rows
         xm = xm.contiguous()
     if out is None:
         out = torch.empty((rows, last), dtype=torch.float32, device=x.device)
@@ -584,8 +584,8 @@ class QuantPlan:
     ``run(inputs=...)``; they must have the planned shapes and dtype.  The
     outputs stay the same tensors across re-binds.
 
-    Inputs must be device tensors with 16-byte aligned rows (every torch
-    allocation of a [N, K] weight with K % 8 == 0 qualifies).  float64 weights
+    Inputs are device tensors with K % 8 == 0 (any element-aligned view, any
+    row pitch: the kernels' 16-byte loads take 2-byte-aligned addresses).  float64 weights
     take ``fmt="fp8_block"`` with ``native_arith=True`` (float64 arithmetic and
     scales, as ``quantize_tensor`` on a float64 tensor).
     """

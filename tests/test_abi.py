@@ -165,7 +165,9 @@ def test_group_pack_expert_stack_single_descriptor():
 
 def test_group_pack_rejects_mixed_kernels_and_small_buffers():
     ts = _tensors([(1, 256, 256), (1, 256, 256)])
-    ts[1].in_ = ts[1].in_ + 2  # misaligned: needs the generic kernel
+    ts[1].in_ = ts[1].in_ + 2  # element-aligned, off 16 bytes: the same tile kernel
+    assert L().lrq_group_table_bytes(_lib.FMT_FP8_BLOCK, ts, 2, 0, 128, 128, 0) > 0, _lib.last_error()
+    ts[1].codes = ts[1].codes + 1  # codes off a lane's 8-byte chunk: the generic kernel
     need = L().lrq_group_table_bytes(_lib.FMT_FP8_BLOCK, ts, 2, 0, 128, 128, 0)
     assert need == _lib.ERR_ARG and "kernel" in _lib.last_error()
     ts = _tensors([(1, 256, 256)])
@@ -182,7 +184,7 @@ def test_tensor_scale_tables():
     ts = _tensors(qkv + [(1, 300, 100)])
     for t in ts:
         t.codes = None
-    ts[3].in_ = ts[3].in_ + 2  # misaligned: element walk
+    ts[3].in_ = ts[3].in_ + 2  # 100 columns (not whole 16-byte chunks): element walk
     fmt = _lib.FMT_TENSOR_SCALE
     need = L().lrq_group_table_bytes(fmt, ts, 4, 0, 1, 1, 0)
     assert need > 0, _lib.last_error()

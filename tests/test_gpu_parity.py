@@ -280,9 +280,9 @@ def test_ragged_tiles_and_strided_views():
     big = weights((520, 1100)).to(DEV)
     say("ragged tiles")
     assert_fp8_matches_oracle(big[:300, :392], (128, 128))        # strided (ld=1100), fast path
-    assert_fp8_matches_oracle(big[:300, 1:393], (128, 128))       # misaligned -> generic
+    assert_fp8_matches_oracle(big[:300, 1:393], (128, 128))       # 2-byte aligned rows, tile kernel
     assert_fp8_matches_oracle(big[:256, 8:520], (1, 128))         # strided rows, fast path
-    assert_fp8_matches_oracle(big[:256, 3:515], (1, 128))         # misaligned -> generic
+    assert_fp8_matches_oracle(big[:256, 3:515], (1, 128))         # 2-byte aligned rows, row kernel
     c1, s1 = ops.fp8_block_quant(big[:256, 8:520], (1, 128))
     c2, s2 = ops.fp8_block_quant(big[:256, 8:520].contiguous(), (1, 128))
     assert torch.equal(u8t(c1), u8t(c2)) and torch.equal(s1, s2)
@@ -365,7 +365,7 @@ def test_mx_random_and_strided(fmt, dt):
         oc, osc = O.mx_quant(host_bits(xd.contiguous()), dt, fmt)
         assert np.array_equal(u8(s), osc), tag
         assert np.array_equal(u8(c), oc), tag
-    # misaligned view -> generic MX kernel
+    # a view off its 16-byte alignment (2-byte aligned rows): the vector MX kernel
     big = torch.cat([x, x], 1).to(DEV)
     xv = big[:, 1:1025 - 0][:, :992]
     c, s = fn(xv)
