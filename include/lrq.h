@@ -98,6 +98,9 @@ typedef struct ihipStream_t* lrq_stream_t; /* == hipStream_t */
  *             the input dtype with LRQ_FLAG_NATIVE_ARITH (16-bit words, or float64
  *             for LRQ_DTYPE_F64), or bf16 with LRQ_FLAG_SCALE_BF16.  Edge blocks
  *             may be partial.
+ * in needs element alignment only (any ld): with codes aligned to 8 bytes and
+ * cols % 8 == 0, 128x128 tiles and 1xB blocks of B = 8g <= 16384 run on the
+ * vector kernels; other shapes and alignments on the generic kernel.
  * Bit-exact with the reference evaluated by torch on x86, including NaN, inf,
  * all-zero and subnormal blocks.
  */
@@ -123,7 +126,9 @@ int lrq_fp8_block_dequant(const uint8_t* codes, const void* scales, int scale_dt
  * reference delegates MX to absent aiter/vLLM code:
  * examples/DAPO/atom_aiter_shim/sitecustomize.py:31-32,
  * examples/Qwen3_8B_SDDD_MI350_vLLM/configs/opd_qwen3_8b.yaml:43); the rules
- * are OCP MX v1.0 with round-to-nearest-even and saturation.
+ * are OCP MX v1.0 with round-to-nearest-even and saturation.  in needs element
+ * alignment only (any ld); codes aligned to 8 bytes (MXFP8) or 4 (MXFP4) take
+ * the vector kernel, others the generic one.
  */
 int lrq_mxfp8_quant(const void* in, int in_dtype, int64_t rows, int64_t cols, int64_t ld,
                     uint8_t* codes, uint8_t* scales, lrq_stream_t stream);
