@@ -122,8 +122,11 @@ int fp8_kernel_for(const Desc& d, int in_dtype, int64_t blk_r, int64_t blk_c) {
     return tile ? lrq::kKernF64Tile : lrq::kKernF64;
   }
   const int64_t es = esize(in_dtype);
-  // input loads take element-aligned addresses (any row pitch); chunks of 8
-  // elements stay inside a row
+  // input loads take element-aligned addresses (any row pitch); the tile
+  // kernel's chunks of 8 elements stay inside a row, and 1xB blocks hold
+  // ceil(B/8) chunks whose last one may overlap its neighbour
+  const bool vec_row = aligned(d.in, (uintptr_t)es) && aligned(d.codes, 8) &&
+                       (d.batch == 1 || d.bstride == d.rows * d.ld);
   const bool vec = aligned(d.in, (uintptr_t)es) && aligned(d.codes, 8) && d.cols % 8 == 0;
   if (blk_r == 128 && blk_c == 128 && vec) return lrq::kKernTile128;
   if (in_dtype == lrq::kF32 && blk_r == 1 && (pow2_block(blk_c) || blk_c == 8 || blk_c == 16 || blk_c == 1024) &&
@@ -132,14 +135,12 @@ int fp8_kernel_for(const Desc& d, int in_dtype, int64_t blk_r, int64_t blk_c) {
   if (blk_r == 1 && row_block(blk_c) && d.cols % blk_c == 0 && vec &&
       (d.batch == 1 || d.bstride == d.rows * d.ld))
     return lrq::kKernRowQuad;
-  // other widths of 8 g elements up to 512 (g = 1..63): 1- and 2-lane groups,
-  // padded lane groups beyond
-  if (blk_r == 1 && blk_c % 8 == 0 && blk_c <= 512 && d.cols % blk_c == 0 && vec &&
-      (d.batch == 1 || d.bstride == d.rows * d.ld))
+  // other widths 8..512: 1- and 2-lane groups (1x8, 1x16), padded lane groups
+  // of ceil(B/8) chunks beyond
+  if (blk_r == 1 && blk_c >= 8 && blk_c <= 512 && d.cols % blk_c == 0 && vec_row)
     return lrq::kKernRowG;
-  // wider blocks of 8 g elements: one wave per block up to 4096, four up to 16384
-  if (blk_r == 1 && blk_c % 8 == 0 && blk_c > 512 && blk_c <= 4 * 512 * lrq::kWideChunks &&
-      d.cols % blk_c == 0 && vec && (d.batch == 1 || d.bstride == d.rows * d.ld))
+  // wider blocks: one wave per block up to 4096, four up to 16384
+  if (blk_r == 1 && blk_c > 512 && blk_c <= 4 * 512 * lrq::kWideChunks && d.cols % blk_c == 0 && vec_row)
     return lrq::kKernRowWide;
   return lrq::kKernGenericFp8;
 }
@@ -217,8 +218,8 @@ bool plan_units(const LaunchCfg& cfg, Desc& d) {
       if (!fold_batch(d)) return false;
       d.bpr = d.cols / cfg.blk_c;
       d.nblocks = d.rows * d.bpr;
-      int64_t lanes = 1;  // a block's lane group: 1, 2, or the next power of two of blk_c / 8
-      while (lanes < cfg.blk_c / 8) lanes *= 2;
+      int64_t lanes = 1;  // a block's lane group: the next power of two of ceil(blk_c / 8)
+      while (lanes < (cfg.blk_c + 7) / 8) lanes *= 2;
       const int64_t per_wg = 4 * kRowBlocks * (64 / lanes);
       d.units = (d.nblocks + per_wg - 1) / per_wg;
       return true;
@@ -323,7 +324,8 @@ __global__ __launch_bounds__(256) void k_build_map(const Desc* __restrict__ desc
 // Build the launch configuration and descriptors for a group; `ds` may be null
 // (sizing only).  Returns 0 or an error; *units_out = total work-groups.
 int plan_group(int fmt, const lrq_tensor* ts, int64_t n, int in_dtype, int64_t blk_r,
-               int64_t blk_c, unsigned flags, LaunchCfg* cfg_out, Desc* ds, int64_t* units_out) {
+               int64_t blk_c, unsigned flags, LaunchCfg* cfg_out, Desc* ds, int64_t* units_out,
+               bool limit = true) {
   if (n < 0 || (n > 0 && !ts)) return fail(LRQ_ERR_ARG, "bad tensor list");
   if (n > 0xFFFFFFFFll) return fail(LRQ_ERR_ARG, "more than 2^32 tensors in one table");  // uint32 map
   if (in_dtype == lrq::kF64) {
@@ -471,7 +473,7 @@ int plan_group(int fmt, const lrq_tensor* ts, int64_t n, int in_dtype, int64_t b
     for (int64_t i = 0; i < n; ++i)
       if (ts[i].cols % blk_c != 0) cfg.rows_dense = 0;
   }
-  if (units > max_units(cfg.kernel)) return fail(LRQ_ERR_ARG, "group too large for one launch");
+  if (limit && units > max_units(cfg.kernel)) return fail(LRQ_ERR_ARG, "group too large for one launch");
   *cfg_out = cfg;
   *units_out = units;
   return 0;
@@ -489,9 +491,40 @@ int lrq_fp8_block_quant(const void* in, int in_dtype, int64_t batch, int64_t row
   LaunchCfg cfg;
   Desc d;
   int64_t units;
-  if (int rc = plan_group(LRQ_FMT_FP8_BLOCK, &t, 1, in_dtype, blk_r, blk_c, flags, &cfg, &d, &units))
+  if (int rc = plan_group(LRQ_FMT_FP8_BLOCK, &t, 1, in_dtype, blk_r, blk_c, flags, &cfg, &d, &units,
+                          /*limit=*/false))
     return rc;
   if (units == 0) return 0;
+  if (units > max_units(cfg.kernel)) {
+    // More work-groups than one launch takes (small blocks on the one-block-per-
+    // work-group generic kernel): one launch per matrix, then per band of rows
+    // (whole block rows), each re-planned on its own.
+    const int64_t es = esize(in_dtype);
+    const int64_t ses = in_dtype == lrq::kF64 ? 8
+                        : (flags & LRQ_FLAG_NATIVE_ARITH) && in_dtype != lrq::kF32 ? 2
+                        : (flags & LRQ_FLAG_SCALE_BF16) ? 2 : 4;
+    const int64_t srows = (rows + blk_r - 1) / blk_r, scols = (cols + blk_c - 1) / blk_c;
+    auto* in8 = static_cast<const uint8_t*>(in);
+    auto* sc8 = static_cast<uint8_t*>(scales);
+    if (batch > 1) {
+      for (int64_t b = 0; b < batch; ++b)
+        if (int rc = lrq_fp8_block_quant(in8 + b * batch_stride * es, in_dtype, 1, rows, cols, ld, rows * ld,
+                                         blk_r, blk_c, codes + b * rows * cols, sc8 + b * srows * scols * ses,
+                                         flags, stream))
+          return rc;
+      return 0;
+    }
+    const int64_t parts = units / max_units(cfg.kernel) + 2;
+    const int64_t band = (srows + parts - 1) / parts * blk_r;  // rows per launch
+    if (band >= rows) return fail(LRQ_ERR_ARG, "one row of blocks exceeds a launch");
+    for (int64_t r0 = 0; r0 < rows; r0 += band) {
+      const int64_t nr = rows - r0 < band ? rows - r0 : band;
+      if (int rc = lrq_fp8_block_quant(in8 + r0 * ld * es, in_dtype, 1, nr, cols, ld, nr * ld, blk_r, blk_c,
+                                       codes + r0 * cols, sc8 + (r0 / blk_r) * scols * ses, flags, stream))
+        return rc;
+    }
+    return 0;
+  }
   d.unit0 = 0;
   return check_hip(lrq::launch(cfg, d, nullptr, nullptr, units, (hipStream_t)stream), "kernel launch");
 }

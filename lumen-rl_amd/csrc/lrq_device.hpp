@@ -294,8 +294,16 @@ typedef unsigned int v4u_in __attribute__((ext_vector_type(4), aligned(2)));
 __device__ __forceinline__ v4u load_nt(const void* p) {
   return __builtin_nontemporal_load((const LRQ_GLOBAL v4u_in*)p);
 }
-__device__ __forceinline__ void store_nt(void* p, v2u v) { gst_nt<v2u>(p, v); }
-__device__ __forceinline__ void store_nt(void* p, uint32_t v) { gst_nt<uint32_t>(p, v); }
+// Code stores take any byte alignment, in the same unaligned-access mode: the
+// row kernels write blocks whose width is not a multiple of 8 at odd offsets.
+typedef unsigned int v2u_out __attribute__((ext_vector_type(2), aligned(1)));
+typedef unsigned int u32_out __attribute__((aligned(1)));
+__device__ __forceinline__ void store_nt(void* p, v2u v) {
+  __builtin_nontemporal_store(v, (LRQ_GLOBAL v2u_out*)p);
+}
+__device__ __forceinline__ void store_nt(void* p, uint32_t v) {
+  __builtin_nontemporal_store(v, (LRQ_GLOBAL u32_out*)p);
+}
 
 // MI355X dispatches work-group i to XCD i % 8.  Work units adjacent in memory
 // (the tiles of a 128-row band, consecutive row blocks) are given to one XCD in

@@ -200,24 +200,25 @@ __global__ __launch_bounds__(T) void k_tile128(Desc single, const Desc* __restri
 // the NJ scales are exchanged by shuffles, so the IEEE divisions cost one
 // pair per lane instead of NJ.  Rows are folded over the batch by the host.
 // LPB = 1 or 2 (1x8, 1x16) gives every lane its own blocks' scales.
-// PAD takes widths that are not a power of two, 8 g elements with g = 3..63
-// (the 4-lane group at least): each block keeps the LPB-lane group of the next
-// power of two and its last LPB - g lanes idle, so the same DPP reductions
-// apply (padding beat a segmented reduction over exactly g lanes in 16 of 18
-// width x dtype cases).  IPB = 2 or 4 takes 1x1024 and 1x2048 blocks, each
-// spanning IPB of a wave's instructions.
+// PAD takes the other widths B = 9..512: a block is g = ceil(B/8) chunks in the
+// LPB-lane group of the next power of two (2 at least), whose last LPB - g
+// lanes idle, so the same DPP reductions apply (padding beat a segmented
+// reduction over exactly g lanes in 16 of 18 width x dtype cases).  When 8
+// does not divide B the last chunk starts at B - 8, overlapping its
+// neighbour: the amax is unchanged by the repeat, and both lanes write the
+// same codes to the shared bytes.  IPB = 2 or 4 takes 1x1024 and 1x2048
+// blocks, each spanning IPB of a wave's instructions.
 // ---------------------------------------------------------------------------
 template <int DT, int CDT, int LPB, bool PAD = false, int IPB = 1>
 __global__ __launch_bounds__(256) void k_row(Desc single, const Desc* __restrict__ descs,
                                              const uint32_t* __restrict__ map, int pow2,
-                                             int scale_bf16, int g = LPB) {
-  // PAD: blocks of 8 g elements, g < LPB, in LPB-lane groups whose last
-  // LPB - g lanes idle (widths that are not a power of two).  IPB > 1: blocks
-  // of 512 IPB elements spanning IPB consecutive wave instructions of all 64
-  // lanes (1x1024, 1x2048).
+                                             int scale_bf16, int bw = 0) {
+  // PAD: blocks of bw elements, g = ceil(bw/8) <= LPB chunks, in LPB-lane
+  // groups whose last LPB - g lanes idle.  IPB > 1: blocks of 512 IPB elements
+  // spanning IPB consecutive wave instructions of all 64 lanes (1x1024, 1x2048).
   static_assert(IPB == 1 || (LPB == 64 && !PAD && kRowBlocks % IPB == 0), "whole blocks per wave");
-  const int G = PAD ? g : LPB;        // lanes holding a chunk of the block
-  const int B = 8 * G * IPB;          // elements per block
+  const int B = PAD ? bw : 8 * LPB * IPB;  // elements per block
+  const int G = PAD ? (bw + 7) / 8 : LPB;  // lanes holding a chunk of the block
   constexpr int BPI = 64 / LPB;       // blocks per wave instruction
   constexpr int NJ = kRowBlocks;      // wave instructions (chunks per lane)
   constexpr int NB = NJ / IPB;        // blocks per lane
@@ -233,7 +234,7 @@ __global__ __launch_bounds__(256) void k_row(Desc single, const Desc* __restrict
 #pragma unroll
   for (int j = 0; j < NJ; ++j) {
     const int64_t gb = wb + (j / IPB) * BPI;
-    const int64_t part = (j % IPB) * 512 + c * 8;  // element of the block
+    const int64_t part = (j % IPB) * 512 + (PAD && c * 8 > B - 8 ? B - 8 : c * 8);  // element of the block
     ok[j] = (!PAD || c < G) && gb < d.nblocks;
     if (ok[j]) {
       int64_t off;
@@ -282,7 +283,8 @@ __global__ __launch_bounds__(256) void k_row(Desc single, const Desc* __restrict
     if (!ok[j]) continue;
     const int64_t gb = wb + (j / IPB) * BPI;
     if (c == 0 && j % IPB == 0) store_scale<CDT>(d.scales, gb, bs[j / IPB].s, scale_bf16);
-    store_nt(d.codes + gb * B + (j % IPB) * 512 + c * 8, encode_chunk<DT, CDT>(ch[j], bs[j / IPB]));
+    const int64_t part = (j % IPB) * 512 + (PAD && c * 8 > B - 8 ? B - 8 : c * 8);
+    store_nt(d.codes + gb * B + part, encode_chunk<DT, CDT>(ch[j], bs[j / IPB]));
   }
 }
 
@@ -386,10 +388,12 @@ __global__ __launch_bounds__(256) void k_row_f32(Desc single, const Desc* __rest
 }
 
 // ---------------------------------------------------------------------------
-// Wide 1xB row blocks, B = 8 g elements with 512 < B <= 16384 (other than
-// 1024 and 2048, which k_row takes): a block belongs to W waves of the
+// Wide 1xB row blocks, 512 < B <= 16384 (other than 1024 and 2048, which
+// k_row takes), in g = ceil(B/8) chunks: a block belongs to W waves of the
 // work-group (W = 1 up to B = 4096, else 4), whose lane l of wave w holds
-// chunks c = 64 w + l + 64 W k for k < K = ceil(g / 64W).  With W = 1 a wave
+// chunks c = 64 w + l + 64 W k for k < K = ceil(g / 64W).  When 8 does not
+// divide B the last chunk starts at B - 8, overlapping its neighbour (the
+// amax ignores the repeat; both lanes write the same codes).  With W = 1 a wave
 // takes P consecutive blocks (P = 4, 2, 1 for K <= 2, 4, 8), so it keeps
 // about kWideChunks loads in flight per lane whatever the width.  Every wave
 // instruction of a block reads 1 KiB contiguous (of bf16), except the last
@@ -400,8 +404,9 @@ __global__ __launch_bounds__(256) void k_row_f32(Desc single, const Desc* __rest
 template <int DT, int CDT, int W, int P>
 __global__ __launch_bounds__(256) void k_row_wide(Desc single, const Desc* __restrict__ descs,
                                                   const uint32_t* __restrict__ map, int pow2,
-                                                  int scale_bf16, int g) {
+                                                  int scale_bf16, int bw) {
   static_assert(W == 1 || P == 1, "blocks of several waves: one block per wave group");
+  const int g = (bw + 7) / 8;  // chunks per block
   constexpr int KP = kWideChunks / P;  // chunk slots per block
   __shared__ uint32_t red[4];
   Desc d;
@@ -410,7 +415,7 @@ __global__ __launch_bounds__(256) void k_row_wide(Desc single, const Desc* __res
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int K = (g + 64 * W - 1) / (64 * W);  // <= KP
   const int64_t blk0 = (u * (4 / W) + wave / W) * P;
-  const int64_t B = 8 * (int64_t)g;
+  const int64_t B = bw;
   const int c0 = 64 * (wave % W) + lane;
 
   bool live[P];
@@ -431,7 +436,7 @@ __global__ __launch_bounds__(256) void k_row_wide(Desc single, const Desc* __res
     for (int k = 0; k < KP; ++k) {
       if (k < K) {
         const int c = c0 + 64 * W * k;
-        load_chunk<DT>(ch[p][k], d.in, base + 8 * (c < g ? c : 0));
+        load_chunk<DT>(ch[p][k], d.in, base + (c < g ? (8 * c > bw - 8 ? bw - 8 : 8 * c) : 0));
       }
     }
   }
@@ -462,7 +467,8 @@ __global__ __launch_bounds__(256) void k_row_wide(Desc single, const Desc* __res
 #pragma unroll
     for (int k = 0; k < KP; ++k) {
       const int c = c0 + 64 * W * k;
-      if (k < K && c < g) store_nt(d.codes + gb[p] * B + 8 * c, encode_chunk<DT, CDT>(ch[p][k], bs[p]));
+      if (k < K && c < g)
+        store_nt(d.codes + gb[p] * B + (8 * c > bw - 8 ? bw - 8 : 8 * c), encode_chunk<DT, CDT>(ch[p][k], bs[p]));
     }
   }
 }
@@ -563,25 +569,29 @@ static hipError_t launch_fp8_typed(const LaunchCfg& cfg, const Desc& single, con
       }
       return hipErrorInvalidValue;
     case kKernRowG: {
-      const int g = cfg.blk_c / 8;  // 1..63, not a power of two of 4..64 lanes
-      if (g == 1)
-        hipLaunchKernelGGL((k_row<DT, CDT, 1>), grid, block, 0, stream, single, descs, map, cfg.pow2, cfg.scale_bf16, g);
-      else if (g == 2)
-        hipLaunchKernelGGL((k_row<DT, CDT, 2>), grid, block, 0, stream, single, descs, map, cfg.pow2, cfg.scale_bf16, g);
-      else if (g < 4)
-        hipLaunchKernelGGL((k_row<DT, CDT, 4, true>), grid, block, 0, stream, single, descs, map, cfg.pow2, cfg.scale_bf16, g);
-      else if (g < 8)
-        hipLaunchKernelGGL((k_row<DT, CDT, 8, true>), grid, block, 0, stream, single, descs, map, cfg.pow2, cfg.scale_bf16, g);
-      else if (g < 16)
-        hipLaunchKernelGGL((k_row<DT, CDT, 16, true>), grid, block, 0, stream, single, descs, map, cfg.pow2, cfg.scale_bf16, g);
-      else if (g < 32)
-        hipLaunchKernelGGL((k_row<DT, CDT, 32, true>), grid, block, 0, stream, single, descs, map, cfg.pow2, cfg.scale_bf16, g);
+      // widths 8..512 other than 32..512 powers of two: g = ceil(bw/8) chunks
+      // in the next power of two of lanes (1x8 and 1x16 unpadded)
+      const int bw = (int)cfg.blk_c, g = (bw + 7) / 8;
+      if (bw == 8)
+        hipLaunchKernelGGL((k_row<DT, CDT, 1>), grid, block, 0, stream, single, descs, map, cfg.pow2, cfg.scale_bf16, bw);
+      else if (bw == 16)
+        hipLaunchKernelGGL((k_row<DT, CDT, 2>), grid, block, 0, stream, single, descs, map, cfg.pow2, cfg.scale_bf16, bw);
+      else if (g <= 2)
+        hipLaunchKernelGGL((k_row<DT, CDT, 2, true>), grid, block, 0, stream, single, descs, map, cfg.pow2, cfg.scale_bf16, bw);
+      else if (g <= 4)
+        hipLaunchKernelGGL((k_row<DT, CDT, 4, true>), grid, block, 0, stream, single, descs, map, cfg.pow2, cfg.scale_bf16, bw);
+      else if (g <= 8)
+        hipLaunchKernelGGL((k_row<DT, CDT, 8, true>), grid, block, 0, stream, single, descs, map, cfg.pow2, cfg.scale_bf16, bw);
+      else if (g <= 16)
+        hipLaunchKernelGGL((k_row<DT, CDT, 16, true>), grid, block, 0, stream, single, descs, map, cfg.pow2, cfg.scale_bf16, bw);
+      else if (g <= 32)
+        hipLaunchKernelGGL((k_row<DT, CDT, 32, true>), grid, block, 0, stream, single, descs, map, cfg.pow2, cfg.scale_bf16, bw);
       else
-        hipLaunchKernelGGL((k_row<DT, CDT, 64, true>), grid, block, 0, stream, single, descs, map, cfg.pow2, cfg.scale_bf16, g);
+        hipLaunchKernelGGL((k_row<DT, CDT, 64, true>), grid, block, 0, stream, single, descs, map, cfg.pow2, cfg.scale_bf16, bw);
       break;
     }
     case kKernRowWide: {
-      const int g = (int)(cfg.blk_c / 8);
+      const int g = (int)cfg.blk_c;  // the block width
       switch (wide_blocks_per_wave(cfg.blk_c)) {
         case 4: hipLaunchKernelGGL((k_row_wide<DT, CDT, 1, 4>), grid, block, 0, stream, single, descs, map, cfg.pow2, cfg.scale_bf16, g); break;
         case 2: hipLaunchKernelGGL((k_row_wide<DT, CDT, 1, 2>), grid, block, 0, stream, single, descs, map, cfg.pow2, cfg.scale_bf16, g); break;

@@ -40,11 +40,11 @@ enum Kernel : int {
   kKernF64 = 11,           // FP8 blocks of a float64 tensor in float64 arithmetic, one wave per block
   kKernF64Row = 12,        // dense 1xB float64 blocks (B = 32..512), 16-byte loads
   kKernF64Tile = 13,       // 128x128 float64 tiles, one 512-thread work-group per tile
-  kKernRowWide = 16,       // 1xB FP8 blocks, B = 8 g, 512 < B <= 16384 but 1024/2048: k_row_wide
+  kKernRowWide = 16,       // 1xB FP8 blocks, 512 < B <= 16384 but 1024/2048: k_row_wide
   kKernRowF32 = 15,        // 1xB FP8 blocks of float32 input (B = 8..1024, a power of two), one 16-byte load per lane chunk
-  kKernRowG = 14,          // 1xB FP8 blocks of 8 g elements, g = 1..63 not 4..64 a power of two: k_row
-                           // with 1- or 2-lane groups (g = 1, 2), else g lanes of each
-                           // next-power-of-two group (4 at least) active
+  kKernRowG = 14,          // 1xB FP8 blocks, B = 8..512 but 32..512 powers of two: k_row with
+                           // 1- or 2-lane groups (1x8, 1x16), else g = ceil(B/8) lanes of each
+                           // next-power-of-two group (2 at least) active
 };
 
 // Work per lane of the streaming kernels, shared by the kernels and the
@@ -53,7 +53,7 @@ constexpr int64_t kCopyUnit = 4096;  // k_copy: bytes per work-group (one 16 B l
 constexpr int kDequantChunks = 2;    // k_dequant: 16-byte output chunks per lane (2 beat 1, 4 and 8)
 constexpr int kMxLoads = 2;          // k_mx: 32-element groups per quad of lanes (2 beat 1, 3 and 4)
 constexpr int kWideChunks = 8;       // k_row_wide: 8-element chunks per lane (at most)
-// k_row_wide's blocks per wave for a 1xB block (B = 8 g, 512 < B <= 16384):
+// k_row_wide's blocks per wave for a 1xB block (512 < B <= 16384):
 // 4, 2 or 1 when a block takes at most 2, 4 or 8 of a wave's 64-lane steps
 // (one wave per block), 0 when it takes four waves (B > 4096).
 constexpr int wide_blocks_per_wave(int64_t blk_c) {

@@ -145,7 +145,8 @@ def test_group_pack_rows_and_mx_units():
     del blocks
     # other widths: 1x8 and 1x16 take 1- and 2-lane groups, wider ones the next
     # power of two of B/8 lanes (4 at least); 4 waves x 4 instructions per work-group
-    for B, lanes in ((8, 1), (16, 2), (24, 4), (40, 8), (96, 16), (200, 32), (504, 64)):
+    for B, lanes in ((8, 1), (16, 2), (24, 4), (40, 8), (96, 16), (200, 32), (504, 64),
+                     (12, 2), (36, 8), (100, 16), (500, 64)):  # ceil(B/8) chunks when 8 does not divide B
         shapes = [(1, 256, 16 * B), (1, 63, 3 * B)]
         buf = _pack(_lib.FMT_FP8_BLOCK, shapes, (1, B))
         per_wg = 4 * 4 * (64 // lanes)
@@ -153,9 +154,13 @@ def test_group_pack_rows_and_mx_units():
     # wider blocks: 4 waves of 4, 2 or 1 blocks (B <= 1024, 2048, 4096), or one
     # block of 4 waves (B <= 16384); 1024 and 2048 stay on the row kernel
     for B, per_wg in ((640, 16), (1032, 8), (1536, 8), (3072, 4), (4096, 4), (4104, 1), (16384, 1),
-                      (1024, 16 // 2), (2048, 16 // 4)):
-        buf = _pack(_lib.FMT_FP8_BLOCK, [(1, 256, 16 * B), (1, 63, 3 * B)], (1, B))
-        assert L().lrq_group_units(buf.ctypes.data) == -(-256 * 16 // per_wg) + -(-63 * 3 // per_wg), B
+                      (1024, 16 // 2), (2048, 16 // 4), (1000, 16), (3001, 4), (9999, 1)):
+        buf = _pack(_lib.FMT_FP8_BLOCK, [(1, 256, 16 * B), (1, 72, 3 * B)], (1, B))
+        assert L().lrq_group_units(buf.ctypes.data) == -(-256 * 16 // per_wg) + -(-72 * 3 // per_wg), B
+    # widths under 8 and past 16384 take the generic kernel: one work-group per block
+    for B in (5, 7, 16392):
+        buf = _pack(_lib.FMT_FP8_BLOCK, [(1, 4, 2 * B)], (1, B))
+        assert L().lrq_group_units(buf.ctypes.data) == 4 * 2, B
 
 
 def test_group_pack_expert_stack_single_descriptor():

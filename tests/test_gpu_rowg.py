@@ -1,14 +1,15 @@
 """1xB blocks of widths that are not 32..512 powers of two, on an MI355X.
 
 ``quantize_tensor(tensor, block_size=B)`` takes any B dividing the last dim
-(weight_quantizer.py:40-77).  Widths B = 8 g up to 512 run on the row kernel
-with 1- or 2-lane groups (8, 16) or lane groups padded to the next power of
-two (the last lanes of each group idle); 1024 and 2048 on the row kernel with
-a block spanning 2 or 4 wave instructions; other widths up to 16384 on the
-wide-row kernel, one wave per block up to 4096 (640, 1032, 1536, 4096) and
-four beyond (4104, 12288, 16384); the rest (36, 16392) on the generic kernel.
-Every code and scale bit is compared with the oracle, and the drop-in with the
-reference's torch op sequence.
+(weight_quantizer.py:40-77).  Widths 8..512 run on the row kernel with 1- or
+2-lane groups (8, 16) or ceil(B/8) chunks in lane groups padded to the next
+power of two (the last lanes of each group idle); when 8 does not divide B
+(12, 36, 100, 500) the last chunk overlaps its neighbour.  1024 and 2048 run on
+the row kernel with a block spanning 2 or 4 wave instructions; other widths up
+to 16384 on the wide-row kernel, one wave per block up to 4096 (640, 1000,
+1032, 1536, 3001, 4096) and four beyond (4104, 9999, 12288, 16384); the rest
+(5, 7, 16392) on the generic kernel.  Every code and scale bit is compared
+with the oracle, and the drop-in with the reference's torch op sequence.
 """
 
 from __future__ import annotations
@@ -29,7 +30,7 @@ if not torch.cuda.is_available():  # pragma: no cover - CPU container
 DEV = torch.device("cuda", 0)
 DT = {"bf16": torch.bfloat16, "f16": torch.float16, "f32": torch.float32}
 WIDTHS = [40, 48, 96, 120, 200, 248, 504, 8, 16, 24, 36, 1024, 2048, 1536,
-          640, 1032, 4096, 4104, 12288, 16384, 16392]
+          640, 1032, 4096, 4104, 12288, 16384, 16392, 12, 100, 500, 1000, 3001, 9999, 5, 7]
 # (rows, blocks per row, row pitch padding, pow2, bf16 scales when arith is f32)
 CASES = [(1, 1, 0, False, False), (37, 3, 0, True, False), (200, 5, 16, False, True),
          (513, 2, 0, False, False), (64, 11, 8, True, False)]
@@ -76,7 +77,7 @@ def test_width_vs_oracle(B, dt, arith):
         assert np.array_equal(got.reshape(-1), want.reshape(-1)), (B, rows, cols, ld)
 
 
-@pytest.mark.parametrize("B", [96, 40, 200, 8, 1536, 4104])
+@pytest.mark.parametrize("B", [96, 40, 200, 8, 1536, 4104, 36, 1000])
 def test_grouped_plan_and_expert_stacks(B):
     print("rowg grouped", B, flush=True)
     rng = np.random.default_rng(B)
@@ -94,14 +95,31 @@ def test_grouped_plan_and_expert_stacks(B):
             assert np.array_equal(s.cpu().view(torch.int16).numpy().view(np.uint16).reshape(-1), want), (B, step)
 
 
+@pytest.mark.parametrize("block", [96, 36, 1000])
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
-def test_dropin_quantize_tensor_block_96_matches_reference_ops(dtype):
+def test_dropin_quantize_tensor_odd_blocks_match_reference_ops(dtype, block):
     torch.manual_seed(5)
-    w = (torch.randn(300, 960) * 0.02).to(dtype)
+    w = (torch.randn(300, 9000 if block == 1000 else 2880) * 0.02).to(dtype)
     wq = WeightQuantizer(FP8Config())
-    q, s = wq.quantize_tensor(w.to(DEV), block_size=96)
-    rq, rs = TR.quantize_tensor(w, 96)
+    q, s = wq.quantize_tensor(w.to(DEV), block_size=block)
+    rq, rs = TR.quantize_tensor(w, block)
     assert q.shape == rq.shape and s.shape == rs.shape and s.dtype == rs.dtype
     assert torch.equal(q.cpu().view(torch.uint8), rq.view(torch.uint8))
     assert torch.equal(s.cpu().view(torch.int16 if s.element_size() == 2 else torch.int32),
                        rs.view(torch.int16 if rs.element_size() == 2 else torch.int32))
+
+
+def test_tiny_blocks_past_one_launch():
+    """1x5 blocks of a [8192, 16400] weight: 26.9 M blocks on the generic kernel
+    (one work-group each) exceed one launch's 2^32 threads, so the entry point
+    splits the tensor into bands of rows, one launch each."""
+    print("rowg 1x5 past one launch", flush=True)
+    rng = np.random.default_rng(55)
+    x = torch.from_numpy(rng.normal(0, 0.02, (8192, 16400)).astype(np.float32)).to(torch.bfloat16)
+    x[77, 5:10] = 0.0
+    x[4000, 12] = float("inf")
+    c, s = ops.fp8_block_quant(x.to(DEV), (1, 5))
+    torch.cuda.synchronize()
+    oc, osc = O.fp8_block_quant(host(x, "bf16"), "bf16", "f32", (1, 5), nthreads=16)
+    assert np.array_equal(c.view(torch.uint8).cpu().numpy(), oc[0])
+    assert np.array_equal(s.cpu().numpy().view(np.uint32), osc[0].view(np.uint32))
