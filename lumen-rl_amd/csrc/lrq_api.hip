@@ -145,8 +145,10 @@ int fp8_kernel_for(const Desc& d, int in_dtype, int64_t blk_r, int64_t blk_c) {
   return lrq::kKernGenericFp8;
 }
 
-int dequant_kernel_for(const Desc& d, int64_t blk_c) {
-  const bool vec = aligned(d.in, 16) && aligned(d.codes, 16) && d.cols % 16 == 0 && blk_c % 16 == 0;
+// codes (d.in) at any alignment; the output (d.codes) takes 16-byte stores, and
+// each lane-chunk of cpc codes must lie inside one block and one row
+int dequant_kernel_for(const Desc& d, int64_t blk_c, int64_t cpc) {
+  const bool vec = aligned(d.codes, 16) && d.cols % cpc == 0 && blk_c % cpc == 0;
   return vec ? lrq::kKernDequant : lrq::kKernGenericDequant;
 }
 
@@ -386,10 +388,8 @@ int plan_group(int fmt, const lrq_tensor* ts, int64_t n, int in_dtype, int64_t b
         return fail(LRQ_ERR_ARG, "tensor %lld: MX dequant needs dense codes (ld == cols)", (long long)i);
       if (d.cols % 32 != 0) return fail(LRQ_ERR_ARG, "tensor %lld: cols %% 32 != 0", (long long)i);
       const int64_t cpc = cfg.out_dtype == lrq::kBF16 ? 8 : 4;  // elements per lane-chunk
-      const int64_t cb = cfg.mx_fmt == 8 ? cpc : cpc / 2;       // code bytes per lane-chunk
-      if (!aligned(d.in, (uintptr_t)cb) || !aligned(d.codes, 16))
-        return fail(LRQ_ERR_ALIGN, "tensor %lld: MX dequant needs codes aligned to %lld bytes and a "
-                    "16-byte aligned output", (long long)i, (long long)cb);
+      if (!aligned(d.codes, 16))  // the codes may sit at any byte alignment
+        return fail(LRQ_ERR_ALIGN, "tensor %lld: MX dequant needs a 16-byte aligned output", (long long)i);
       d.nblocks = d.batch * d.rows * d.cols / cpc;
       d.units = (d.nblocks + 256 * lrq::kDequantChunks - 1) / (256 * lrq::kDequantChunks);
       d.unit0 = units;
@@ -447,7 +447,7 @@ int plan_group(int fmt, const lrq_tensor* ts, int64_t n, int in_dtype, int64_t b
     } else if (fmt == LRQ_FMT_FP8_DEQUANT) {
       if (d.ld != d.cols || d.bstride != d.rows * d.cols)
         return fail(LRQ_ERR_ARG, "tensor %lld: dequant needs dense codes (ld == cols)", (long long)i);
-      k = dequant_kernel_for(d, blk_c);
+      k = dequant_kernel_for(d, blk_c, cfg.out_dtype == lrq::kBF16 ? 8 : 4);
     } else {
       if (d.cols % 32 != 0) return fail(LRQ_ERR_ARG, "tensor %lld: cols %% 32 != 0", (long long)i);
       k = mx_kernel_for(d, in_dtype, cfg.mx_fmt);

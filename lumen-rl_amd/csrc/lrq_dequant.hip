@@ -59,8 +59,9 @@ __global__ __launch_bounds__(256) void k_dequant_generic(Desc single, const Desc
 // Vectorized: a lane-chunk is CPC codes (8 for bf16 output, 4 for fp32) whose
 // output is exactly one 16-byte store, so every wave load and store
 // instruction covers one contiguous span (512 B / 256 B of codes, 1 KiB out);
-// kDequantChunks chunks per lane, all loaded before the first store.  A chunk lies inside one
-// block (blk_c % 16 == 0), so its scale is uniform: when the scale is finite
+// kDequantChunks chunks per lane, all loaded before the first store (codes at
+// any byte alignment).  A chunk lies inside one block (blk_c and cols
+// multiples of CPC), so its scale is uniform: when the scale is finite
 // and non-zero and no code is NaN the chunk takes the hardware path
 // (v_cvt_pk_f32_fp8 -> multiply -> v_cvt_pk_bf16_f32); anything else takes the
 // explicit x86 rules.  ROWS1: 1xB blocks over dense rows (scale = element / blk_c).
@@ -93,11 +94,11 @@ __global__ __launch_bounds__(256) void k_dequant(Desc single, const Desc* __rest
 #pragma unroll
   for (int j = 0; j < NCH; ++j) {  // every code load first, then the scales
     if constexpr (NW == 2) {
-      const v2u v = gld_nt<v2u>(codes + at[j] * CPC);
+      const v2u v = load_nt8(codes + at[j] * CPC);
       cw[j][0] = v.x;
       cw[j][1] = v.y;
     } else {
-      cw[j][0] = gld_nt<uint32_t>(codes + at[j] * CPC);
+      cw[j][0] = load_nt4(codes + at[j] * CPC);
     }
   }
 #pragma unroll
@@ -229,13 +230,13 @@ __global__ __launch_bounds__(256) void k_mx_dequant(Desc single, const Desc* __r
   for (int j = 0; j < NCH; ++j) {  // every code load first, then the scale bytes
     const uint8_t* p = codes + at[j] * CB;
     if constexpr (CB == 8) {
-      const v2u v = gld_nt<v2u>(p);
+      const v2u v = load_nt8(p);
       cw[j][0] = v.x;
       cw[j][1] = v.y;
     } else if constexpr (CB == 4) {
-      cw[j][0] = gld_nt<uint32_t>(p);
+      cw[j][0] = load_nt4(p);
     } else {
-      cw[j][0] = gld_nt<uint16_t>(p);
+      cw[j][0] = load_nt2(p);
     }
   }
 #pragma unroll

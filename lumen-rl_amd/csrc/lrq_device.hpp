@@ -294,6 +294,17 @@ typedef unsigned int v4u_in __attribute__((ext_vector_type(4), aligned(2)));
 __device__ __forceinline__ v4u load_nt(const void* p) {
   return __builtin_nontemporal_load((const LRQ_GLOBAL v4u_in*)p);
 }
+// Code loads of the dequant kernels take any byte alignment, likewise.
+typedef unsigned int v2u_in __attribute__((ext_vector_type(2), aligned(1)));
+typedef uint32_t u32_in __attribute__((aligned(1)));
+typedef uint16_t u16_in __attribute__((aligned(1)));
+__device__ __forceinline__ v2u load_nt8(const void* p) { return __builtin_nontemporal_load((const LRQ_GLOBAL v2u_in*)p); }
+__device__ __forceinline__ uint32_t load_nt4(const void* p) {
+  return __builtin_nontemporal_load((const LRQ_GLOBAL u32_in*)p);
+}
+__device__ __forceinline__ uint16_t load_nt2(const void* p) {
+  return __builtin_nontemporal_load((const LRQ_GLOBAL u16_in*)p);
+}
 // Code stores take any byte alignment, in the same unaligned-access mode: the
 // row kernels write blocks whose width is not a multiple of 8 at odd offsets.
 typedef unsigned int v2u_out __attribute__((ext_vector_type(2), aligned(1)));

@@ -265,10 +265,7 @@ def _mx_dequant(codes: Tensor, scales: Tensor, fmt: int, out_dtype: torch.dtype)
     if cols % 32 or tuple(scales.shape) != (*lead, cols // 32):
         raise ValueError(f"codes {tuple(codes.shape)} and scales {tuple(scales.shape)} are not an "
                          f"MXFP{fmt} pair")
-    c = codes.contiguous().view(torch.uint8)
-    cb = (8 if out_dtype == torch.bfloat16 else 4) // (1 if fmt == 8 else 2)
-    if c.data_ptr() % cb:
-        c = c.clone()
+    c = codes.contiguous().view(torch.uint8)  # read at any byte alignment
     s = scales.contiguous().view(torch.uint8)
     out = torch.empty((*lead, cols), dtype=out_dtype, device=codes.device)
     if out.numel() == 0:

@@ -325,7 +325,9 @@ def test_mx_dequant_tables():
             assert L().lrq_group_pack(fmt, ts, 2, 0, 1, 32, flags, buf.ctypes.data, need) == 0
             units = [-(-64 * 1024 // cpc // 512), -(-2 * 32 * 512 // cpc // 512)]
             assert L().lrq_group_units(buf.ctypes.data) == sum(units)
-    ts[1].in_ = ts[1].in_ + 2  # MXFP8 codes must hold a whole lane-chunk (4 or 8 bytes)
+    ts[1].in_ = ts[1].in_ + 3  # codes at any byte offset
+    assert L().lrq_group_table_bytes(_lib.FMT_MXFP8_DEQUANT, ts, 2, 0, 1, 32, 0) > 0, _lib.last_error()
+    ts[1].codes = ts[1].codes + 8  # the output takes 16-byte stores
     assert L().lrq_group_table_bytes(_lib.FMT_MXFP8_DEQUANT, ts, 2, 0, 1, 32, 0) == _lib.ERR_ALIGN
     fake = ctypes.c_void_p(0x10000)
     assert L().lrq_mx_dequant(3, fake, fake, 4, 64, fake, 0, None) == _lib.ERR_ARG      # bad format

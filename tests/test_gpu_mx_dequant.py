@@ -89,7 +89,7 @@ def test_grouped_plan_and_misaligned_codes(fmt):
         for (q, s), o in zip(pairs, outs):
             want = T.mx_dequant(q, s, 8 if fmt == "mxfp8" else 4, odt)
             assert np.array_equal(bits(o), bits(want.reshape(o.shape)))
-    # a code view starting 2 bytes into its storage is copied to aligned memory first
+    # a code view starting 2 bytes into its storage is read in place
     q, s = pairs[3]
     qv, sv = q.view(torch.uint8).reshape(-1)[2:].reshape(-1)[: 64 * q.shape[-1]].reshape(64, -1), s[:64]
     qv = qv if fmt == "mxfp4" else qv.view(torch.float8_e4m3fn)
