@@ -581,9 +581,12 @@ class QuantPlan:
     ``run(inputs=...)``; they must have the planned shapes and dtype.  The
     outputs stay the same tensors across re-binds.
 
-    Inputs are device tensors with K % 8 == 0 (any element-aligned view, any
-    row pitch: the kernels' 16-byte loads take 2-byte-aligned addresses).  float64 weights
-    take ``fmt="fp8_block"`` with ``native_arith=True`` (float64 arithmetic and
+    Inputs are device tensors: any element-aligned view and any row pitch (the
+    kernels' 16-byte loads take 2-byte-aligned addresses).  All tensors of a plan
+    must take one kernel: 128x128 tiles need K % 8 == 0, 1xB blocks K % B == 0
+    (B from 8 to 16384), MX K % 32 == 0; other shapes raise ``ValueError`` and
+    go through :func:`fp8_block_quant` one by one.  float64 weights take
+    ``fmt="fp8_block"`` with ``native_arith=True`` (float64 arithmetic and
     scales, as ``quantize_tensor`` on a float64 tensor).
     """
 
