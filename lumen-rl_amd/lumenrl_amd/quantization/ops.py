@@ -583,9 +583,10 @@ class QuantPlan:
 
     Inputs are device tensors: any element-aligned view and any row pitch (the
     kernels' 16-byte loads take 2-byte-aligned addresses).  All tensors of a plan
-    must take one kernel: 128x128 tiles need K % 8 == 0, 1xB blocks K % B == 0
-    (B from 8 to 16384), MX K % 32 == 0; other shapes raise ``ValueError`` and
-    go through :func:`fp8_block_quant` one by one.  float64 weights take
+    must take one kernel: 128x128 tiles with K % 8 == 0 and 1xB blocks (B from
+    8 to 16384) take the vector kernels, other shapes the generic one, and a
+    plan mixing the two raises ``ValueError`` (quantize those tensors with
+    :func:`fp8_block_quant` one by one).  float64 weights take
     ``fmt="fp8_block"`` with ``native_arith=True`` (float64 arithmetic and
     scales, as ``quantize_tensor`` on a float64 tensor).
     """
