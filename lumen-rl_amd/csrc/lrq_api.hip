@@ -40,7 +40,7 @@ bool pow2_block(int64_t b) { return b == 32 || b == 64 || b == 128 || b == 256 |
 bool row_block(int64_t b) { return pow2_block(b) || b == 1024 || b == 2048; }
 
 constexpr uint32_t kMagic = 0x4C525154u;  // "LRQT"
-constexpr uint32_t kTableVersion = 2u;
+constexpr uint32_t kTableVersion = 3u;  // 3: LaunchCfg gained `pitched`
 // HIP takes a launch's thread count (work-groups x threads per work-group) as
 // a 32-bit value.  kMaxGrid is the limit for 256-thread work-groups;
 // max_units() gives it per kernel.
@@ -113,7 +113,7 @@ bool fold_batch(Desc& d) {
 
 int fp8_kernel_for(const Desc& d, int in_dtype, int64_t blk_r, int64_t blk_c) {
   if (in_dtype == lrq::kF64) {
-    const bool row = blk_r == 1 && pow2_block(blk_c) && d.cols % blk_c == 0 && d.ld == d.cols &&
+    const bool row = blk_r == 1 && pow2_block(blk_c) && d.cols % blk_c == 0 &&
                      (d.batch == 1 || d.bstride == d.rows * d.ld) && aligned(d.in, 8) &&
                      aligned(d.codes, 2) && aligned(d.scales, 8);
     if (row) return lrq::kKernF64Row;
@@ -468,6 +468,11 @@ int plan_group(int fmt, const lrq_tensor* ts, int64_t n, int in_dtype, int64_t b
     cfg.kernel = fmt == LRQ_FMT_FP8_BLOCK     ? lrq::kKernGenericFp8
                  : fmt == LRQ_FMT_FP8_DEQUANT ? lrq::kKernGenericDequant
                                               : lrq::kKernGenericMx;
+  if (cfg.kernel == lrq::kKernF64Row) {
+    cfg.pitched = 0;
+    for (int64_t i = 0; i < n; ++i)
+      if (ts[i].rows > 1 && ts[i].ld != ts[i].cols) cfg.pitched = 1;
+  }
   if (fmt == LRQ_FMT_FP8_DEQUANT) {
     cfg.rows_dense = 1;
     for (int64_t i = 0; i < n; ++i)

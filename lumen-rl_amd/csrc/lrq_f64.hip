@@ -7,7 +7,7 @@
 // rounded to float32 (:68) before the e4m3 cast (:71): a double rounding
 // (f64 -> f32 -> e4m3) that this kernel keeps.  Scales are written as float64.
 //
-// k_row_f64 takes dense 1xB blocks (B = 32...512, the reference's layout) and
+// k_row_f64 takes 1xB blocks (B = 32...512, the reference's layout) and
 // k_tile_f64 128x128 tiles, both with 16-byte loads.  Their quotients of finite
 // blocks use one correctly rounded 1/s per block and Markstein's correction per
 // element (the IEEE division in blocks with tiny scales) and the hardware e4m3
@@ -217,15 +217,17 @@ __global__ __launch_bounds__(256) void k_f64(Desc single, const Desc* __restrict
     }
 }
 
-// 1xB row blocks (B = 32...512) of a dense float64 tensor.  Wave instruction i
-// reads 128 consecutive doubles (1 KiB; 16 bytes = 2 doubles per lane), so a
-// block spans B/2 lanes of one instruction (B < 128) or B/128 instructions of
-// all 64 lanes (B >= 128).  Each wave runs kF64RowInstr instructions; code
+// 1xB row blocks (B = 32...512) of a float64 tensor.  Wave instruction i
+// reads 128 consecutive doubles of the row-major element sequence (1 KiB when
+// the rows are dense; 16 bytes = 2 doubles per lane, never split by a row end
+// since cols is even), so a block spans B/2 lanes of one instruction (B < 128)
+// or B/128 instructions of all 64 lanes (B >= 128).  PITCHED: rows ld apart,
+// element e read at e + (e / cols) (ld - cols).  Each wave runs kF64RowInstr instructions; code
 // stores are 2 bytes per lane (128 contiguous bytes per wave instruction).
 // For B >= 128 a wave holds 4 / (B/128) whole blocks: each lane computes the
 // scale of one of them (split_max) and the scales reach the whole wave by
 // readlane, so the quotient loop runs on wave-uniform s and 1/s.
-template <int B>
+template <int B, bool PITCHED>
 __global__ __launch_bounds__(256) void k_row_f64(Desc single, const Desc* __restrict__ descs,
                                                  const uint32_t* __restrict__ map, int pow2) {
   constexpr int IPB = B >= 128 ? B / 128 : 1;  // instructions per block
@@ -250,7 +252,8 @@ __global__ __launch_bounds__(256) void k_row_f64(Desc single, const Desc* __rest
   for (int i = 0; i < NI; ++i) {
     const int64_t e = e0 + i * 128;
     ok[i] = e < n;  // n is a multiple of B >= 32: e < n covers e + 1
-    raw[i] = load_nt(in + (ok[i] ? e : n - 2));
+    const int64_t ee = ok[i] ? e : n - 2;
+    raw[i] = load_nt(in + (PITCHED ? ee + (ee / d.cols) * (d.ld - d.cols) : ee));
   }
   __builtin_amdgcn_sched_barrier(0);
   uint64_t x[NI][2];
@@ -394,13 +397,24 @@ hipError_t launch_f64(const LaunchCfg& cfg, const Desc& single, const Desc* desc
                       const uint32_t* map, int64_t units, hipStream_t stream) {
   const dim3 grid((unsigned)units), block(256);
   if (cfg.kernel == kKernF64Row) {
-    switch (cfg.blk_c) {
-      case 32: hipLaunchKernelGGL(k_row_f64<32>, grid, block, 0, stream, single, descs, map, cfg.pow2); break;
-      case 64: hipLaunchKernelGGL(k_row_f64<64>, grid, block, 0, stream, single, descs, map, cfg.pow2); break;
-      case 128: hipLaunchKernelGGL(k_row_f64<128>, grid, block, 0, stream, single, descs, map, cfg.pow2); break;
-      case 256: hipLaunchKernelGGL(k_row_f64<256>, grid, block, 0, stream, single, descs, map, cfg.pow2); break;
-      case 512: hipLaunchKernelGGL(k_row_f64<512>, grid, block, 0, stream, single, descs, map, cfg.pow2); break;
-      default: return hipErrorInvalidValue;
+    if (cfg.pitched) {
+      switch (cfg.blk_c) {
+        case 32: hipLaunchKernelGGL((k_row_f64<32, true>), grid, block, 0, stream, single, descs, map, cfg.pow2); break;
+        case 64: hipLaunchKernelGGL((k_row_f64<64, true>), grid, block, 0, stream, single, descs, map, cfg.pow2); break;
+        case 128: hipLaunchKernelGGL((k_row_f64<128, true>), grid, block, 0, stream, single, descs, map, cfg.pow2); break;
+        case 256: hipLaunchKernelGGL((k_row_f64<256, true>), grid, block, 0, stream, single, descs, map, cfg.pow2); break;
+        case 512: hipLaunchKernelGGL((k_row_f64<512, true>), grid, block, 0, stream, single, descs, map, cfg.pow2); break;
+        default: return hipErrorInvalidValue;
+      }
+    } else {
+      switch (cfg.blk_c) {
+        case 32: hipLaunchKernelGGL((k_row_f64<32, false>), grid, block, 0, stream, single, descs, map, cfg.pow2); break;
+        case 64: hipLaunchKernelGGL((k_row_f64<64, false>), grid, block, 0, stream, single, descs, map, cfg.pow2); break;
+        case 128: hipLaunchKernelGGL((k_row_f64<128, false>), grid, block, 0, stream, single, descs, map, cfg.pow2); break;
+        case 256: hipLaunchKernelGGL((k_row_f64<256, false>), grid, block, 0, stream, single, descs, map, cfg.pow2); break;
+        case 512: hipLaunchKernelGGL((k_row_f64<512, false>), grid, block, 0, stream, single, descs, map, cfg.pow2); break;
+        default: return hipErrorInvalidValue;
+      }
     }
     return hipGetLastError();
   }

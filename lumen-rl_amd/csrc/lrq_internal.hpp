@@ -103,6 +103,7 @@ struct LaunchCfg {
   int scale_bf16; // FP8 kernels: write the float32 scales rounded to bf16
   int out_dtype;  // dequant: kF32 or kBF16 (in_dtype is then the scale dtype)
   int rows_dense; // dequant, 1xB: every tensor has cols % blk_c == 0
+  int pitched;    // float64 rows: some tensor's row pitch exceeds its width
 };
 
 // Work-groups a tensor needs under `cfg` (filled into d.units and the unit
