@@ -113,7 +113,7 @@ bool fold_batch(Desc& d) {
 
 int fp8_kernel_for(const Desc& d, int in_dtype, int64_t blk_r, int64_t blk_c) {
   if (in_dtype == lrq::kF64) {
-    const bool row = blk_r == 1 && pow2_block(blk_c) && d.cols % blk_c == 0 &&
+    const bool row = blk_r == 1 && row_block(blk_c) && d.cols % blk_c == 0 &&
                      (d.batch == 1 || d.bstride == d.rows * d.ld) && aligned(d.in, 8) &&
                      aligned(d.codes, 2) && aligned(d.scales, 8);
     if (row) return lrq::kKernF64Row;
@@ -176,9 +176,9 @@ bool plan_units(const LaunchCfg& cfg, Desc& d) {
       d.units_c = (d.cols + cfg.blk_c - 1) / cfg.blk_c;
       d.units = d.batch * d.units_r * d.units_c;
       return true;
-    case kKernF64Row: {  // 4 waves x kF64RowInstr instructions of 128 doubles
+    case kKernF64Row: {  // 4 waves x f64_row_instr instructions of 128 doubles
       if (!fold_batch(d)) return false;
-      const int64_t per_wg = 4 * kF64RowInstr * 128;
+      const int64_t per_wg = 4 * f64_row_instr(cfg.blk_c) * 128;
       d.units = (d.batch * d.rows * d.cols + per_wg - 1) / per_wg;
       return true;
     }

@@ -217,14 +217,15 @@ __global__ __launch_bounds__(256) void k_f64(Desc single, const Desc* __restrict
     }
 }
 
-// 1xB row blocks (B = 32...512) of a float64 tensor.  Wave instruction i
+// 1xB row blocks (B = 32...2048, powers of two) of a float64 tensor.  Wave instruction i
 // reads 128 consecutive doubles of the row-major element sequence (1 KiB when
 // the rows are dense; 16 bytes = 2 doubles per lane, never split by a row end
 // since cols is even), so a block spans B/2 lanes of one instruction (B < 128)
 // or B/128 instructions of all 64 lanes (B >= 128).  PITCHED: rows ld apart,
-// element e read at e + (e / cols) (ld - cols).  Each wave runs kF64RowInstr instructions; code
-// stores are 2 bytes per lane (128 contiguous bytes per wave instruction).
-// For B >= 128 a wave holds 4 / (B/128) whole blocks: each lane computes the
+// element e read at e + (e / cols) (ld - cols).  Each wave runs kF64RowInstr
+// instructions (B/128 for 1x1024 and 1x2048); code stores are 2 bytes per
+// lane (128 contiguous bytes per wave instruction).
+// For B >= 128 a wave holds NI / (B/128) whole blocks: each lane computes the
 // scale of one of them (split_max) and the scales reach the whole wave by
 // readlane, so the quotient loop runs on wave-uniform s and 1/s.
 template <int B, bool PITCHED>
@@ -232,7 +233,7 @@ __global__ __launch_bounds__(256) void k_row_f64(Desc single, const Desc* __rest
                                                  const uint32_t* __restrict__ map, int pow2) {
   constexpr int IPB = B >= 128 ? B / 128 : 1;  // instructions per block
   constexpr int LPB = B >= 128 ? 64 : B / 2;   // lanes per block
-  constexpr int NI = kF64RowInstr;
+  constexpr int NI = f64_row_instr(B);
   static_assert(NI % IPB == 0, "a wave holds whole blocks");
   Desc d;
   int64_t u;
@@ -404,6 +405,8 @@ hipError_t launch_f64(const LaunchCfg& cfg, const Desc& single, const Desc* desc
         case 128: hipLaunchKernelGGL((k_row_f64<128, true>), grid, block, 0, stream, single, descs, map, cfg.pow2); break;
         case 256: hipLaunchKernelGGL((k_row_f64<256, true>), grid, block, 0, stream, single, descs, map, cfg.pow2); break;
         case 512: hipLaunchKernelGGL((k_row_f64<512, true>), grid, block, 0, stream, single, descs, map, cfg.pow2); break;
+        case 1024: hipLaunchKernelGGL((k_row_f64<1024, true>), grid, block, 0, stream, single, descs, map, cfg.pow2); break;
+        case 2048: hipLaunchKernelGGL((k_row_f64<2048, true>), grid, block, 0, stream, single, descs, map, cfg.pow2); break;
         default: return hipErrorInvalidValue;
       }
     } else {
@@ -413,6 +416,8 @@ hipError_t launch_f64(const LaunchCfg& cfg, const Desc& single, const Desc* desc
         case 128: hipLaunchKernelGGL((k_row_f64<128, false>), grid, block, 0, stream, single, descs, map, cfg.pow2); break;
         case 256: hipLaunchKernelGGL((k_row_f64<256, false>), grid, block, 0, stream, single, descs, map, cfg.pow2); break;
         case 512: hipLaunchKernelGGL((k_row_f64<512, false>), grid, block, 0, stream, single, descs, map, cfg.pow2); break;
+        case 1024: hipLaunchKernelGGL((k_row_f64<1024, false>), grid, block, 0, stream, single, descs, map, cfg.pow2); break;
+        case 2048: hipLaunchKernelGGL((k_row_f64<2048, false>), grid, block, 0, stream, single, descs, map, cfg.pow2); break;
         default: return hipErrorInvalidValue;
       }
     }

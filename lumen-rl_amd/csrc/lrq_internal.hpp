@@ -38,7 +38,7 @@ enum Kernel : int {
   kKernCast = 9,           // grouped unscaled cast to float8_e4m3fn
   kKernMxDequant = 10,     // MXFP8 / MXFP4 dequant, 8 (bf16 out) or 4 (fp32) elements per lane-chunk
   kKernF64 = 11,           // FP8 blocks of a float64 tensor in float64 arithmetic, one wave per block
-  kKernF64Row = 12,        // dense 1xB float64 blocks (B = 32..512), 16-byte loads
+  kKernF64Row = 12,        // 1xB float64 blocks (B = 32..2048, powers of two), 16-byte loads
   kKernF64Tile = 13,       // 128x128 float64 tiles, one 512-thread work-group per tile
   kKernRowWide = 16,       // 1xB FP8 blocks, 512 < B <= 16384 but 1024/2048: k_row_wide
   kKernRowF32 = 15,        // 1xB FP8 blocks of float32 input (B = 8..1024, a power of two), one 16-byte load per lane chunk
@@ -71,8 +71,9 @@ constexpr int kCastLaneElems = 16;   // k_cast_e4m3: elements per lane
 constexpr int64_t kCastUnit = 256 * kCastLaneElems;  // k_cast_e4m3: elements per work-group
 constexpr int kAmaxLoads = 2;        // k_amax: 16-byte loads per lane (2 beat 1, 3, 4 and 8)
 // k_row_f64: 1 KiB wave instructions per wave (128 doubles each); 4 beats 8 by
-// 8-10% on 1x128 blocks
+// 8-10% on 1x128 blocks.  1x1024 and 1x2048 blocks take one block per wave.
 constexpr int kF64RowInstr = 4;
+constexpr int f64_row_instr(int64_t blk_c) { return blk_c > 128 * kF64RowInstr ? (int)(blk_c / 128) : kF64RowInstr; }
 
 // Descriptor and local work unit of this work-group: the single-tensor
 // descriptor (kernel argument) or, for a grouped launch, the one the device

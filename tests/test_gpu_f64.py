@@ -66,15 +66,17 @@ def check(xd: torch.Tensor, blk, pow2):
 
 
 @pytest.mark.parametrize("pow2", [False, True])
-@pytest.mark.parametrize("blk", [(1, 128), (1, 32), (1, 64), (1, 256), (1, 512), (1, 96), (1, 384), (128, 128), (3, 40), (64, 96)])
+@pytest.mark.parametrize("blk", [(1, 128), (1, 32), (1, 64), (1, 256), (1, 512), (1, 1024), (1, 2048), (1, 96),
+                                 (1, 384), (128, 128), (3, 40), (64, 96)])
 @pytest.mark.parametrize("data", ["weights", "edge"])
 def test_f64_blocks_vs_oracle(data, blk, pow2):
     say("f64", data, blk, pow2)
+    cols = blk[1] * 2 if blk[1] >= 512 else 384
     if data == "weights":
-        x = RNG.normal(0, 0.02, (200, 512) if blk[1] == 512 else (200, 384))
+        x = RNG.normal(0, 0.02, (200, cols))
         x.flat[RNG.integers(0, x.size, 80)] *= 150
     else:
-        x = edge64(cols=512 if blk[1] == 512 else 384)
+        x = edge64(cols=cols)
     check(torch.from_numpy(x).to(DEV), blk, pow2)
 
 
@@ -83,6 +85,7 @@ def test_f64_views_and_batches(pow2):
     base = torch.from_numpy(edge64(48, 640)).to(DEV)
     check(base[:, 64:448], (1, 128), pow2)          # row stride 640, offset view
     check(base[::3, :512], (1, 128), pow2)          # row stride 1920
+    check(base[::2, :512], (1, 512), pow2)          # row stride 1280, one block per row
     check(base[:40].reshape(5, 8, 640), (1, 64), pow2)  # batched matrices
     check(base.reshape(3, 16, 640)[:, :, :384], (8, 128), pow2)  # strided batch, 2-D blocks
     e = torch.empty(0, 128, dtype=torch.float64, device=DEV)

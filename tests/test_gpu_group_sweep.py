@@ -30,7 +30,7 @@ if not torch.cuda.is_available():  # pragma: no cover - CPU container
 DEV = torch.device("cuda", 0)
 DT = {"bf16": torch.bfloat16, "f16": torch.float16, "f32": torch.float32}
 KINDS = ["tile", "row", "mx8", "mx4", "cast", "kv", "deq", "mxdeq", "blk", "f64"]
-F64_BLOCKS = [(1, 32), (1, 128), (1, 512), (128, 128), (3, 40), (1, 96)]
+F64_BLOCKS = [(1, 32), (1, 128), (1, 512), (128, 128), (3, 40), (1, 96), (1, 1024)]
 BLOCKS = [(1, 32), (1, 64), (1, 256), (1, 512), (3, 40), (64, 96), (128, 64), (2, 128), (1, 96), (1, 40), (1, 16),
           (1, 1024), (1, 8), (1, 1536), (1, 4104), (1, 36), (1, 100), (1, 12)]
 
