@@ -114,6 +114,33 @@ int main() {
            blk_r == 128 ? "lrq_fp8_block_quant 128x128" : "lrq_fp8_block_quant 1x128");
   }
 
+  // 1b. a view one element into weight 1 (2-byte aligned rows, pitch 3072),
+  // 255 x 2304, in 1x128 and 1x36 blocks (36: the last 8-element chunk of each
+  // block overlaps its neighbour)
+  {
+    const int64_t vr = 255, vc = 2304, vld = C[1];
+    const uint16_t* dv = static_cast<const uint16_t*>(dw[1]) + 1;
+    std::vector<uint16_t> hv((size_t)(vr * vc));
+    for (int64_t r = 0; r < vr; ++r)
+      memcpy(&hv[(size_t)(r * vc)], &hw[1][(size_t)(1 + r * vld)], (size_t)vc * 2);
+    float* dvs;  // scales of the narrowest blocks: vr * vc / 36 floats
+    HIP(hipMalloc(&dvs, (size_t)(vr * (vc / 36)) * 4));
+    for (int64_t bc : {128, 36}) {
+      const int64_t ns = vr * (vc / bc);
+      LRQ(lrq_fp8_block_quant(dv, LRQ_DTYPE_BF16, 1, vr, vc, vld, vr * vld, 1, bc, dcodes[1], dvs, 0,
+                              (lrq_stream_t)st));
+      HIP(hipStreamSynchronize(st));
+      std::vector<uint8_t> got((size_t)(vr * vc)), want(got.size());
+      std::vector<float> gs((size_t)ns), ws(gs.size());
+      HIP(hipMemcpy(got.data(), dcodes[1], got.size(), hipMemcpyDeviceToHost));
+      HIP(hipMemcpy(gs.data(), dvs, gs.size() * 4, hipMemcpyDeviceToHost));
+      lrqo_fp8_block_quant(hv.data(), LRQ_DTYPE_BF16, 0, 1, vr, vc, vc, vr * vc, 1, bc, 0, want.data(), ws.data(), 0);
+      expect(got == want && memcmp(gs.data(), ws.data(), gs.size() * 4) == 0,
+             bc == 128 ? "lrq_fp8_block_quant 1x128, offset view" : "lrq_fp8_block_quant 1x36, offset view");
+    }
+    HIP(hipFree(dvs));
+  }
+
   // 2. grouped: both tensors in one launch through a hand-uploaded table
   lrq_tensor ts[2];
   for (int i = 0; i < 2; ++i) {
