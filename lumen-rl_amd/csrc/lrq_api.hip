@@ -40,7 +40,7 @@ bool pow2_block(int64_t b) { return b == 32 || b == 64 || b == 128 || b == 256 |
 bool row_block(int64_t b) { return pow2_block(b) || b == 1024 || b == 2048; }
 
 constexpr uint32_t kMagic = 0x4C525154u;  // "LRQT"
-constexpr uint32_t kTableVersion = 3u;  // 3: LaunchCfg gained `pitched`
+constexpr uint32_t kTableVersion = 4u;  // 4: LaunchCfg gained `pitched` and `chunk`
 // HIP takes a launch's thread count (work-groups x threads per work-group) as
 // a 32-bit value.  kMaxGrid is the limit for 256-thread work-groups;
 // max_units() gives it per kernel.
@@ -231,7 +231,7 @@ bool plan_units(const LaunchCfg& cfg, Desc& d) {
       d.units_r = (d.rows + cfg.blk_r - 1) / cfg.blk_r;
       d.units_c = (d.cols + cfg.blk_c - 1) / cfg.blk_c;
       if (cfg.kernel == kKernDequant) {
-        const int64_t cpc = cfg.out_dtype == kBF16 ? 8 : 4;  // codes per lane-chunk
+        const int64_t cpc = cfg.chunk;  // codes per lane-chunk
         d.nblocks = d.batch * d.rows * d.cols / cpc;
         d.units = (d.nblocks + 256 * kDequantChunks - 1) / (256 * kDequantChunks);
       } else {
@@ -357,6 +357,12 @@ int plan_group(int fmt, const lrq_tensor* ts, int64_t n, int in_dtype, int64_t b
     cfg.blk_r = (int)blk_r;
     cfg.blk_c = (int)blk_c;
     cfg.out_dtype = (flags & LRQ_FLAG_OUT_BF16) ? lrq::kBF16 : lrq::kF32;
+    // a lane-chunk lies inside one block and one row: 8 codes (one 16-byte
+    // bf16 store) when every width allows, else 4 (16-byte float32 or 8-byte
+    // bf16 stores)
+    cfg.chunk = cfg.out_dtype == lrq::kBF16 && blk_c % 8 == 0 ? 8 : 4;
+    for (int64_t i = 0; i < n; ++i)
+      if (ts[i].cols % cfg.chunk != 0) cfg.chunk = 4;
   } else if (fmt == LRQ_FMT_TENSOR_SCALE) {
     cfg.kernel = lrq::kKernAmax;
   } else if (fmt == LRQ_FMT_COPY) {
@@ -447,7 +453,7 @@ int plan_group(int fmt, const lrq_tensor* ts, int64_t n, int in_dtype, int64_t b
     } else if (fmt == LRQ_FMT_FP8_DEQUANT) {
       if (d.ld != d.cols || d.bstride != d.rows * d.cols)
         return fail(LRQ_ERR_ARG, "tensor %lld: dequant needs dense codes (ld == cols)", (long long)i);
-      k = dequant_kernel_for(d, blk_c, cfg.out_dtype == lrq::kBF16 ? 8 : 4);
+      k = dequant_kernel_for(d, blk_c, cfg.chunk);
     } else {
       if (d.cols % 32 != 0) return fail(LRQ_ERR_ARG, "tensor %lld: cols %% 32 != 0", (long long)i);
       k = mx_kernel_for(d, in_dtype, cfg.mx_fmt);

@@ -70,10 +70,11 @@ __device__ __forceinline__ bool word_has_nan_code(uint32_t w) {
   return (((w & 0x7F7F7F7Fu) + 0x01010101u) & 0x80808080u) != 0u;
 }
 
-template <int SDT, int ODT, bool ROWS1>
+template <int SDT, int ODT, bool ROWS1, int CPC>
 __global__ __launch_bounds__(256) void k_dequant(Desc single, const Desc* __restrict__ descs,
                                                  const uint32_t* __restrict__ map, int blk_r, int blk_c) {
-  constexpr int CPC = ODT == kBF16 ? 8 : 4;  // codes per lane-chunk
+  // CPC codes per lane-chunk: 8 (bf16 out, one 16-byte store) or 4 (float32
+  // out, one 16-byte store; bf16 out for widths 8 does not divide, 8 bytes)
   constexpr int NW = CPC / 4;                // code words per chunk
   constexpr int NCH = kDequantChunks;        // chunks per lane
   Desc d;
@@ -106,7 +107,7 @@ __global__ __launch_bounds__(256) void k_dequant(Desc single, const Desc* __rest
     const int64_t si = ROWS1 ? (at[j] * CPC) / blk_c : scale_index(d, at[j] * CPC, blk_r, blk_c);
     sc[j] = load_scale<SDT>(d.scales, si);
   }
-  v4u val[NCH];  // every chunk decoded before the first store
+  v4u val[NCH];  // every chunk decoded before the first store (bf16 x 4: .x, .y)
 #pragma unroll
   for (int j = 0; j < NCH; ++j) {
     const float s = sc[j];
@@ -130,22 +131,24 @@ __global__ __launch_bounds__(256) void k_dequant(Desc single, const Desc* __rest
       for (int k = 0; k < CPC; ++k) o[k] = x86_mul(e4m3_decode((cw[j][k >> 2] >> (8 * (k & 3))) & 0xFFu), s);
     }
     if constexpr (ODT == kBF16) {
-      if (fast) {
-        val[j] = {bf16x2_bits(o[0], o[1]), bf16x2_bits(o[2], o[3]), bf16x2_bits(o[4], o[5]),
-                  bf16x2_bits(o[6], o[7])};
-      } else {
-        val[j] = {bf16_bits(o[0]) | (bf16_bits(o[1]) << 16), bf16_bits(o[2]) | (bf16_bits(o[3]) << 16),
-                  bf16_bits(o[4]) | (bf16_bits(o[5]) << 16), bf16_bits(o[6]) | (bf16_bits(o[7]) << 16)};
-      }
+      uint32_t w[CPC / 2];
+#pragma unroll
+      for (int k = 0; k < CPC / 2; ++k)
+        w[k] = fast ? bf16x2_bits(o[2 * k], o[2 * k + 1]) : bf16_bits(o[2 * k]) | (bf16_bits(o[2 * k + 1]) << 16);
+      if constexpr (CPC == 8) val[j] = {w[0], w[1], w[2], w[3]};
+      else val[j] = {w[0], w[1], 0u, 0u};
     } else {
       val[j] = {f2u(o[0]), f2u(o[1]), f2u(o[2]), f2u(o[3])};
     }
   }
   uint8_t* out = static_cast<uint8_t*>(d.codes);
-  constexpr int OB = CPC * (ODT == kBF16 ? 2 : 4);  // output bytes per chunk
+  constexpr int OB = CPC * (ODT == kBF16 ? 2 : 4);  // output bytes per chunk: 16, or 8 (bf16 x 4)
 #pragma unroll
-  for (int j = 0; j < NCH; ++j)
-    if (ok[j]) gst_nt<v4u>(out + at[j] * OB, val[j]);
+  for (int j = 0; j < NCH; ++j) {
+    if (!ok[j]) continue;
+    if constexpr (OB == 16) gst_nt<v4u>(out + at[j] * OB, val[j]);
+    else store_nt(out + at[j] * OB, v2u{val[j].x, val[j].y});
+  }
 }
 
 template <int SDT, int ODT>
@@ -153,10 +156,15 @@ static hipError_t launch_dq(const LaunchCfg& cfg, const Desc& single, const Desc
                             const uint32_t* map, int64_t units, hipStream_t stream) {
   const dim3 grid((unsigned)units), block(256);
   const bool rows1 = cfg.blk_r == 1 && (map != nullptr ? cfg.rows_dense : (single.cols % cfg.blk_c == 0));
-  if (cfg.kernel == kKernDequant && rows1)
-    hipLaunchKernelGGL((k_dequant<SDT, ODT, true>), grid, block, 0, stream, single, descs, map, cfg.blk_r, cfg.blk_c);
-  else if (cfg.kernel == kKernDequant)
-    hipLaunchKernelGGL((k_dequant<SDT, ODT, false>), grid, block, 0, stream, single, descs, map, cfg.blk_r, cfg.blk_c);
+  constexpr int C0 = ODT == kBF16 ? 8 : 4;  // the chunk of full 16-byte stores
+  if (cfg.kernel == kKernDequant && cfg.chunk == C0 && rows1)
+    hipLaunchKernelGGL((k_dequant<SDT, ODT, true, C0>), grid, block, 0, stream, single, descs, map, cfg.blk_r, cfg.blk_c);
+  else if (cfg.kernel == kKernDequant && cfg.chunk == C0)
+    hipLaunchKernelGGL((k_dequant<SDT, ODT, false, C0>), grid, block, 0, stream, single, descs, map, cfg.blk_r, cfg.blk_c);
+  else if (ODT == kBF16 && cfg.kernel == kKernDequant && rows1)
+    hipLaunchKernelGGL((k_dequant<SDT, ODT, true, 4>), grid, block, 0, stream, single, descs, map, cfg.blk_r, cfg.blk_c);
+  else if (ODT == kBF16 && cfg.kernel == kKernDequant)
+    hipLaunchKernelGGL((k_dequant<SDT, ODT, false, 4>), grid, block, 0, stream, single, descs, map, cfg.blk_r, cfg.blk_c);
   else
     hipLaunchKernelGGL((k_dequant_generic<SDT, ODT>), grid, block, 0, stream, single, descs, map, cfg.blk_r, cfg.blk_c);
   return hipGetLastError();
@@ -271,22 +279,24 @@ __global__ __launch_bounds__(256) void k_mx_dequant(Desc single, const Desc* __r
       }
     }
     if constexpr (ODT == kBF16) {
-      if (fast) {
-        val[j] = {bf16x2_bits(o[0], o[1]), bf16x2_bits(o[2], o[3]), bf16x2_bits(o[4], o[5]),
-                  bf16x2_bits(o[6], o[7])};
-      } else {
-        val[j] = {bf16_bits(o[0]) | (bf16_bits(o[1]) << 16), bf16_bits(o[2]) | (bf16_bits(o[3]) << 16),
-                  bf16_bits(o[4]) | (bf16_bits(o[5]) << 16), bf16_bits(o[6]) | (bf16_bits(o[7]) << 16)};
-      }
+      uint32_t w[CPC / 2];
+#pragma unroll
+      for (int k = 0; k < CPC / 2; ++k)
+        w[k] = fast ? bf16x2_bits(o[2 * k], o[2 * k + 1]) : bf16_bits(o[2 * k]) | (bf16_bits(o[2 * k + 1]) << 16);
+      if constexpr (CPC == 8) val[j] = {w[0], w[1], w[2], w[3]};
+      else val[j] = {w[0], w[1], 0u, 0u};
     } else {
       val[j] = {f2u(o[0]), f2u(o[1]), f2u(o[2]), f2u(o[3])};
     }
   }
   uint8_t* out = static_cast<uint8_t*>(d.codes);
-  constexpr int OB = CPC * (ODT == kBF16 ? 2 : 4);  // output bytes per chunk
+  constexpr int OB = CPC * (ODT == kBF16 ? 2 : 4);  // output bytes per chunk: 16, or 8 (bf16 x 4)
 #pragma unroll
-  for (int j = 0; j < NCH; ++j)
-    if (ok[j]) gst_nt<v4u>(out + at[j] * OB, val[j]);
+  for (int j = 0; j < NCH; ++j) {
+    if (!ok[j]) continue;
+    if constexpr (OB == 16) gst_nt<v4u>(out + at[j] * OB, val[j]);
+    else store_nt(out + at[j] * OB, v2u{val[j].x, val[j].y});
+  }
 }
 
 hipError_t launch_mx_dequant(const LaunchCfg& cfg, const Desc& single, const Desc* descs,

@@ -105,6 +105,7 @@ struct LaunchCfg {
   int out_dtype;  // dequant: kF32 or kBF16 (in_dtype is then the scale dtype)
   int rows_dense; // dequant, 1xB: every tensor has cols % blk_c == 0
   int pitched;    // float64 rows: some tensor's row pitch exceeds its width
+  int chunk;      // FP8 dequant: codes per lane-chunk (8: bf16 out, 4: float32 out or narrow blocks)
 };
 
 // Work-groups a tensor needs under `cfg` (filled into d.units and the unit

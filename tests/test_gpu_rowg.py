@@ -123,3 +123,33 @@ def test_tiny_blocks_past_one_launch():
     oc, osc = O.fp8_block_quant(host(x, "bf16"), "bf16", "f32", (1, 5), nthreads=16)
     assert np.array_equal(c.view(torch.uint8).cpu().numpy(), oc[0])
     assert np.array_equal(s.cpu().numpy().view(np.uint32), osc[0].view(np.uint32))
+
+
+@pytest.mark.parametrize("B", [8, 12, 36, 96, 100, 1000])
+@pytest.mark.parametrize("odt", [torch.float32, torch.bfloat16])
+def test_dequant_widths_vs_reference_ops(B, odt):
+    """dequantize_tensor (weight_quantizer.py:79-89) at widths the lane-chunks
+    fit differently: 8 codes per chunk (bf16 out, 8 | B), 4 (float32 out, or
+    bf16 out with 4 | B but not 8: 12, 36, 100), the per-element kernel
+    otherwise; the bf16 output is the reference's float32 result cast, as
+    dequantize_state_dict does (:133).  Codes also read from a view 3 bytes
+    into its storage."""
+    print("rowg dequant", B, odt, flush=True)
+    g = torch.Generator().manual_seed(B)
+    w = (torch.randn(97, B * 7, generator=g) * 0.05).to(torch.bfloat16)
+    w[3, :B] = 0.0
+    w[5, 2] = float("inf")
+    w[9, 1] = float("nan")
+    q, s = TR.quantize_tensor(w, B)
+    want = TR.dequantize_tensor(q, s, B).to(odt)
+    got = ops.fp8_block_dequant(q.to(DEV), s.to(DEV), (1, B), odt)
+    buf = torch.zeros(q.numel() + 16, dtype=torch.uint8, device=DEV)
+    buf[3:3 + q.numel()] = q.view(torch.uint8).reshape(-1).to(DEV)
+    got_view = ops.fp8_block_dequant(buf[3:3 + q.numel()].view(q.shape), s.to(DEV), (1, B), odt)
+    torch.cuda.synchronize()
+    ints = torch.int32 if odt == torch.float32 else torch.int16
+    for g_ in (got, got_view):
+        g_ = g_.cpu()
+        nan = torch.isnan(g_)
+        assert torch.equal(nan, torch.isnan(want))
+        assert torch.equal(g_[~nan].view(ints), want[~nan].view(ints))
