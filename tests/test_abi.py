@@ -440,3 +440,20 @@ def test_float64_input_needs_float64_arithmetic_and_the_fp8_block_format():
     assert units(40, 256, 256) == 5
     assert units(40, 256, 384) == 5
     assert units(5, 288, 288, 96) == (5 * 3 + 3) // 4
+
+
+def test_fp8_dequant_chunk_per_width():
+    """FP8 dequant lane-chunks: 8 codes for bf16 output when 8 divides the block
+    width and every row, else 4 (a 4-code bf16 chunk stores 8 bytes); 512
+    chunks per work-group; widths 4 does not divide take the per-element kernel
+    (256 elements per work-group)."""
+    def units(cols, blk_c, out_bf16, rows=64):
+        flags = _lib.FLAG_OUT_BF16 if out_bf16 else 0
+        return L().lrq_group_units(_pack(_lib.FMT_FP8_DEQUANT, [(1, rows, cols)], (1, blk_c), flags).ctypes.data)
+
+    n = 64 * 1152
+    assert units(1152, 128, True) == -(-n // 8 // 512)
+    assert units(1152, 36, True) == -(-n // 4 // 512)
+    assert units(1152, 128, False) == -(-n // 4 // 512)
+    assert units(1152, 36, False) == -(-n // 4 // 512)
+    assert units(1152, 6, True) == -(-n // 256)
