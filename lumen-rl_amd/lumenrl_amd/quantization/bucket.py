@@ -53,7 +53,9 @@ class _Entry:
 
 class Bucket:
     """One planned bucket: grouped quantize launches (one per input dtype: a
-    bucket may hold bf16 weights next to an fp32 router gate) plus the
+    bucket may hold bf16 weights next to an fp32 router gate; weights whose
+    width 8 does not divide, which a custom ``quantize_if`` may admit, get a
+    launch of their own kind) plus the
     pass-through copies, which (16-byte-aligned sources, the torch norm) go in
     one grouped copy launch.
 
@@ -69,9 +71,10 @@ class Bucket:
         self.copies = copies
         self._src = src
         self.nbytes = max((e.offset + e.nbytes for e in entries), default=0)
-        by_dtype: dict[torch.dtype, list[tuple[str, Tensor, Tensor]]] = {}
+        by_dtype: dict[tuple, list[tuple[str, Tensor, Tensor]]] = {}
         for name, codes, scales in quant:
-            by_dtype.setdefault(src[name].dtype, []).append((name, codes, scales))
+            key = (src[name].dtype, src[name].shape[-1] % 8 == 0)  # one kernel per plan
+            by_dtype.setdefault(key, []).append((name, codes, scales))
         self.plans: list[tuple[list[str], ops.QuantPlan]] = [
             ([n for n, _, _ in items],
              ops.QuantPlan([src[n] for n, _, _ in items], fmt, block_size,

@@ -192,6 +192,18 @@ def test_mixed_dtype_bucket_decoded_like_the_reference_receivers():
         writer.rebind([("nope", weight((512, 128)))])
 
 
+def test_bucket_with_a_width_8_does_not_divide():
+    """A custom quantize_if may admit a [130, 100] weight: its 128x128 tiles need
+    the generic kernel, so it gets a launch of its own next to the vector one."""
+    named = [("a.q_proj.weight", weight((256, 512))), ("a.odd_proj.weight", weight((130, 100))),
+             ("a.k_proj.weight", weight((128, 256)))]
+    writer = QuantizedBucketWriter(named, bucket_bytes=4 << 20, fmt="fp8_block",
+                                   quantize_if=lambda n, t: t.dim() == 2)
+    assert len(writer) == 1 and len(writer.buckets[0].plans) == 2
+    seen = check_received(writer, dict(named))
+    assert seen == {n for n, _ in named} | {n + "_scale_inv" for n, _ in named}
+
+
 def test_encode_bucket_like_the_rccl_sender():
     """encode_bucket mirrors _encode_bucket (rdma_weight_transfer.py:22-57): compact
     JSON metadata as a uint8 device tensor, and a payload the receiver decodes with
