@@ -85,6 +85,31 @@ def test_mx(base, fmt):
     same(s, osc.reshape(BASE_ROWS, -1), f"mx{fmt} scales")
 
 
+@pytest.mark.parametrize("blk", [(1, 36), (1, 4096)])
+def test_fp8_row_widths(base, blk):
+    """1x36 (padded lane groups, the last chunk overlapped) over the first 32760
+    columns of each row, a strided view of 2.15 G elements; 1x4096 (the
+    wide-row kernel) over the whole tensor."""
+    say("large fp8 rows", blk)
+    x = big_of(base)
+    cols = COLS - COLS % blk[1]
+    c, s = ops.fp8_block_quant(x[:, :cols], blk)
+    torch.cuda.synchronize()
+    oc, osc = O.fp8_block_quant(np.ascontiguousarray(bf16_np(base)[:, :cols]), "bf16", "f32", blk, nthreads=16)
+    same(c, oc.reshape(BASE_ROWS, cols), f"codes {blk}")
+    same(s, osc.view(np.int32).reshape(-1, s.shape[1]), f"scales {blk}")
+
+
+def test_mx_float32_input(base):
+    say("large mx float32")
+    x = big_of(base, torch.float32)
+    c, s = ops.quantize_mxfp8(x)
+    torch.cuda.synchronize()
+    oc, osc = O.mx_quant(base.float().numpy(), "f32", 8, nthreads=16)
+    same(c, oc.reshape(BASE_ROWS, -1), "mx8 f32 codes")
+    same(s, osc.reshape(BASE_ROWS, -1), "mx8 f32 scales")
+
+
 def test_fp8_dequant_to_bf16(base):
     say("large dequant")
     x = big_of(base)
