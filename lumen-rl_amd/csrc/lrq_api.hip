@@ -117,6 +117,10 @@ int fp8_kernel_for(const Desc& d, int in_dtype, int64_t blk_r, int64_t blk_c) {
                      (d.batch == 1 || d.bstride == d.rows * d.ld) && aligned(d.in, 8) &&
                      aligned(d.codes, 2) && aligned(d.scales, 8);
     if (row) return lrq::kKernF64Row;
+    // other widths 2..4096 (2-double chunks, the last overlapped when B is odd)
+    const bool wide = blk_r == 1 && blk_c >= 2 && blk_c <= 4096 && d.cols % blk_c == 0 &&
+                      (d.batch == 1 || d.bstride == d.rows * d.ld) && aligned(d.in, 8) && aligned(d.scales, 8);
+    if (wide) return lrq::kKernF64Wide;
     const bool tile = blk_r == 128 && blk_c == 128 && aligned(d.in, 8) && d.cols % 2 == 0 &&
                       aligned(d.codes, 2) && aligned(d.scales, 8);
     return tile ? lrq::kKernF64Tile : lrq::kKernF64;
@@ -180,6 +184,15 @@ bool plan_units(const LaunchCfg& cfg, Desc& d) {
       if (!fold_batch(d)) return false;
       const int64_t per_wg = 4 * f64_row_instr(cfg.blk_c) * 128;
       d.units = (d.batch * d.rows * d.cols + per_wg - 1) / per_wg;
+      return true;
+    }
+    case kKernF64Wide: {  // 4 waves of P blocks each (B <= 1024), or one block of 4 waves
+      if (!fold_batch(d)) return false;
+      d.bpr = d.cols / cfg.blk_c;
+      d.nblocks = d.rows * d.bpr;
+      const int P = f64_wide_blocks_per_wave(cfg.blk_c);
+      const int64_t per_wg = P > 0 ? 4 * P : 1;
+      d.units = (d.nblocks + per_wg - 1) / per_wg;
       return true;
     }
     case kKernF64:  // one wave per block, four per work-group
@@ -263,7 +276,8 @@ hipError_t launch(const LaunchCfg& cfg, const Desc& single, const Desc* descs_de
     return launch_mx(cfg, single, descs_dev, map_dev, total_units, stream);
   if (cfg.kernel == kKernDequant || cfg.kernel == kKernGenericDequant)
     return launch_dequant(cfg, single, descs_dev, map_dev, total_units, stream);
-  if (cfg.kernel == kKernF64 || cfg.kernel == kKernF64Row || cfg.kernel == kKernF64Tile)
+  if (cfg.kernel == kKernF64 || cfg.kernel == kKernF64Row || cfg.kernel == kKernF64Tile ||
+      cfg.kernel == kKernF64Wide)
     return launch_f64(cfg, single, descs_dev, map_dev, total_units, stream);
   return launch_fp8(cfg, single, descs_dev, map_dev, total_units, stream);
 }

@@ -315,6 +315,10 @@ __device__ __forceinline__ void store_nt(void* p, v2u v) {
 __device__ __forceinline__ void store_nt(void* p, uint32_t v) {
   __builtin_nontemporal_store(v, (LRQ_GLOBAL u32_out*)p);
 }
+typedef uint16_t u16_out __attribute__((aligned(1)));
+__device__ __forceinline__ void store_nt2(void* p, uint16_t v) {
+  __builtin_nontemporal_store(v, (LRQ_GLOBAL u16_out*)p);
+}
 
 // MI355X dispatches work-group i to XCD i % 8.  Work units adjacent in memory
 // (the tiles of a 128-row band, consecutive row blocks) are given to one XCD in

@@ -394,6 +394,104 @@ __global__ __launch_bounds__(512) void k_tile_f64(Desc single, const Desc* __res
   else tile_f64<false>(d, u, b, r0, col, pow2, red);
 }
 
+// 1xB blocks of a float64 tensor for the widths k_row_f64 does not take (B not
+// a power of two, or 4096; 2 <= B <= 4096): ceil(B/2) chunks of 2 doubles (16
+// bytes), the last starting at B - 2 when B is odd (it overlaps its
+// neighbour: the amax ignores the repeat, and both lanes write the same
+// codes).  As k_row_wide: W waves per block (1 up to B = 1024, else 4), lane l
+// of wave w holding chunks 64 w + l + 64 W k for k < K = ceil(g / 64W) <= 8;
+// with W = 1 a wave takes P consecutive blocks.  Lanes past a block's end,
+// and slots past K, re-load its first chunk and drop out of the amax, so the
+// loads issue without branches.  Quotients as in k_row_f64 (Markstein's step in
+// fast blocks, IEEE division otherwise).
+template <int W, int P>
+__global__ __launch_bounds__(256) void k_row_wide_f64(Desc single, const Desc* __restrict__ descs,
+                                                      const uint32_t* __restrict__ map, int pow2, int bw) {
+  static_assert(W == 1 || P == 1, "blocks of several waves: one block per wave group");
+  constexpr int KP = 8 / P;  // chunk slots per block
+  __shared__ uint64_t red[4];
+  Desc d;
+  int64_t u;
+  pick_desc<kXcdRunRow>(single, descs, map, d, u);
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int g = (bw + 1) / 2;  // chunks per block
+  const int K = (g + 64 * W - 1) / (64 * W);
+  const int64_t blk0 = (u * (4 / W) + wave / W) * P;
+  const int c0 = 64 * (wave % W) + lane;
+  const double* in = static_cast<const double*>(d.in);
+
+  bool live[P];
+  int64_t gb[P];
+  v4u raw[P][KP];
+#pragma unroll
+  for (int p = 0; p < P; ++p) {
+    live[p] = blk0 + p < d.nblocks;  // the same for the W waves of a block
+    gb[p] = live[p] ? blk0 + p : d.nblocks - 1;
+    const int64_t row = gb[p] / d.bpr;
+    const int64_t base = row * d.ld + (gb[p] - row * d.bpr) * bw;
+#pragma unroll
+    for (int k = 0; k < KP; ++k) {
+      // every slot loads (past the block's chunks: its first chunk again, an
+      // L2 hit), so the loads carry no branches and issue back to back
+      const int c = c0 + 64 * W * k;
+      const bool ok = k < K && c < g;
+      raw[p][k] = load_nt(in + base + (ok ? (2 * c > bw - 2 ? bw - 2 : 2 * c) : 0));
+    }
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  uint64_t am[P];  // block maxima, wave-uniform
+#pragma unroll
+  for (int p = 0; p < P; ++p) {
+    uint64_t a = 0;
+#pragma unroll
+    for (int k = 0; k < KP; ++k) {
+      const bool ok = k < K && c0 + 64 * W * k < g;
+      const uint64_t m = umax64((((uint64_t)raw[p][k].y << 32) | raw[p][k].x) & kAbs64,
+                                (((uint64_t)raw[p][k].w << 32) | raw[p][k].z) & kAbs64);
+      a = umax64(a, ok ? m : 0);
+    }
+    a = group_max_u64<64>(a);
+    if constexpr (W > 1) {
+      if (lane == 0) red[wave] = a;
+      __syncthreads();
+      const int w0 = wave & ~(W - 1);
+#pragma unroll
+      for (int w = 0; w < W; ++w) a = umax64(a, red[w0 + w]);
+    }
+    am[p] = a;
+  }
+  // one pass of the float64 scale math for all P blocks: lane p computes block
+  // p's scale and 1/s, which readlane hands to the whole wave
+  uint64_t mine = am[0];
+#pragma unroll
+  for (int p = 1; p < P; ++p) mine = (lane % P) == p ? am[p] : mine;
+  double s_l;
+  int kind_l;
+  block_scale_f64(mine, pow2 != 0, s_l, kind_l);
+  const double y_l = 1.0 / s_l;  // correctly rounded
+#pragma unroll
+  for (int p = 0; p < P; ++p) {
+    if (!live[p]) continue;
+    const double s = readlane_f64(s_l, p), y = readlane_f64(y_l, p);
+    const int kind = __builtin_amdgcn_readlane(kind_l, p);
+    const bool fast = fast_block(s, kind);
+    if (c0 == 0) gst<double>(static_cast<double*>(d.scales) + gb[p], s);
+#pragma unroll
+    for (int k = 0; k < KP; ++k) {
+      const int c = c0 + 64 * W * k;
+      if (k < K && c < g) {
+        const int64_t off = 2 * c > bw - 2 ? bw - 2 : 2 * c;
+        const uint64_t x0 = ((uint64_t)raw[p][k].y << 32) | raw[p][k].x;
+        const uint64_t x1 = ((uint64_t)raw[p][k].w << 32) | raw[p][k].z;
+        store_nt2(d.codes + gb[p] * bw + off, (uint16_t)code2_f64(x0, x1, s, y, kind, fast));
+      }
+      // one chunk's quotients at a time: interleaving all of them would take
+      // four times the registers (occupancy 2)
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  }
+}
+
 hipError_t launch_f64(const LaunchCfg& cfg, const Desc& single, const Desc* descs,
                       const uint32_t* map, int64_t units, hipStream_t stream) {
   const dim3 grid((unsigned)units), block(256);
@@ -420,6 +518,16 @@ hipError_t launch_f64(const LaunchCfg& cfg, const Desc& single, const Desc* desc
         case 2048: hipLaunchKernelGGL((k_row_f64<2048, false>), grid, block, 0, stream, single, descs, map, cfg.pow2); break;
         default: return hipErrorInvalidValue;
       }
+    }
+    return hipGetLastError();
+  }
+  if (cfg.kernel == kKernF64Wide) {
+    const int bw = cfg.blk_c;
+    switch (f64_wide_blocks_per_wave(cfg.blk_c)) {
+      case 4: hipLaunchKernelGGL((k_row_wide_f64<1, 4>), grid, block, 0, stream, single, descs, map, cfg.pow2, bw); break;
+      case 2: hipLaunchKernelGGL((k_row_wide_f64<1, 2>), grid, block, 0, stream, single, descs, map, cfg.pow2, bw); break;
+      case 1: hipLaunchKernelGGL((k_row_wide_f64<1, 1>), grid, block, 0, stream, single, descs, map, cfg.pow2, bw); break;
+      default: hipLaunchKernelGGL((k_row_wide_f64<4, 1>), grid, block, 0, stream, single, descs, map, cfg.pow2, bw); break;
     }
     return hipGetLastError();
   }

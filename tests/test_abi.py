@@ -423,23 +423,27 @@ def test_float64_input_needs_float64_arithmetic_and_the_fp8_block_format():
     # tables pack (host memory only) with each float64 kernel's geometry: a dense
     # 1x128 tensor, dense or with a padded row pitch, takes the row kernel (4
     # waves x 4 instructions of 128 doubles of the element sequence per
-    # work-group); a 1x96 block the generic kernel (one wave per block, four
-    # per work-group)
-    def units(rows, cols, ld, blk=128):
+    # work-group); a 1x96 block the wide-row kernel (4 blocks per wave, 16 per
+    # work-group); a 2-D block the generic kernel (one wave per block, four per
+    # work-group)
+    def units(rows, cols, ld, blk=128, blk_r=1):
         t = (_lib.LrqTensor * 1)()
         t[0].in_, t[0].codes, t[0].scales = 0x10000, 0x20000, 0x30000
         t[0].batch, t[0].rows, t[0].cols, t[0].ld, t[0].batch_stride = 1, rows, cols, ld, rows * ld
-        need = L().lrq_group_table_bytes(_lib.FMT_FP8_BLOCK, t, 1, _lib.DTYPE_F64, 1, blk,
+        need = L().lrq_group_table_bytes(_lib.FMT_FP8_BLOCK, t, 1, _lib.DTYPE_F64, blk_r, blk,
                                          _lib.FLAG_NATIVE_ARITH)
         host = (ctypes.c_uint8 * need)()
-        assert L().lrq_group_pack(_lib.FMT_FP8_BLOCK, t, 1, _lib.DTYPE_F64, 1, blk,
+        assert L().lrq_group_pack(_lib.FMT_FP8_BLOCK, t, 1, _lib.DTYPE_F64, blk_r, blk,
                                   _lib.FLAG_NATIVE_ARITH, host, need) == 0
         return L().lrq_group_units(host)
 
     assert units(5, 256, 256) == 1
     assert units(40, 256, 256) == 5
     assert units(40, 256, 384) == 5
-    assert units(5, 288, 288, 96) == (5 * 3 + 3) // 4
+    assert units(5, 288, 288, 96) == -(-5 * 3 // 16)   # wide rows: 4 waves x 4 blocks
+    assert units(50, 768, 800, 384) == -(-50 * 2 // 8)  # 2 blocks per wave
+    assert units(9, 3000, 3000, 3000) == 9              # one block of 4 waves
+    assert units(5, 288, 288, 96, 2) == (3 * 3 + 3) // 4  # 2-D blocks: generic
 
 
 def test_fp8_dequant_chunk_per_width():

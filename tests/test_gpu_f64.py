@@ -67,11 +67,12 @@ def check(xd: torch.Tensor, blk, pow2):
 
 @pytest.mark.parametrize("pow2", [False, True])
 @pytest.mark.parametrize("blk", [(1, 128), (1, 32), (1, 64), (1, 256), (1, 512), (1, 1024), (1, 2048), (1, 96),
-                                 (1, 384), (128, 128), (3, 40), (64, 96)])
+                                 (1, 384), (1, 2), (1, 3), (1, 45), (1, 100), (1, 1000), (1, 3000), (1, 4096),
+                                 (128, 128), (3, 40), (64, 96)])
 @pytest.mark.parametrize("data", ["weights", "edge"])
 def test_f64_blocks_vs_oracle(data, blk, pow2):
     say("f64", data, blk, pow2)
-    cols = blk[1] * 2 if blk[1] >= 512 else 384
+    cols = blk[1] * 2 if blk[1] >= 512 else blk[1] * -(-384 // blk[1])
     if data == "weights":
         x = RNG.normal(0, 0.02, (200, cols))
         x.flat[RNG.integers(0, x.size, 80)] *= 150
@@ -86,6 +87,8 @@ def test_f64_views_and_batches(pow2):
     check(base[:, 64:448], (1, 128), pow2)          # row stride 640, offset view
     check(base[::3, :512], (1, 128), pow2)          # row stride 1920
     check(base[::2, :512], (1, 512), pow2)          # row stride 1280, one block per row
+    check(base[:, 3:603], (1, 100), pow2)           # wide rows: row stride 640, 8 bytes off 16
+    check(base[:, 1:46], (1, 45), pow2)             # odd width: the last chunk overlaps
     check(base[:40].reshape(5, 8, 640), (1, 64), pow2)  # batched matrices
     check(base.reshape(3, 16, 640)[:, :, :384], (8, 128), pow2)  # strided batch, 2-D blocks
     e = torch.empty(0, 128, dtype=torch.float64, device=DEV)

@@ -30,7 +30,7 @@ if not torch.cuda.is_available():  # pragma: no cover - CPU container
 DEV = torch.device("cuda", 0)
 DT = {"bf16": torch.bfloat16, "f16": torch.float16, "f32": torch.float32}
 KINDS = ["tile", "row", "mx8", "mx4", "cast", "kv", "deq", "mxdeq", "blk", "f64"]
-F64_BLOCKS = [(1, 32), (1, 128), (1, 512), (128, 128), (3, 40), (1, 96), (1, 1024)]
+F64_BLOCKS = [(1, 32), (1, 128), (1, 512), (128, 128), (3, 40), (1, 96), (1, 1024), (1, 45), (1, 3000)]
 BLOCKS = [(1, 32), (1, 64), (1, 256), (1, 512), (3, 40), (64, 96), (128, 64), (2, 128), (1, 96), (1, 40), (1, 16),
           (1, 1024), (1, 8), (1, 1536), (1, 4104), (1, 36), (1, 100), (1, 12)]
 
@@ -157,25 +157,28 @@ def test_grouped_plans_random_sweep(seed):
 
 
 def _f64_case(rng, seed, case):
-    """One grouped float64 plan: dense tensors with 1xB rows (the row kernel);
-    128x128 tiles over even widths and row pitches (the tile kernel) or odd
-    widths (the generic kernel); any other block over possibly strided tensors
-    (the generic kernel).  One kernel per plan, as a grouped table requires."""
+    """One grouped float64 plan: 1xB rows over widths that B divides (the row
+    kernel for powers of two, the wide-row kernel for other B), possibly
+    strided; 128x128 tiles over even widths (the tile kernel) or odd widths
+    (the generic kernel); 1xB blocks over widths B does not divide, and 2-D
+    blocks (the generic kernel).  One kernel per plan, as a grouped table
+    requires."""
     blk = F64_BLOCKS[rng.integers(0, len(F64_BLOCKS))]
-    row = blk[0] == 1 and blk[1] in (32, 64, 128, 256, 512)
+    row = blk[0] == 1 and rng.random() < 0.7  # whole blocks: row or wide-row kernel
     even = blk == (128, 128) and rng.random() < 0.6
     pow2 = bool(rng.random() < 0.3)
     ts = []
     for _ in range(int(rng.integers(1, 9))):
         rows = int(rng.integers(1, 300))
         if row:
-            cols = blk[1] * int(rng.integers(1, 9))
+            cols = blk[1] * int(rng.integers(1, 9 if blk[1] <= 512 else 3))
         elif blk == (128, 128):
             cols = 2 * int(rng.integers(1, 200)) + (0 if even else 1)
         else:
             cols = int(rng.integers(1, 400))
-        ts.append(_tensor64(rng, rows, cols, strided=not row and rng.random() < 0.3,
-                            pitch_step=2 if even else 1))
+            if blk[0] == 1 and cols % blk[1] == 0:
+                cols += 1  # a partial last block: the generic kernel
+        ts.append(_tensor64(rng, rows, cols, strided=rng.random() < 0.3, pitch_step=2 if even else 1))
     print("group sweep", seed, case, "f64", blk, pow2, [tuple(t.shape) for t in ts], flush=True)
     outs = ops.QuantPlan(ts, "fp8_block", blk, native_arith=True, use_pow2_scale=pow2).run()
     torch.cuda.synchronize()
