@@ -220,12 +220,12 @@ bool plan_units(const LaunchCfg& cfg, Desc& d) {
       d.units = (d.nblocks + per_wg - 1) / per_wg;
       return true;
     }
-    case kKernRowWide: {  // 4 waves of P blocks each (B <= 4096), or one block of 4 waves
+    case kKernRowWide: {  // 4 waves of P blocks each, or 2 or 1 blocks of 2 or 4 waves
       if (!fold_batch(d)) return false;
       d.bpr = d.cols / cfg.blk_c;
       d.nblocks = d.rows * d.bpr;
-      const int P = wide_blocks_per_wave(cfg.blk_c);
-      const int64_t per_wg = P > 0 ? 4 * P : 1;
+      const WideShape ws = wide_shape(cfg.in_dtype, cfg.blk_c);
+      const int64_t per_wg = 4 / ws.w * ws.p;
       d.units = (d.nblocks + per_wg - 1) / per_wg;
       return true;
     }

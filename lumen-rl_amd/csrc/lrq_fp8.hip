@@ -390,25 +390,26 @@ __global__ __launch_bounds__(256) void k_row_f32(Desc single, const Desc* __rest
 // ---------------------------------------------------------------------------
 // Wide 1xB row blocks, 512 < B <= 16384 (other than 1024 and 2048, which
 // k_row takes), in g = ceil(B/8) chunks: a block belongs to W waves of the
-// work-group (W = 1 up to B = 4096, else 4), whose lane l of wave w holds
-// chunks c = 64 w + l + 64 W k for k < K = ceil(g / 64W).  When 8 does not
-// divide B the last chunk starts at B - 8, overlapping its neighbour (the
-// amax ignores the repeat; both lanes write the same codes).  With W = 1 a wave
-// takes P consecutive blocks (P = 4, 2, 1 for K <= 2, 4, 8), so it keeps
-// about kWideChunks loads in flight per lane whatever the width.  Every wave
+// work-group (W = 1, 2 or 4), whose lane l of wave w holds chunks
+// c = 64 w + l + 64 W k for k < K = ceil(g / 64W).  When 8 does not divide B
+// the last chunk starts at B - 8, overlapping its neighbour (the amax ignores
+// the repeat; both lanes write the same codes).  A lane has NC chunk slots
+// (4 or 8); with W = 1 a wave takes P = NC/KP consecutive blocks of
+// KP = nextpow2(K) slots each, so it keeps about NC loads in flight per lane
+// whatever the width.  Every wave
 // instruction of a block reads 1 KiB contiguous (of bf16), except the last
 // when 64 W does not divide g: its lanes past the end, and every slot past K,
 // re-load chunk 0 of their block (in bounds, an L2 hit) and drop out of the
 // amax, so no branch separates the loads.  The W waves' maxima meet in LDS;
 // the scale math then runs once per block.
 // ---------------------------------------------------------------------------
-template <int DT, int CDT, int W, int P>
+template <int DT, int CDT, int W, int P, int NC>
 __global__ __launch_bounds__(256) void k_row_wide(Desc single, const Desc* __restrict__ descs,
                                                   const uint32_t* __restrict__ map, int pow2,
                                                   int scale_bf16, int bw) {
   static_assert(W == 1 || P == 1, "blocks of several waves: one block per wave group");
   const int g = (bw + 7) / 8;  // chunks per block
-  constexpr int KP = kWideChunks / P;  // chunk slots per block
+  constexpr int KP = NC / P;  // chunk slots per block
   __shared__ uint32_t red[4];
   Desc d;
   int64_t u;
@@ -595,12 +596,19 @@ static hipError_t launch_fp8_typed(const LaunchCfg& cfg, const Desc& single, con
     }
     case kKernRowWide: {
       const int g = (int)cfg.blk_c;  // the block width
-      switch (wide_blocks_per_wave(cfg.blk_c)) {
-        case 4: hipLaunchKernelGGL((k_row_wide<DT, CDT, 1, 4>), grid, block, 0, stream, single, descs, map, cfg.pow2, cfg.scale_bf16, g); break;
-        case 2: hipLaunchKernelGGL((k_row_wide<DT, CDT, 1, 2>), grid, block, 0, stream, single, descs, map, cfg.pow2, cfg.scale_bf16, g); break;
-        case 1: hipLaunchKernelGGL((k_row_wide<DT, CDT, 1, 1>), grid, block, 0, stream, single, descs, map, cfg.pow2, cfg.scale_bf16, g); break;
-        default: hipLaunchKernelGGL((k_row_wide<DT, CDT, 4, 1>), grid, block, 0, stream, single, descs, map, cfg.pow2, cfg.scale_bf16, g); break;
+      const WideShape ws = wide_shape(DT, cfg.blk_c);
+#define LRQ_WIDE(W, P, NC) \
+  hipLaunchKernelGGL((k_row_wide<DT, CDT, W, P, NC>), grid, block, 0, stream, single, descs, map, cfg.pow2, cfg.scale_bf16, g)
+      if (ws.nc == kWideChunks) {
+        if (ws.w == 4) LRQ_WIDE(4, 1, kWideChunks);
+        else LRQ_WIDE(1, 1, kWideChunks);
+      } else {
+        if (ws.w == 4) LRQ_WIDE(4, 1, 4);
+        else if (ws.w == 2) LRQ_WIDE(2, 1, 4);
+        else if (ws.p == 2) LRQ_WIDE(1, 2, 4);
+        else LRQ_WIDE(1, 1, 4);
       }
+#undef LRQ_WIDE
       break;
     }
     case kKernGenericFp8:

@@ -54,11 +54,25 @@ constexpr int64_t kCopyUnit = 4096;  // k_copy: bytes per work-group (one 16 B l
 constexpr int kDequantChunks = 2;    // k_dequant: 16-byte output chunks per lane (2 beat 1, 4 and 8)
 constexpr int kMxLoads = 2;          // k_mx: 32-element groups per quad of lanes (2 beat 1, 3 and 4)
 constexpr int kWideChunks = 8;       // k_row_wide: 8-element chunks per lane (at most)
-// k_row_wide's blocks per wave for a 1xB block (512 < B <= 16384):
-// 4, 2 or 1 when a block takes at most 2, 4 or 8 of a wave's 64-lane steps
-// (one wave per block), 0 when it takes four waves (B > 4096).
-constexpr int wide_blocks_per_wave(int64_t blk_c) {
-  return blk_c <= 2 * 512 ? 4 : blk_c <= 4 * 512 ? 2 : blk_c <= kWideChunks * 512 ? 1 : 0;
+// k_row_wide's launch shape for a 1xB block (512 < B <= 16384) of g =
+// ceil(B/8) chunks: the block takes C = nextpow2(ceil(g/64)) 64-lane steps of
+// chunk slots, as NC slots per lane on W = C/NC waves (at least one), and a
+// wave holds P = NC/C blocks (at least one).  Every slot past a block's chunks
+// re-loads its first chunk.  NC = 4 (43-57 VGPRs) unless the sweeps on an
+// MI355X favoured 8 (65-97 VGPRs): blocks past C = 16, blocks of exactly
+// 512 chunks (one wave, every slot used: 1x4096 by 1-2 %) and 16-bit blocks
+// of more than 768 chunks (4 waves of 4 slots, all used: 1x7168 and 1x8192 by
+// 1.5-2 %).  4 slots instead of 8 gained up to 9 % elsewhere (1x4104), float32
+// up to 8.7 % (1x5120).
+struct WideShape {
+  int nc, w, p;  // chunk slots per lane, waves per block, blocks per wave
+};
+constexpr WideShape wide_shape(int dtype, int64_t blk_c) {
+  const int64_t g = (blk_c + 7) / 8;
+  int c = 1;
+  while (64 * c < g) c *= 2;
+  if (c > 16 || g == 64 * 8 || (dtype != kF32 && g > 64 * 12)) return {kWideChunks, c > 8 ? 4 : 1, 1};
+  return {4, c > 4 ? c / 4 : 1, c < 4 ? 4 / c : 1};
 }
 constexpr int kTileThreads = 512;    // k_tile128: threads per 128x128 tile (512 beat 256 and 1024)
 constexpr int kRowBlocks = 4;        // k_row: wave instructions per lane, one 1xB block each up to B = 512, sharing

@@ -104,12 +104,12 @@ QWEN3_8B_LAYER = [(1, 4096, 4096), (1, 1024, 4096), (1, 1024, 4096), (1, 4096, 4
                   (1, 12288, 4096), (1, 12288, 4096), (1, 4096, 12288)]
 
 
-def _pack(fmt, shapes, blk=(128, 128), flags=0):
+def _pack(fmt, shapes, blk=(128, 128), flags=0, dtype=0):
     ts = _tensors(shapes)
-    need = L().lrq_group_table_bytes(fmt, ts, len(shapes), 0, blk[0], blk[1], flags)
+    need = L().lrq_group_table_bytes(fmt, ts, len(shapes), dtype, blk[0], blk[1], flags)
     assert need > 0, _lib.last_error()
     buf = np.zeros(need, np.uint8)
-    rc = L().lrq_group_pack(fmt, ts, len(shapes), 0, blk[0], blk[1], flags, buf.ctypes.data, need)
+    rc = L().lrq_group_pack(fmt, ts, len(shapes), dtype, blk[0], blk[1], flags, buf.ctypes.data, need)
     assert rc == 0, _lib.last_error()
     return buf
 
@@ -151,12 +151,17 @@ def test_group_pack_rows_and_mx_units():
         buf = _pack(_lib.FMT_FP8_BLOCK, shapes, (1, B))
         per_wg = 4 * 4 * (64 // lanes)
         assert L().lrq_group_units(buf.ctypes.data) == -(-256 * 16 // per_wg) + -(-63 * 3 // per_wg), B
-    # wider blocks: 4 waves of 4, 2 or 1 blocks (B <= 1024, 2048, 4096), or one
-    # block of 4 waves (B <= 16384); 1024 and 2048 stay on the row kernel
-    for B, per_wg in ((640, 16), (1032, 8), (1536, 8), (3072, 4), (4096, 4), (4104, 1), (16384, 1),
-                      (1024, 16 // 2), (2048, 16 // 4), (1000, 16), (3001, 4), (9999, 1)):
-        buf = _pack(_lib.FMT_FP8_BLOCK, [(1, 256, 16 * B), (1, 72, 3 * B)], (1, B))
-        assert L().lrq_group_units(buf.ctypes.data) == -(-256 * 16 // per_wg) + -(-72 * 3 // per_wg), B
+    # wider blocks: 4 waves of 2 or 1 blocks (B <= 1024, 2048), blocks of 2
+    # waves (B <= 4096) or 4 (B <= 16384), with 4 chunk slots per lane; with 8
+    # slots, one wave per block at B = 4096 and 4 waves per block past 6144
+    # (16-bit) or 8192; 1024 and 2048 stay on the row kernel
+    for dt, cases in ((0, ((640, 8), (1032, 4), (1536, 4), (3072, 2), (4096, 4), (4104, 1), (6144, 1),
+                           (8192, 1), (16384, 1), (1000, 8), (3001, 2), (9999, 1))),
+                      (_lib.DTYPE_F32, ((640, 8), (1000, 8), (1536, 4), (3072, 2), (4096, 4),
+                                        (4104, 1), (8192, 1), (8200, 1)))):
+        for B, per_wg in cases:
+            buf = _pack(_lib.FMT_FP8_BLOCK, [(1, 256, 16 * B), (1, 72, 3 * B)], (1, B), dtype=dt)
+            assert L().lrq_group_units(buf.ctypes.data) == -(-256 * 16 // per_wg) + -(-72 * 3 // per_wg), B
     # widths under 8 and past 16384 take the generic kernel: one work-group per block
     for B in (5, 7, 16392):
         buf = _pack(_lib.FMT_FP8_BLOCK, [(1, 4, 2 * B)], (1, B))

@@ -30,7 +30,8 @@ if not torch.cuda.is_available():  # pragma: no cover - CPU container
 DEV = torch.device("cuda", 0)
 DT = {"bf16": torch.bfloat16, "f16": torch.float16, "f32": torch.float32}
 WIDTHS = [40, 48, 96, 120, 200, 248, 504, 8, 16, 24, 36, 1024, 2048, 1536,
-          640, 1032, 4096, 4104, 12288, 16384, 16392, 12, 100, 500, 1000, 3001, 9999, 5, 7]
+          640, 1032, 4096, 4104, 12288, 16384, 16392, 12, 100, 500, 1000, 3001, 9999, 5, 7,
+          3072, 4090, 6144, 7000, 8192]
 # (rows, blocks per row, row pitch padding, pow2, bf16 scales when arith is f32)
 CASES = [(1, 1, 0, False, False), (37, 3, 0, True, False), (200, 5, 16, False, True),
          (513, 2, 0, False, False), (64, 11, 8, True, False)]
@@ -77,7 +78,7 @@ def test_width_vs_oracle(B, dt, arith):
         assert np.array_equal(got.reshape(-1), want.reshape(-1)), (B, rows, cols, ld)
 
 
-@pytest.mark.parametrize("B", [96, 40, 200, 8, 1536, 4104, 36, 1000])
+@pytest.mark.parametrize("B", [96, 40, 200, 8, 1536, 4104, 36, 1000, 3001, 7000])
 def test_grouped_plan_and_expert_stacks(B):
     print("rowg grouped", B, flush=True)
     rng = np.random.default_rng(B)

@@ -51,8 +51,18 @@ def model_units(dt, batch, rows, cols, ld, bstride, blk_r, blk_c, in_off, codes_
             lanes *= 2
         return cdiv(nblocks, 4 * ROW_BLOCKS * (64 // lanes))
     if 512 < blk_c <= 16384 and vec_row:
-        p = 4 if blk_c <= 1024 else 2 if blk_c <= 2048 else 1 if blk_c <= 4096 else 0
-        return cdiv(nblocks, 4 * p if p else 1)
+        # the fewest 64-lane steps (a power of two) of 8-element chunk slots that
+        # hold a block, as 4 or 8 slots per lane
+        chunks = cdiv(blk_c, 8)
+        steps = 2
+        while steps * 64 < chunks:
+            steps *= 2
+        eight = steps > 16 or chunks == 512 or (dt != _lib.DTYPE_F32 and chunks > 768)
+        if eight:
+            return cdiv(nblocks, 4 if steps == 8 else 1)  # 4 one-wave blocks, or one 4-wave block
+        if steps <= 4:
+            return cdiv(nblocks, 4 * (4 // steps))  # 4 waves of 4/steps blocks
+        return cdiv(nblocks, 4 // (steps // 4))  # blocks of 2 or 4 waves
     return generic
 
 
@@ -70,7 +80,7 @@ def library_units(dt, batch, rows, cols, ld, bstride, blk_r, blk_c, in_off, code
 
 
 WIDTHS = [5, 8, 12, 16, 24, 32, 36, 40, 64, 96, 100, 128, 256, 500, 512, 640, 1000, 1024, 1536,
-          2048, 3001, 4096, 4104, 9999, 16384, 16392]
+          2048, 2056, 3001, 4090, 4096, 4104, 6144, 6152, 8192, 8200, 9999, 16384, 16392]
 
 
 @settings(max_examples=400, deadline=None)
@@ -99,4 +109,12 @@ def test_model_spot_checks():
     assert model_units(bf, 1, 256, 3600, 3600, 256 * 3600, 1, 36, 2, 0) == cdiv(256 * 100, 128)
     assert model_units(bf, 1, 4, 4096, 4096, 4 * 4096, 1, 4096, 0, 0) == 1
     assert model_units(bf, 1, 4, 10, 10, 40, 1, 5, 0, 0) == 8
+    f32 = _lib.DTYPE_F32
+    assert model_units(f32, 1, 64, 3840, 3840, 64 * 3840, 1, 640, 0, 0) == 64 * 6 // 8
+    assert model_units(bf, 1, 64, 3840, 3840, 64 * 3840, 1, 640, 0, 0) == 64 * 6 // 8
+    assert model_units(bf, 1, 8, 6144, 6144, 8 * 6144, 1, 3072, 0, 0) == 8  # 2 waves per block
+    assert model_units(f32, 1, 4, 8192, 8192, 4 * 8192, 1, 4096, 0, 0) == 2  # one wave per block
+    assert model_units(bf, 1, 4, 8192, 8192, 4 * 8192, 1, 4096, 0, 0) == 2
+    assert model_units(bf, 1, 4, 12000, 12000, 4 * 12000, 1, 6000, 0, 0) == 8  # 4 waves per block
+    assert model_units(bf, 1, 4, 7000, 7000, 4 * 7000, 1, 7000, 0, 0) == 4
     assert library_units(bf, 1, 4096, 4096, 4096, 4096 * 4096, 128, 128, 0, 0) == 1024
