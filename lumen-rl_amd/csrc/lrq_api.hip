@@ -186,12 +186,14 @@ bool plan_units(const LaunchCfg& cfg, Desc& d) {
       d.units = (d.batch * d.rows * d.cols + per_wg - 1) / per_wg;
       return true;
     }
-    case kKernF64Wide: {  // 4 waves of P blocks each (B <= 1024), or one block of 4 waves
+    case kKernF64Wide: {  // 4 waves of 64/L blocks per instruction (B < 128), of P blocks
+                          // each (B <= 1024), or one block of 4 waves
       if (!fold_batch(d)) return false;
       d.bpr = d.cols / cfg.blk_c;
       d.nblocks = d.rows * d.bpr;
+      const int L = f64_pad_lanes(cfg.blk_c);
       const int P = f64_wide_blocks_per_wave(cfg.blk_c);
-      const int64_t per_wg = P > 0 ? 4 * P : 1;
+      const int64_t per_wg = L > 0 ? 4 * kF64RowInstr * (64 / L) : P > 0 ? 4 * P : 1;
       d.units = (d.nblocks + per_wg - 1) / per_wg;
       return true;
     }

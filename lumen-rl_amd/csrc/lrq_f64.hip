@@ -492,6 +492,76 @@ __global__ __launch_bounds__(256) void k_row_wide_f64(Desc single, const Desc* _
   }
 }
 
+// 1xB blocks of a float64 tensor, 5 <= B < 128 (other than 32 and 64, which
+// k_row_f64 takes): a block's g = ceil(B/2) chunks of 2 doubles sit on an
+// aligned group of L = nextpow2(g) lanes (the last chunk starting at B - 2 when
+// B is odd), so a wave instruction holds 64/L blocks and a lane runs
+// kF64RowInstr instructions, each on the next 64/L blocks.  Lanes past g
+// re-load their block's first chunk and drop out of the amax, so the loads
+// issue without branches.  split_max leaves each lane the maximum of one of
+// its group's blocks; the group's other lanes fetch that scale by shuffle.
+// Quotients as in k_row_f64.
+template <int L>
+__global__ __launch_bounds__(256) void k_row_pad_f64(Desc single, const Desc* __restrict__ descs,
+                                                     const uint32_t* __restrict__ map, int pow2, int bw) {
+  constexpr int NI = kF64RowInstr;  // instructions per lane
+  constexpr int BPI = 64 / L;       // blocks per wave instruction
+  constexpr int Q = L / NI;         // lanes holding one block's scale
+  static_assert(L >= NI && L <= 64, "a lane group holds one scale per instruction");
+  Desc d;
+  int64_t u;
+  pick_desc<kXcdRunRow>(single, descs, map, d, u);
+  const int lane = threadIdx.x & 63;
+  const int g = (bw + 1) / 2;  // chunks per block
+  const int c = lane % L;      // this lane's chunk of its block
+  const int off = c < g ? (2 * c > bw - 2 ? bw - 2 : 2 * c) : 0;
+  const int64_t b0 = (u * 4 + (threadIdx.x >> 6)) * (NI * BPI) + lane / L;  // block, instruction 0
+  const double* in = static_cast<const double*>(d.in);
+  v4u raw[NI];
+  bool ok[NI];
+  int64_t blk[NI];
+#pragma unroll
+  for (int i = 0; i < NI; ++i) {
+    const int64_t b = b0 + i * BPI;
+    ok[i] = c < g && b < d.nblocks;
+    blk[i] = b < d.nblocks ? b : d.nblocks - 1;
+    int64_t base;
+    if (d.ld == d.cols) {
+      base = blk[i] * bw;
+    } else {
+      const int64_t row = blk[i] / d.bpr;
+      base = row * d.ld + (blk[i] - row * d.bpr) * bw;
+    }
+    raw[i] = load_nt(in + base + off);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  uint64_t p[NI];
+#pragma unroll
+  for (int i = 0; i < NI; ++i) {
+    const uint64_t m = umax64((((uint64_t)raw[i].y << 32) | raw[i].x) & kAbs64,
+                              (((uint64_t)raw[i].w << 32) | raw[i].z) & kAbs64);
+    p[i] = ok[i] ? m : 0;
+  }
+  double s;
+  int kind;
+  block_scale_f64(split_max<NI, L>(p, lane), pow2 != 0, s, kind);  // block of instruction c / Q
+  const double y = 1.0 / s;  // correctly rounded
+  const int64_t mine = b0 + (c / Q) * BPI;
+  if (c % Q == 0 && mine < d.nblocks) gst<double>(static_cast<double*>(d.scales) + mine, s);
+#pragma unroll
+  for (int i = 0; i < NI; ++i) {
+    const int src = (lane / L) * L + i * Q;
+    const double si = shfl_f64(s, src), yi = shfl_f64(y, src);
+    const int ki = __shfl(kind, src, 64);
+    if (ok[i]) {
+      const uint64_t x0 = ((uint64_t)raw[i].y << 32) | raw[i].x;
+      const uint64_t x1 = ((uint64_t)raw[i].w << 32) | raw[i].z;
+      store_nt2(d.codes + blk[i] * bw + off, (uint16_t)code2_f64(x0, x1, si, yi, ki, fast_block(si, ki)));
+    }
+    __builtin_amdgcn_sched_barrier(0);
+  }
+}
+
 hipError_t launch_f64(const LaunchCfg& cfg, const Desc& single, const Desc* descs,
                       const uint32_t* map, int64_t units, hipStream_t stream) {
   const dim3 grid((unsigned)units), block(256);
@@ -523,6 +593,14 @@ hipError_t launch_f64(const LaunchCfg& cfg, const Desc& single, const Desc* desc
   }
   if (cfg.kernel == kKernF64Wide) {
     const int bw = cfg.blk_c;
+    switch (f64_pad_lanes(cfg.blk_c)) {
+      case 4: hipLaunchKernelGGL((k_row_pad_f64<4>), grid, block, 0, stream, single, descs, map, cfg.pow2, bw); return hipGetLastError();
+      case 8: hipLaunchKernelGGL((k_row_pad_f64<8>), grid, block, 0, stream, single, descs, map, cfg.pow2, bw); return hipGetLastError();
+      case 16: hipLaunchKernelGGL((k_row_pad_f64<16>), grid, block, 0, stream, single, descs, map, cfg.pow2, bw); return hipGetLastError();
+      case 32: hipLaunchKernelGGL((k_row_pad_f64<32>), grid, block, 0, stream, single, descs, map, cfg.pow2, bw); return hipGetLastError();
+      case 64: hipLaunchKernelGGL((k_row_pad_f64<64>), grid, block, 0, stream, single, descs, map, cfg.pow2, bw); return hipGetLastError();
+      default: break;
+    }
     switch (f64_wide_blocks_per_wave(cfg.blk_c)) {
       case 4: hipLaunchKernelGGL((k_row_wide_f64<1, 4>), grid, block, 0, stream, single, descs, map, cfg.pow2, bw); break;
       case 2: hipLaunchKernelGGL((k_row_wide_f64<1, 2>), grid, block, 0, stream, single, descs, map, cfg.pow2, bw); break;

@@ -41,7 +41,8 @@ enum Kernel : int {
   kKernF64Row = 12,        // 1xB float64 blocks (B = 32..2048, powers of two), 16-byte loads
   kKernF64Tile = 13,       // 128x128 float64 tiles, one 512-thread work-group per tile
   kKernRowWide = 16,       // 1xB FP8 blocks, 512 < B <= 16384 but 1024/2048: k_row_wide
-  kKernF64Wide = 17,       // 1xB float64 blocks k_row_f64 does not take, 2 <= B <= 4096: k_row_wide_f64
+  kKernF64Wide = 17,       // 1xB float64 blocks k_row_f64 does not take, 2 <= B <= 4096:
+                           // k_row_pad_f64 (5 <= B < 128), else k_row_wide_f64
   kKernRowF32 = 15,        // 1xB FP8 blocks of float32 input (B = 8..1024, a power of two), one 16-byte load per lane chunk
   kKernRowG = 14,          // 1xB FP8 blocks, B = 8..512 but 32..512 powers of two: k_row with
                            // 1- or 2-lane groups (1x8, 1x16), else g = ceil(B/8) lanes of each
@@ -94,6 +95,15 @@ constexpr int f64_row_instr(int64_t blk_c) { return blk_c > 128 * kF64RowInstr ?
 // 0 when it takes four waves (B > 1024).
 constexpr int f64_wide_blocks_per_wave(int64_t blk_c) {
   return blk_c <= 256 ? 4 : blk_c <= 512 ? 2 : blk_c <= 1024 ? 1 : 0;
+}
+// Narrower float64 blocks (5 <= B < 128) take k_row_pad_f64 instead: the
+// lanes of a block's aligned group, L = nextpow2(ceil(B/2)) (4..64), or 0 for
+// widths outside that range.
+constexpr int f64_pad_lanes(int64_t blk_c) {
+  if (blk_c < 5 || blk_c >= 128) return 0;
+  int l = 4;
+  while (2 * l < blk_c) l *= 2;
+  return l;
 }
 
 // Descriptor and local work unit of this work-group: the single-tensor

@@ -428,9 +428,10 @@ def test_float64_input_needs_float64_arithmetic_and_the_fp8_block_format():
     # tables pack (host memory only) with each float64 kernel's geometry: a dense
     # 1x128 tensor, dense or with a padded row pitch, takes the row kernel (4
     # waves x 4 instructions of 128 doubles of the element sequence per
-    # work-group); a 1x96 block the wide-row kernel (4 blocks per wave, 16 per
-    # work-group); a 2-D block the generic kernel (one wave per block, four per
-    # work-group)
+    # work-group); blocks narrower than 128 the padded-group kernel (64/L blocks
+    # per wave instruction for L = nextpow2(ceil(B/2)) lanes, 4 instructions, 4
+    # waves); wider ones the wide-row kernel; a 2-D block the generic kernel
+    # (one wave per block, four per work-group)
     def units(rows, cols, ld, blk=128, blk_r=1):
         t = (_lib.LrqTensor * 1)()
         t[0].in_, t[0].codes, t[0].scales = 0x10000, 0x20000, 0x30000
@@ -445,7 +446,10 @@ def test_float64_input_needs_float64_arithmetic_and_the_fp8_block_format():
     assert units(5, 256, 256) == 1
     assert units(40, 256, 256) == 5
     assert units(40, 256, 384) == 5
-    assert units(5, 288, 288, 96) == -(-5 * 3 // 16)   # wide rows: 4 waves x 4 blocks
+    assert units(5, 288, 288, 96) == -(-5 * 3 // 16)   # L = 64: one block per instruction
+    assert units(5, 450, 450, 45) == -(-5 * 10 // 32)  # L = 32: two
+    assert units(64, 80, 80, 5) == 64 * 16 // 256      # L = 4: sixteen
+    assert units(7, 112, 120, 16) == -(-7 * 7 // 128)  # L = 8, padded row pitch
     assert units(50, 768, 800, 384) == -(-50 * 2 // 8)  # 2 blocks per wave
     assert units(9, 3000, 3000, 3000) == 9              # one block of 4 waves
     assert units(5, 288, 288, 96, 2) == (3 * 3 + 3) // 4  # 2-D blocks: generic

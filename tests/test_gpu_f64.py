@@ -68,6 +68,7 @@ def check(xd: torch.Tensor, blk, pow2):
 @pytest.mark.parametrize("pow2", [False, True])
 @pytest.mark.parametrize("blk", [(1, 128), (1, 32), (1, 64), (1, 256), (1, 512), (1, 1024), (1, 2048), (1, 96),
                                  (1, 384), (1, 2), (1, 3), (1, 45), (1, 100), (1, 1000), (1, 3000), (1, 4096),
+                                 (1, 5), (1, 7), (1, 8), (1, 16), (1, 33), (1, 65), (1, 127),
                                  (128, 128), (3, 40), (64, 96)])
 @pytest.mark.parametrize("data", ["weights", "edge"])
 def test_f64_blocks_vs_oracle(data, blk, pow2):
@@ -193,13 +194,14 @@ def _division_regimes(n_blocks: int, rng) -> dict:
 
 
 @pytest.mark.parametrize("pow2,blk", [(False, 128), (True, 128), (False, 32), (False, 64),
-                                      (False, 256), (False, 512)])
+                                      (False, 256), (False, 512), (False, 8), (True, 16)])
 def test_f64_row_kernel_division_sweep_vs_oracle(pow2, blk):
     """The 1xB float64 kernel (Markstein's correction in blocks with s >= 2^-900,
     the IEEE division below) against the oracle's IEEE division, bit for bit, on
     4 x 64 K rows of adversarial quotients.  The same rows read as 1x32, 1x64,
     1x256 and 1x512 blocks take the layouts whose scales reach each lane from
-    other lanes (shuffles within a block's lanes, or readlane)."""
+    other lanes (shuffles within a block's lanes, or readlane); 1x8 and 1x16
+    blocks take the padded-group kernel (4 and 8 lanes per block)."""
     rng = np.random.default_rng(1717 + int(pow2))
     for name, x in _division_regimes(1 << 16, rng).items():
         say("f64 division sweep", name, pow2, blk)
