@@ -8,8 +8,8 @@
 //                   kAmaxLoads (two) 16-byte nontemporal loads per lane, all
 //                   issued before the reduction, and writes the unit's max |x| bit pattern to
 //                   workspace[global unit];
-//   k_tensor_scale  one work-group per tensor reduces its units' partials and
-//                   writes the float32 scale.
+//   k_tensor_scale  one 1024-thread work-group per tensor reduces its units'
+//                   partials (16-byte loads) and writes the float32 scale.
 // No atomics and no zero-initialised memory: every partial is written before
 // it is read, and the result does not depend on scheduling.
 #include <string.h>
@@ -165,18 +165,49 @@ __global__ __launch_bounds__(256) void k_amax(Desc single, const Desc* __restric
   if (threadIdx.x == 0) partial[d.unit0 + u] = m;
 }
 
-// One work-group per tensor: max over the tensor's partials, then the scale.
-__global__ __launch_bounds__(256) void k_tensor_scale(const Desc* __restrict__ descs,
-                                                      const uint32_t* __restrict__ partial) {
-  __shared__ uint32_t lds[4];
+// One 1024-thread work-group per tensor: max over the tensor's partials, then
+// the scale.  The partials between the first and last 16-byte boundary of the
+// tensor's slice are read 4 at a time, kScaleLoads loads in flight per thread
+// (a 2 GiB tensor has 262144 partials: 8 rounds instead of 1024 with one
+// 4-byte load per thread and round); the at most 3 before and 3 after are read
+// singly.
+constexpr int kScaleThreads = 1024;
+constexpr int kScaleLoads = 8;
+__global__ __launch_bounds__(kScaleThreads) void k_tensor_scale(const Desc* __restrict__ descs,
+                                                                const uint32_t* __restrict__ partial) {
+  __shared__ uint32_t lds[kScaleThreads / 64];
   const Desc d = descs[blockIdx.x];
-  uint32_t a = 0u;
-  for (int64_t i = threadIdx.x; i < d.units; i += 256) {
-    const uint32_t t = partial[d.unit0 + i];
-    a = t > a ? t : a;
+  const uint32_t* p = partial + d.unit0;
+  const int64_t n = d.units;
+  const int tid = threadIdx.x;
+  int64_t head = (int64_t)((16u - ((uintptr_t)p & 15u)) & 15u) / 4;  // partials before a 16-byte boundary
+  head = head < n ? head : n;
+  uint32_t a = tid < head ? p[tid] : 0u;
+  const v4u* q = reinterpret_cast<const v4u*>(p + head);
+  const int64_t nv = (n - head) / 4;  // 16-byte groups
+  for (int64_t i = tid; i < nv; i += (int64_t)kScaleThreads * kScaleLoads) {
+    v4u v[kScaleLoads];
+#pragma unroll
+    for (int k = 0; k < kScaleLoads; ++k) {
+      const int64_t j = i + (int64_t)kScaleThreads * k;
+      v[k] = j < nv ? q[j] : v4u{0u, 0u, 0u, 0u};
+    }
+#pragma unroll
+    for (int k = 0; k < kScaleLoads; ++k) {
+      const uint32_t m01 = v[k].x > v[k].y ? v[k].x : v[k].y, m23 = v[k].z > v[k].w ? v[k].z : v[k].w;
+      const uint32_t m = m01 > m23 ? m01 : m23;
+      a = m > a ? m : a;
+    }
   }
-  a = block_reduce_max(a, lds);
-  if (threadIdx.x == 0) {
+  const int64_t t0 = head + 4 * nv;  // the last n - t0 (< 4) partials
+  if (tid < n - t0) a = p[t0 + tid] > a ? p[t0 + tid] : a;
+  a = wave_max(a);
+  if ((tid & 63) == 0) lds[tid >> 6] = a;
+  __syncthreads();
+  a = lds[0];
+#pragma unroll
+  for (int w = 1; w < kScaleThreads / 64; ++w) a = lds[w] > a ? lds[w] : a;
+  if (tid == 0) {
     float s;
     if (a > 0x7F800000u) {
       s = u2f(0x7FC00000u);
@@ -202,7 +233,7 @@ hipError_t launch_tensor_scale(const LaunchCfg& cfg, const Desc* descs, const ui
   }
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL(k_tensor_scale, dim3((unsigned)n), dim3(256), 0, stream, descs, partial);
+  hipLaunchKernelGGL(k_tensor_scale, dim3((unsigned)n), dim3(kScaleThreads), 0, stream, descs, partial);
   return hipGetLastError();
 }
 

@@ -88,6 +88,28 @@ def test_tensor_scales_strided_and_batched_vs_reference():
         assert bits(got[i]) == bits(T.kv_scale(w.cpu())), i
 
 
+@pytest.mark.parametrize("lead", [1, 2, 3, 4])
+def test_tensor_scale_many_partials_any_slice_offset(lead):
+    """A [70001, 4096] bf16 weight (one 8 KiB amax unit per row, so 70001
+    partials: several rounds of the finishing kernel's 16-byte loads) after
+    `lead` one-unit tensors, so its partials start at every 4-byte offset of a
+    16-byte line.  The maximum sits in the first unit (read singly before the
+    first boundary), a middle one, and the last (read singly after the last),
+    then a NaN in the last unit."""
+    say("tensor scale many partials", lead)
+    rows = 70001
+    big = torch.full((rows, 4096), 0.01, dtype=torch.bfloat16, device=DEV)
+    ws = [weight((1, 64), "bf16") for _ in range(lead)] + [big]
+    plan = TensorScalePlan(ws)
+    for row, v in ((0, 3.5), (rows // 2, -2.25), (rows - 1, 1.75), (rows - 1, float("nan"))):
+        big.fill_(0.01)
+        big[row, 4095] = v
+        want = oracle_scale(torch.tensor([[v, 0.01]], dtype=torch.bfloat16), "bf16")  # the same max |x|
+        assert bits(plan.run()[lead]) == want, (lead, row, v)
+        for i in range(lead):
+            assert bits(plan.run()[i]) == oracle_scale(ws[i], "bf16"), (lead, i)
+
+
 def test_tensor_scale_errors():
     with pytest.raises(RuntimeError):
         TensorScalePlan([torch.empty(0, 128, device=DEV, dtype=torch.bfloat16)])
