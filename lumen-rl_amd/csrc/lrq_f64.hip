@@ -7,13 +7,15 @@
 // rounded to float32 (:68) before the e4m3 cast (:71): a double rounding
 // (f64 -> f32 -> e4m3) that this kernel keeps.  Scales are written as float64.
 //
-// k_row_f64 takes 1xB blocks (B = 32...512, the reference's layout) and
-// k_tile_f64 128x128 tiles, both with 16-byte loads.  Their quotients of finite
-// blocks use one correctly rounded 1/s per block and Markstein's correction per
-// element (the IEEE division in blocks with tiny scales) and the hardware e4m3
-// encoder.  k_f64 takes every other shape, one wave per block (any block
-// shape), four blocks per 256-thread work-group, re-reading the block from L2
-// for the encode, with the IEEE float64 division and the software encoder.
+// k_row_f64 takes 1xB blocks (B = 32...2048, powers of two, the reference's
+// layout), k_row_pad_f64 narrower widths (5 <= B < 128) on padded lane groups,
+// k_row_wide_f64 the other 1xB widths up to 4096, and k_tile_f64 128x128 tiles,
+// all with 16-byte loads.  Their quotients of finite blocks use one correctly
+// rounded 1/s per block and Markstein's correction per element (the IEEE
+// division in blocks with tiny scales) and the hardware e4m3 encoder.  k_f64
+// takes every other shape, one wave per block (any block shape), four blocks
+// per 256-thread work-group, re-reading the block from L2 for the encode, with
+// the IEEE float64 division and the software encoder.
 #include "lrq_device.hpp"
 #include "lrq_internal.hpp"
 
@@ -394,8 +396,9 @@ __global__ __launch_bounds__(512) void k_tile_f64(Desc single, const Desc* __res
   else tile_f64<false>(d, u, b, r0, col, pow2, red);
 }
 
-// 1xB blocks of a float64 tensor for the widths k_row_f64 does not take (B not
-// a power of two, or 4096; 2 <= B <= 4096): ceil(B/2) chunks of 2 doubles (16
+// 1xB blocks of a float64 tensor for the widths neither k_row_f64 nor
+// k_row_pad_f64 takes (128 < B <= 4096 not a power of two, B = 4096, and
+// B = 2..4): ceil(B/2) chunks of 2 doubles (16
 // bytes), the last starting at B - 2 when B is odd (it overlaps its
 // neighbour: the amax ignores the repeat, and both lanes write the same
 // codes).  As k_row_wide: W waves per block (1 up to B = 1024, else 4), lane l

@@ -3,15 +3,17 @@
 // Restates WeightQuantizer.quantize_tensor
 // (lumenrl/quantization/weight_quantizer.py:40-77): per block amax -> /448 ->
 // clamp(tiny) -> [pow2] -> x/s -> float8_e4m3fn, in one HBM pass (bf16 in,
-// e4m3 + scale out).  Four kernels:
+// e4m3 + scale out).  Five kernels:
 //   k_tile128  : 128x128 tiles (the vLLM/ATOM `weight_scale_inv` layout), one
 //                512-thread work-group per tile, the tile held in VGPRs;
 //                tiles handed to XCDs in runs of kXcdRunTile (xcd_unit).
-//   k_row      : 1xB row blocks (the reference's own layout), B/8 consecutive
-//                lanes per block so every wave instruction is one contiguous
-//                span; one scale computation per lane, shared by shuffles.
-//   k_row_wide : 1xB row blocks wider than 512 (but 1024 and 2048), one or
-//                four waves per block, the block held in VGPRs.
+//   k_row      : 1xB row blocks (the reference's own layout), ceil(B/8)
+//                consecutive lanes per block (padded to a power of two) so
+//                every wave instruction is one contiguous span; one scale
+//                computation per lane, shared by shuffles.
+//   k_row_f32  : the same for float32 input, one 16-byte load per 4 elements.
+//   k_row_wide : 1xB row blocks wider than 512 (but 1024 and 2048), one, two
+//                or four waves per block, the block held in VGPRs.
 //   k_generic  : any block shape, stride or alignment (one work-group per
 //                block, scalar loads); the fallback for odd inputs.
 // All of them share lrq_device.hpp's block_scale / block_quot / special_code.
