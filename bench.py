@@ -819,6 +819,8 @@ def run_ceiling(args):
                         4 or 8 of them per lane
       fill:             write-only, 2 bytes per element (k_dequant's store side)
       widen:            k_dequant's 1:2 bytes, 8 read and 16 written per lane chunk
+      widen 2:4:        the same kernel over the activation fake-quant's bytes (2 read
+                        and 4 written per element), beside k_act_qdq8
       read:             read-only (k_amax's load side)
 
     each the best over a few LDS reservations that cap the work-groups per CU
@@ -827,7 +829,8 @@ def run_ceiling(args):
     same weight:
     128x128 quantization (k_tile128, 512 threads), 1x128 quantization (k_row),
     1x128 dequantization to bf16 (k_dequant: 1 byte read + 2 written per
-    element) and the per-tensor scale (k_amax and its 4-byte finishing launch).
+    element), the activation fake-quant (k_act_qdq8: bf16 in, float32 out) and
+    the per-tensor scale (k_amax and its 4-byte finishing launch).
     GB/s = bytes moved / median launch time (HIP events on the launch stream,
     `--steps` launches after `--warmup`).  Prints one JSON line per width.
     """
@@ -928,6 +931,14 @@ def run_ceiling(args):
         line("fill", 2 * n, fill)
         line("widen", 3 * n, widen, "k_dequant (1x128 -> bf16)", 3 * n + 2 * (n // 128), d_ms)
         del dplan, codes, scales
+        # the activation fake-quant's bytes: 2 in, 4 out per element (one 16-byte
+        # load of 8 bf16, two 16-byte stores of 8 float32 per lane chunk)
+        out32 = torch.empty(n, dtype=torch.float32, device=dev)
+        widen2 = best_ms(lambda lds: ck(C.lrqc_widen(x.data_ptr(), out32.data_ptr(), n // 4, lds, sp), "widen"),
+                         caps)
+        act_ms = median_ms(lambda: ops.act_qdq(x, 128, out=out32.view(R, K)))
+        line("widen 2:4", 6 * n, widen2, "k_act_qdq8 (1x128, bf16 -> float32)", 6 * n, act_ms)
+        del out32
         rd = best_ms(lambda lds: ck(C.lrqc_read(x.data_ptr(), 2 * n, parts.data_ptr(), lds, sp), "read"), caps)
         tplan = ops.TensorScalePlan([x])
         a_ms = median_ms(tplan.run)
