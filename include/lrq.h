@@ -99,7 +99,7 @@ typedef struct ihipStream_t* lrq_stream_t; /* == hipStream_t */
  *             for LRQ_DTYPE_F64), or bf16 with LRQ_FLAG_SCALE_BF16.  Edge blocks
  *             may be partial.
  * in needs element alignment only (any ld): with codes aligned to 8 bytes and
- * cols % 8 == 0, 128x128 tiles and 1xB blocks of B = 8g <= 16384 run on the
+ * cols % 8 == 0, 128x128 tiles and 1xB blocks of 8 <= B <= 65536 run on the
  * vector kernels; other shapes and alignments on the generic kernel.
  * Bit-exact with the reference evaluated by torch on x86, including NaN, inf,
  * all-zero and subnormal blocks.

@@ -143,8 +143,8 @@ int fp8_kernel_for(const Desc& d, int in_dtype, int64_t blk_r, int64_t blk_c) {
   // of ceil(B/8) chunks beyond
   if (blk_r == 1 && blk_c >= 8 && blk_c <= 512 && d.cols % blk_c == 0 && vec_row)
     return lrq::kKernRowG;
-  // wider blocks: one wave per block up to 4096, four up to 16384
-  if (blk_r == 1 && blk_c > 512 && blk_c <= 4 * 512 * lrq::kWideChunks && d.cols % blk_c == 0 && vec_row)
+  // wider blocks: one wave per block up to 4096, up to 16 waves up to 65536
+  if (blk_r == 1 && blk_c > 512 && blk_c <= lrq::kWideMax && d.cols % blk_c == 0 && vec_row)
     return lrq::kKernRowWide;
   return lrq::kKernGenericFp8;
 }
@@ -222,12 +222,12 @@ bool plan_units(const LaunchCfg& cfg, Desc& d) {
       d.units = (d.nblocks + per_wg - 1) / per_wg;
       return true;
     }
-    case kKernRowWide: {  // 4 waves of P blocks each, or 2 or 1 blocks of 2 or 4 waves
+    case kKernRowWide: {  // 4 waves of P blocks each, 2 blocks of 2 waves, or one block of 4-16 waves
       if (!fold_batch(d)) return false;
       d.bpr = d.cols / cfg.blk_c;
       d.nblocks = d.rows * d.bpr;
       const WideShape ws = wide_shape(cfg.in_dtype, cfg.blk_c);
-      const int64_t per_wg = 4 / ws.w * ws.p;
+      const int64_t per_wg = ws.w >= 4 ? 1 : 4 / ws.w * ws.p;
       d.units = (d.nblocks + per_wg - 1) / per_wg;
       return true;
     }

@@ -12,8 +12,8 @@
 //                every wave instruction is one contiguous span; one scale
 //                computation per lane, shared by shuffles.
 //   k_row_f32  : the same for float32 input, one 16-byte load per 4 elements.
-//   k_row_wide : 1xB row blocks wider than 512 (but 1024 and 2048), one, two
-//                or four waves per block, the block held in VGPRs.
+//   k_row_wide : 1xB row blocks wider than 512 (but 1024 and 2048) up to
+//                65536, 1 to 16 waves per block, the block held in VGPRs.
 //   k_generic  : any block shape, stride or alignment (one work-group per
 //                block, scalar loads); the fallback for odd inputs.
 // All of them share lrq_device.hpp's block_scale / block_quot / special_code.
@@ -390,9 +390,10 @@ __global__ __launch_bounds__(256) void k_row_f32(Desc single, const Desc* __rest
 }
 
 // ---------------------------------------------------------------------------
-// Wide 1xB row blocks, 512 < B <= 16384 (other than 1024 and 2048, which
+// Wide 1xB row blocks, 512 < B <= 65536 (other than 1024 and 2048, which
 // k_row takes), in g = ceil(B/8) chunks: a block belongs to W waves of the
-// work-group (W = 1, 2 or 4), whose lane l of wave w holds chunks
+// work-group (W = 1, 2 or 4 of a 256-thread work-group; 8 or 16 waves, the
+// whole work-group, past B = 16384), whose lane l of wave w holds chunks
 // c = 64 w + l + 64 W k for k < K = ceil(g / 64W).  When 8 does not divide B
 // the last chunk starts at B - 8, overlapping its neighbour (the amax ignores
 // the repeat; both lanes write the same codes).  A lane has NC chunk slots
@@ -406,19 +407,20 @@ __global__ __launch_bounds__(256) void k_row_f32(Desc single, const Desc* __rest
 // the scale math then runs once per block.
 // ---------------------------------------------------------------------------
 template <int DT, int CDT, int W, int P, int NC>
-__global__ __launch_bounds__(256) void k_row_wide(Desc single, const Desc* __restrict__ descs,
-                                                  const uint32_t* __restrict__ map, int pow2,
-                                                  int scale_bf16, int bw) {
+__global__ __launch_bounds__(W > 4 ? 64 * W : 256) void k_row_wide(Desc single, const Desc* __restrict__ descs,
+                                                                   const uint32_t* __restrict__ map, int pow2,
+                                                                   int scale_bf16, int bw) {
   static_assert(W == 1 || P == 1, "blocks of several waves: one block per wave group");
+  constexpr int WAVES = W > 4 ? W : 4;  // waves per work-group
   const int g = (bw + 7) / 8;  // chunks per block
   constexpr int KP = NC / P;  // chunk slots per block
-  __shared__ uint32_t red[4];
+  __shared__ uint32_t red[WAVES];
   Desc d;
   int64_t u;
   pick_desc<kXcdRunRow>(single, descs, map, d, u);
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int K = (g + 64 * W - 1) / (64 * W);  // <= KP
-  const int64_t blk0 = (u * (4 / W) + wave / W) * P;
+  const int64_t blk0 = (u * (WAVES / W) + wave / W) * P;
   const int64_t B = bw;
   const int c0 = 64 * (wave % W) + lane;
 
@@ -599,10 +601,13 @@ static hipError_t launch_fp8_typed(const LaunchCfg& cfg, const Desc& single, con
     case kKernRowWide: {
       const int g = (int)cfg.blk_c;  // the block width
       const WideShape ws = wide_shape(DT, cfg.blk_c);
-#define LRQ_WIDE(W, P, NC) \
-  hipLaunchKernelGGL((k_row_wide<DT, CDT, W, P, NC>), grid, block, 0, stream, single, descs, map, cfg.pow2, cfg.scale_bf16, g)
+#define LRQ_WIDE(W, P, NC)                                                                         \
+  hipLaunchKernelGGL((k_row_wide<DT, CDT, W, P, NC>), grid, dim3(W > 4 ? 64 * W : 256), 0, stream, single, \
+                     descs, map, cfg.pow2, cfg.scale_bf16, g)
       if (ws.nc == kWideChunks) {
-        if (ws.w == 4) LRQ_WIDE(4, 1, kWideChunks);
+        if (ws.w == 16) LRQ_WIDE(16, 1, kWideChunks);
+        else if (ws.w == 8) LRQ_WIDE(8, 1, kWideChunks);
+        else if (ws.w == 4) LRQ_WIDE(4, 1, kWideChunks);
         else LRQ_WIDE(1, 1, kWideChunks);
       } else {
         if (ws.w == 4) LRQ_WIDE(4, 1, 4);

@@ -40,7 +40,7 @@ enum Kernel : int {
   kKernF64 = 11,           // FP8 blocks of a float64 tensor in float64 arithmetic, one wave per block
   kKernF64Row = 12,        // 1xB float64 blocks (B = 32..2048, powers of two), 16-byte loads
   kKernF64Tile = 13,       // 128x128 float64 tiles, one 512-thread work-group per tile
-  kKernRowWide = 16,       // 1xB FP8 blocks, 512 < B <= 16384 but 1024/2048: k_row_wide
+  kKernRowWide = 16,       // 1xB FP8 blocks, 512 < B <= 65536 but 1024/2048: k_row_wide
   kKernF64Wide = 17,       // 1xB float64 blocks k_row_f64 does not take, 2 <= B <= 4096:
                            // k_row_pad_f64 (5 <= B < 128), else k_row_wide_f64
   kKernRowF32 = 15,        // 1xB FP8 blocks of float32 input (B = 8..1024, a power of two), one 16-byte load per lane chunk
@@ -55,12 +55,14 @@ constexpr int64_t kCopyUnit = 4096;  // k_copy: bytes per work-group (one 16 B l
 constexpr int kDequantChunks = 2;    // k_dequant: 16-byte output chunks per lane (2 beat 1, 4 and 8)
 constexpr int kMxLoads = 2;          // k_mx: 32-element groups per quad of lanes (2 beat 1, 3 and 4)
 constexpr int kWideChunks = 8;       // k_row_wide: 8-element chunks per lane (at most)
-// k_row_wide's launch shape for a 1xB block (512 < B <= 16384) of g =
+constexpr int64_t kWideMax = 16 * 64 * 8 * kWideChunks;  // k_row_wide: widest block (16 waves)
+// k_row_wide's launch shape for a 1xB block (512 < B <= 65536) of g =
 // ceil(B/8) chunks: the block takes C = nextpow2(ceil(g/64)) 64-lane steps of
-// chunk slots, as NC slots per lane on W = C/NC waves (at least one), and a
-// wave holds P = NC/C blocks (at least one).  Every slot past a block's chunks
-// re-loads its first chunk.  NC = 4 (43-57 VGPRs) unless the sweeps on an
-// MI355X favoured 8 (65-97 VGPRs): blocks past C = 16, blocks of exactly
+// chunk slots, as NC slots per lane on W = C/NC waves (at least one; 8 or 16
+// waves make a 512- or 1024-thread work-group of one block), and a wave holds
+// P = NC/C blocks (at least one).  Every slot past a block's chunks re-loads
+// its first chunk.  NC = 4 (43-57 VGPRs) unless the sweeps on an MI355X
+// favoured 8 (65-97 VGPRs): blocks past C = 16, blocks of exactly
 // 512 chunks (one wave, every slot used: 1x4096 by 1-2 %) and 16-bit blocks
 // of more than 768 chunks (4 waves of 4 slots, all used: 1x7168 and 1x8192 by
 // 1.5-2 %).  4 slots instead of 8 gained up to 9 % elsewhere (1x4104), float32
@@ -72,7 +74,7 @@ constexpr WideShape wide_shape(int dtype, int64_t blk_c) {
   const int64_t g = (blk_c + 7) / 8;
   int c = 1;
   while (64 * c < g) c *= 2;
-  if (c > 16 || g == 64 * 8 || (dtype != kF32 && g > 64 * 12)) return {kWideChunks, c > 8 ? 4 : 1, 1};
+  if (c > 16 || g == 64 * 8 || (dtype != kF32 && g > 64 * 12)) return {kWideChunks, c > 32 ? c / 8 : c > 8 ? 4 : 1, 1};
   return {4, c > 4 ? c / 4 : 1, c < 4 ? 4 / c : 1};
 }
 constexpr int kTileThreads = 512;    // k_tile128: threads per 128x128 tile (512 beat 256 and 1024)

@@ -584,7 +584,7 @@ class QuantPlan:
     Inputs are device tensors: any element-aligned view and any row pitch (the
     kernels' 16-byte loads take 2-byte-aligned addresses).  All tensors of a plan
     must take one kernel: 128x128 tiles with K % 8 == 0 and 1xB blocks (B from
-    8 to 16384) take the vector kernels, other shapes the generic one, and a
+    8 to 65536) take the vector kernels, other shapes the generic one, and a
     plan mixing the two raises ``ValueError`` (quantize those tensors with
     :func:`fp8_block_quant` one by one).  float64 weights take
     ``fmt="fp8_block"`` with ``native_arith=True`` (float64 arithmetic and

@@ -162,8 +162,12 @@ def test_group_pack_rows_and_mx_units():
         for B, per_wg in cases:
             buf = _pack(_lib.FMT_FP8_BLOCK, [(1, 256, 16 * B), (1, 72, 3 * B)], (1, B), dtype=dt)
             assert L().lrq_group_units(buf.ctypes.data) == -(-256 * 16 // per_wg) + -(-72 * 3 // per_wg), B
-    # widths under 8 and past 16384 take the generic kernel: one work-group per block
-    for B in (5, 7, 16392):
+    # past 16384, one block of 8 or 16 waves per work-group up to 65536
+    for B in (16392, 18944, 32768, 65536):
+        buf = _pack(_lib.FMT_FP8_BLOCK, [(1, 8, 2 * B), (1, 3, B)], (1, B))
+        assert L().lrq_group_units(buf.ctypes.data) == 8 * 2 + 3, B
+    # widths under 8 and past 65536 take the generic kernel: one work-group per block
+    for B in (5, 7, 65544):
         buf = _pack(_lib.FMT_FP8_BLOCK, [(1, 4, 2 * B)], (1, B))
         assert L().lrq_group_units(buf.ctypes.data) == 4 * 2, B
 

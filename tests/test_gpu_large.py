@@ -85,11 +85,12 @@ def test_mx(base, fmt):
     same(s, osc.reshape(BASE_ROWS, -1), f"mx{fmt} scales")
 
 
-@pytest.mark.parametrize("blk", [(1, 36), (1, 4096)])
+@pytest.mark.parametrize("blk", [(1, 36), (1, 4096), (1, 32768)])
 def test_fp8_row_widths(base, blk):
     """1x36 (padded lane groups, the last chunk overlapped) over the first 32760
-    columns of each row, a strided view of 2.15 G elements; 1x4096 (the
-    wide-row kernel) over the whole tensor."""
+    columns of each row, a strided view of 2.15 G elements; 1x4096 and 1x32768
+    (whole rows: the wide-row kernel with one and with eight waves per block)
+    over the whole tensor."""
     say("large fp8 rows", blk)
     x = big_of(base)
     cols = COLS - COLS % blk[1]

@@ -6,9 +6,10 @@
 power of two (the last lanes of each group idle); when 8 does not divide B
 (12, 36, 100, 500) the last chunk overlaps its neighbour.  1024 and 2048 run on
 the row kernel with a block spanning 2 or 4 wave instructions; other widths up
-to 16384 on the wide-row kernel, one wave per block up to 4096 (640, 1000,
-1032, 1536, 3001, 4096) and four beyond (4104, 9999, 12288, 16384); the rest
-(5, 7, 16392) on the generic kernel.  Every code and scale bit is compared
+to 65536 on the wide-row kernel: one wave per block up to 4096 (640, 1000,
+1032, 1536, 3001, 4096), two or four up to 16384 (4104, 9999, 12288, 16384),
+a work-group of 8 or 16 waves beyond (16392, 18944, 29568, 65536); the rest
+(5, 7, 65544) on the generic kernel.  Every code and scale bit is compared
 with the oracle, and the drop-in with the reference's torch op sequence.
 """
 
@@ -31,7 +32,7 @@ DEV = torch.device("cuda", 0)
 DT = {"bf16": torch.bfloat16, "f16": torch.float16, "f32": torch.float32}
 WIDTHS = [40, 48, 96, 120, 200, 248, 504, 8, 16, 24, 36, 1024, 2048, 1536,
           640, 1032, 4096, 4104, 12288, 16384, 16392, 12, 100, 500, 1000, 3001, 9999, 5, 7,
-          3072, 4090, 6144, 7000, 8192]
+          3072, 4090, 6144, 7000, 8192, 18944, 29568, 65536, 65544]
 # (rows, blocks per row, row pitch padding, pow2, bf16 scales when arith is f32)
 CASES = [(1, 1, 0, False, False), (37, 3, 0, True, False), (200, 5, 16, False, True),
          (513, 2, 0, False, False), (64, 11, 8, True, False)]

@@ -50,7 +50,7 @@ def model_units(dt, batch, rows, cols, ld, bstride, blk_r, blk_c, in_off, codes_
         while lanes < cdiv(blk_c, 8):
             lanes *= 2
         return cdiv(nblocks, 4 * ROW_BLOCKS * (64 // lanes))
-    if 512 < blk_c <= 16384 and vec_row:
+    if 512 < blk_c <= 65536 and vec_row:
         # the fewest 64-lane steps (a power of two) of 8-element chunk slots that
         # hold a block, as 4 or 8 slots per lane
         chunks = cdiv(blk_c, 8)
@@ -59,7 +59,7 @@ def model_units(dt, batch, rows, cols, ld, bstride, blk_r, blk_c, in_off, codes_
             steps *= 2
         eight = steps > 16 or chunks == 512 or (dt != _lib.DTYPE_F32 and chunks > 768)
         if eight:
-            return cdiv(nblocks, 4 if steps == 8 else 1)  # 4 one-wave blocks, or one 4-wave block
+            return cdiv(nblocks, 4 if steps == 8 else 1)  # 4 one-wave blocks, or one block of 4-16 waves
         if steps <= 4:
             return cdiv(nblocks, 4 * (4 // steps))  # 4 waves of 4/steps blocks
         return cdiv(nblocks, 4 // (steps // 4))  # blocks of 2 or 4 waves
@@ -80,7 +80,8 @@ def library_units(dt, batch, rows, cols, ld, bstride, blk_r, blk_c, in_off, code
 
 
 WIDTHS = [5, 8, 12, 16, 24, 32, 36, 40, 64, 96, 100, 128, 256, 500, 512, 640, 1000, 1024, 1536,
-          2048, 2056, 3001, 4090, 4096, 4104, 6144, 6152, 8192, 8200, 9999, 16384, 16392]
+          2048, 2056, 3001, 4090, 4096, 4104, 6144, 6152, 8192, 8200, 9999, 16384, 16392, 18944,
+          29568, 65536, 65544]
 
 
 @settings(max_examples=400, deadline=None)
@@ -117,4 +118,6 @@ def test_model_spot_checks():
     assert model_units(bf, 1, 4, 8192, 8192, 4 * 8192, 1, 4096, 0, 0) == 2
     assert model_units(bf, 1, 4, 12000, 12000, 4 * 12000, 1, 6000, 0, 0) == 8  # 4 waves per block
     assert model_units(bf, 1, 4, 7000, 7000, 4 * 7000, 1, 7000, 0, 0) == 4
+    assert model_units(bf, 1, 64, 18944, 18944, 64 * 18944, 1, 18944, 0, 0) == 64  # 8 waves per block
+    assert model_units(bf, 1, 4, 65544, 65544, 4 * 65544, 1, 65544, 0, 0) == 4  # generic, one per block
     assert library_units(bf, 1, 4096, 4096, 4096, 4096 * 4096, 128, 128, 0, 0) == 1024
