@@ -117,8 +117,8 @@ int fp8_kernel_for(const Desc& d, int in_dtype, int64_t blk_r, int64_t blk_c) {
                      (d.batch == 1 || d.bstride == d.rows * d.ld) && aligned(d.in, 8) &&
                      aligned(d.codes, 2) && aligned(d.scales, 8);
     if (row) return lrq::kKernF64Row;
-    // other widths 2..4096 (2-double chunks, the last overlapped when B is odd)
-    const bool wide = blk_r == 1 && blk_c >= 2 && blk_c <= 4096 && d.cols % blk_c == 0 &&
+    // other widths 2..16384 (2-double chunks, the last overlapped when B is odd)
+    const bool wide = blk_r == 1 && blk_c >= 2 && blk_c <= 16384 && d.cols % blk_c == 0 &&
                       (d.batch == 1 || d.bstride == d.rows * d.ld) && aligned(d.in, 8) && aligned(d.scales, 8);
     if (wide) return lrq::kKernF64Wide;
     const bool tile = blk_r == 128 && blk_c == 128 && aligned(d.in, 8) && d.cols % 2 == 0 &&

@@ -9,7 +9,7 @@
 //
 // k_row_f64 takes 1xB blocks (B = 32...2048, powers of two, the reference's
 // layout), k_row_pad_f64 narrower widths (5 <= B < 128) on padded lane groups,
-// k_row_wide_f64 the other 1xB widths up to 4096, and k_tile_f64 128x128 tiles,
+// k_row_wide_f64 the other 1xB widths up to 16384, and k_tile_f64 128x128 tiles,
 // all with 16-byte loads.  Their quotients of finite blocks use one correctly
 // rounded 1/s per block and Markstein's correction per element (the IEEE
 // division in blocks with tiny scales) and the hardware e4m3 encoder.  k_f64
@@ -397,29 +397,32 @@ __global__ __launch_bounds__(512) void k_tile_f64(Desc single, const Desc* __res
 }
 
 // 1xB blocks of a float64 tensor for the widths neither k_row_f64 nor
-// k_row_pad_f64 takes (128 < B <= 4096 not a power of two, B = 4096, and
+// k_row_pad_f64 takes (128 < B <= 16384 but the powers of two to 2048, and
 // B = 2..4): ceil(B/2) chunks of 2 doubles (16
 // bytes), the last starting at B - 2 when B is odd (it overlaps its
 // neighbour: the amax ignores the repeat, and both lanes write the same
-// codes).  As k_row_wide: W waves per block (1 up to B = 1024, else 4), lane l
+// codes).  As k_row_wide: W waves per block (1 up to B = 1024, 4 up to 4096,
+// then a 512- or 1024-thread work-group of 8 or 16 waves up to 16384), lane l
 // of wave w holding chunks 64 w + l + 64 W k for k < K = ceil(g / 64W) <= 8;
 // with W = 1 a wave takes P consecutive blocks.  Lanes past a block's end,
 // and slots past K, re-load its first chunk and drop out of the amax, so the
 // loads issue without branches.  Quotients as in k_row_f64 (Markstein's step in
 // fast blocks, IEEE division otherwise).
 template <int W, int P>
-__global__ __launch_bounds__(256) void k_row_wide_f64(Desc single, const Desc* __restrict__ descs,
-                                                      const uint32_t* __restrict__ map, int pow2, int bw) {
+__global__ __launch_bounds__(W > 4 ? 64 * W : 256) void k_row_wide_f64(Desc single, const Desc* __restrict__ descs,
+                                                                       const uint32_t* __restrict__ map, int pow2,
+                                                                       int bw) {
   static_assert(W == 1 || P == 1, "blocks of several waves: one block per wave group");
+  constexpr int WAVES = W > 4 ? W : 4;  // waves per work-group
   constexpr int KP = 8 / P;  // chunk slots per block
-  __shared__ uint64_t red[4];
+  __shared__ uint64_t red[WAVES];
   Desc d;
   int64_t u;
   pick_desc<kXcdRunRow>(single, descs, map, d, u);
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int g = (bw + 1) / 2;  // chunks per block
   const int K = (g + 64 * W - 1) / (64 * W);
-  const int64_t blk0 = (u * (4 / W) + wave / W) * P;
+  const int64_t blk0 = (u * (WAVES / W) + wave / W) * P;
   const int c0 = 64 * (wave % W) + lane;
   const double* in = static_cast<const double*>(d.in);
 
@@ -608,7 +611,14 @@ hipError_t launch_f64(const LaunchCfg& cfg, const Desc& single, const Desc* desc
       case 4: hipLaunchKernelGGL((k_row_wide_f64<1, 4>), grid, block, 0, stream, single, descs, map, cfg.pow2, bw); break;
       case 2: hipLaunchKernelGGL((k_row_wide_f64<1, 2>), grid, block, 0, stream, single, descs, map, cfg.pow2, bw); break;
       case 1: hipLaunchKernelGGL((k_row_wide_f64<1, 1>), grid, block, 0, stream, single, descs, map, cfg.pow2, bw); break;
-      default: hipLaunchKernelGGL((k_row_wide_f64<4, 1>), grid, block, 0, stream, single, descs, map, cfg.pow2, bw); break;
+      default:
+        if (cfg.blk_c <= 4096)
+          hipLaunchKernelGGL((k_row_wide_f64<4, 1>), grid, block, 0, stream, single, descs, map, cfg.pow2, bw);
+        else if (cfg.blk_c <= 8192)
+          hipLaunchKernelGGL((k_row_wide_f64<8, 1>), grid, dim3(512), 0, stream, single, descs, map, cfg.pow2, bw);
+        else
+          hipLaunchKernelGGL((k_row_wide_f64<16, 1>), grid, dim3(1024), 0, stream, single, descs, map, cfg.pow2, bw);
+        break;
     }
     return hipGetLastError();
   }

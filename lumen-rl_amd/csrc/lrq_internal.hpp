@@ -41,7 +41,7 @@ enum Kernel : int {
   kKernF64Row = 12,        // 1xB float64 blocks (B = 32..2048, powers of two), 16-byte loads
   kKernF64Tile = 13,       // 128x128 float64 tiles, one 512-thread work-group per tile
   kKernRowWide = 16,       // 1xB FP8 blocks, 512 < B <= 65536 but 1024/2048: k_row_wide
-  kKernF64Wide = 17,       // 1xB float64 blocks k_row_f64 does not take, 2 <= B <= 4096:
+  kKernF64Wide = 17,       // 1xB float64 blocks k_row_f64 does not take, 2 <= B <= 16384:
                            // k_row_pad_f64 (5 <= B < 128), else k_row_wide_f64
   kKernRowF32 = 15,        // 1xB FP8 blocks of float32 input (B = 8..1024, a power of two), one 16-byte load per lane chunk
   kKernRowG = 14,          // 1xB FP8 blocks, B = 8..512 but 32..512 powers of two: k_row with
@@ -94,7 +94,7 @@ constexpr int kF64RowInstr = 4;
 constexpr int f64_row_instr(int64_t blk_c) { return blk_c > 128 * kF64RowInstr ? (int)(blk_c / 128) : kF64RowInstr; }
 // k_row_wide_f64's blocks per wave for a 1xB float64 block: 4, 2 or 1 when its
 // ceil(B/2) 16-byte chunks take at most 2, 4 or 8 of a wave's 64-lane steps,
-// 0 when it takes four waves (B > 1024).
+// 0 when it takes 4, 8 or 16 waves (B > 1024: up to 4096, 8192, 16384).
 constexpr int f64_wide_blocks_per_wave(int64_t blk_c) {
   return blk_c <= 256 ? 4 : blk_c <= 512 ? 2 : blk_c <= 1024 ? 1 : 0;
 }

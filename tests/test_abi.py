@@ -456,6 +456,8 @@ def test_float64_input_needs_float64_arithmetic_and_the_fp8_block_format():
     assert units(7, 112, 120, 16) == -(-7 * 7 // 128)  # L = 8, padded row pitch
     assert units(50, 768, 800, 384) == -(-50 * 2 // 8)  # 2 blocks per wave
     assert units(9, 3000, 3000, 3000) == 9              # one block of 4 waves
+    assert units(3, 24576, 24576, 12288) == 6           # one block of 16 waves
+    assert units(8, 16386, 16386, 16386) == 2           # past 16384: generic, 4 blocks per work-group
     assert units(5, 288, 288, 96, 2) == (3 * 3 + 3) // 4  # 2-D blocks: generic
 
 

@@ -69,6 +69,7 @@ def check(xd: torch.Tensor, blk, pow2):
 @pytest.mark.parametrize("blk", [(1, 128), (1, 32), (1, 64), (1, 256), (1, 512), (1, 1024), (1, 2048), (1, 96),
                                  (1, 384), (1, 2), (1, 3), (1, 45), (1, 100), (1, 1000), (1, 3000), (1, 4096),
                                  (1, 5), (1, 7), (1, 8), (1, 16), (1, 33), (1, 65), (1, 127),
+                                 (1, 6000), (1, 8192), (1, 12288), (1, 16384), (1, 16386),
                                  (128, 128), (3, 40), (64, 96)])
 @pytest.mark.parametrize("data", ["weights", "edge"])
 def test_f64_blocks_vs_oracle(data, blk, pow2):
