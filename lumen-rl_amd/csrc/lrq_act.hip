@@ -58,6 +58,12 @@ __device__ __forceinline__ void act_block(const float (&x)[N], uint32_t amax, in
   }
 }
 
+// x_dq of one element, given its block's scale (act_block's per-element step).
+__device__ __forceinline__ uint32_t act_elem(float x, const BlockScale& bs) {
+  if (bs.kind <= kScaleExact) return f2u((x / bs.s) * bs.s);
+  return f2u(x86_mul_scale_first(x86_div(x, bs.s), bs.s));
+}
+
 template <int N>
 __device__ __forceinline__ uint32_t abs_max(const float (&x)[N]) {
   uint32_t a = 0u;
@@ -142,14 +148,45 @@ __global__ __launch_bounds__(256) void k_act_qdq(const void* __restrict__ in, in
   }
 }
 
+// Any other block width B (cols % B == 0; the vector kernels take 32, 64,
+// 128 and 256): one wave per block, four per work-group.  The wave walks the
+// block's elements 64 at a time twice, for the amax and then for x_dq (the
+// second pass reads from L2); each pass's loads and float32 stores are
+// coalesced across the wave.
+template <int DT, bool DENSE>
+__global__ __launch_bounds__(256) void k_act_generic(const void* __restrict__ in, int64_t rows, int64_t cols,
+                                                     int64_t ld, int64_t blk, float* __restrict__ out, int pow2) {
+  const int64_t nb = rows * (cols / blk);
+  const int64_t bi = xcd_unit<kXcdRunStream>(blockIdx.x, gridDim.x) * 4 + (threadIdx.x >> 6);
+  if (bi >= nb) return;  // the whole wave: this kernel has no barrier
+  const int lane = threadIdx.x & 63;
+  const int64_t e0 = bi * blk;  // the block's first element of the dense sequence
+  auto load = [&](int64_t i) -> float {
+    const int64_t off = act_offset(e0 + i, cols, ld, DENSE);
+    if constexpr (DT == kF32) return gld<float>(static_cast<const float*>(in) + off);
+    else if constexpr (DT == kBF16) return u2f((uint32_t)gld<uint16_t>(static_cast<const uint16_t*>(in) + off) << 16);
+    else return f16_to_f32(gld<uint16_t>(static_cast<const uint16_t*>(in) + off));
+  };
+  uint32_t a = 0u;
+  for (int64_t i = lane; i < blk; i += 64) {
+    const uint32_t m = f2u(load(i)) & 0x7FFFFFFFu;
+    a = m > a ? m : a;
+  }
+  a = __builtin_amdgcn_readfirstlane(wave_max(a));
+  const BlockScale bs = block_scale<kF32>(a, pow2 != 0);
+  for (int64_t i = lane; i < blk; i += 64) gst_nt<float>(out + e0 + i, u2f(act_elem(load(i), bs)));
+}
+
 constexpr int kActChunks = 2;
 
-// 16-bit input takes the 8-per-lane kernel (any element alignment and row
-// pitch: its 16-byte loads take 2-byte-aligned addresses), float32 the
-// 4-per-lane one.
-int64_t act_grid(const void* in, int dtype, int64_t rows, int64_t cols, int64_t ld) {
-  (void)in;
-  (void)ld;
+// Blocks of 32, 64, 128 or 256 elements take the vector kernels: 16-bit input
+// the 8-per-lane one (any element alignment and row pitch: its 16-byte loads
+// take 2-byte-aligned addresses), float32 the 4-per-lane one.  Other widths
+// take k_act_generic, four blocks per work-group.
+bool act_vector_block(int64_t blk) { return blk == 32 || blk == 64 || blk == 128 || blk == 256; }
+
+int64_t act_grid(int dtype, int64_t rows, int64_t cols, int64_t blk) {
+  if (!act_vector_block(blk)) return (rows * (cols / blk) + 3) / 4;
   const int64_t per_wg = dtype != kF32 ? 2048 : 1024 * kActChunks;
   return (rows * cols + per_wg - 1) / per_wg;
 }
@@ -157,9 +194,11 @@ int64_t act_grid(const void* in, int dtype, int64_t rows, int64_t cols, int64_t 
 template <int DT, bool DENSE>
 static hipError_t launch_act_typed(const void* in, int64_t rows, int64_t cols, int64_t ld, int64_t blk,
                                    float* out, int pow2, hipStream_t stream) {
-  const dim3 grid((unsigned)act_grid(in, DT, rows, cols, ld)), block(256);
+  const dim3 grid((unsigned)act_grid(DT, rows, cols, blk)), block(256);
   const uint16_t* in16 = static_cast<const uint16_t*>(in);
-  if constexpr (DT != kF32) {
+  if (!act_vector_block(blk)) {
+    hipLaunchKernelGGL((k_act_generic<DT, DENSE>), grid, block, 0, stream, in, rows, cols, ld, blk, out, pow2);
+  } else if constexpr (DT != kF32) {
     switch (blk) {
       case 32: hipLaunchKernelGGL((k_act_qdq8<DT, 4, DENSE>), grid, block, 0, stream, in16, rows, cols, ld, out, pow2); break;
       case 64: hipLaunchKernelGGL((k_act_qdq8<DT, 8, DENSE>), grid, block, 0, stream, in16, rows, cols, ld, out, pow2); break;

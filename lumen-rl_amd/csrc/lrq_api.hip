@@ -589,8 +589,7 @@ int lrq_act_qdq(const void* in, int in_dtype, int64_t rows, int64_t cols, int64_
                 unsigned flags, float* out, lrq_stream_t stream) {
   g_err.clear();
   if (!valid_dtype(in_dtype)) return fail(LRQ_ERR_ARG, "bad input dtype %d", in_dtype);
-  if (blk != 32 && blk != 64 && blk != 128 && blk != 256)
-    return fail(LRQ_ERR_ARG, "activation block must be 32, 64, 128 or 256, got %lld", (long long)blk);
+  if (blk < 1) return fail(LRQ_ERR_ARG, "activation block must be positive, got %lld", (long long)blk);
   if (rows < 0 || cols < 0 || cols % blk != 0)
     return fail(LRQ_ERR_ARG, "cols (%lld) must be a multiple of the block", (long long)cols);
   if (!span_ok(1, rows, cols, ld < cols ? cols : ld, 0)) return fail(LRQ_ERR_ARG, "extents exceed 2^48 elements");
@@ -600,7 +599,7 @@ int lrq_act_qdq(const void* in, int in_dtype, int64_t rows, int64_t cols, int64_
   const int64_t es = esize(in_dtype);
   if (!aligned(in, (uintptr_t)es) || !aligned(out, 16))
     return fail(LRQ_ERR_ALIGN, "activation input must be element-aligned, out 16-byte aligned");
-  if (lrq::act_grid(in, in_dtype, rows, cols, ld) > kMaxGrid) return fail(LRQ_ERR_ARG, "tensor too large for one launch");
+  if (lrq::act_grid(in_dtype, rows, cols, blk) > kMaxGrid) return fail(LRQ_ERR_ARG, "tensor too large for one launch");
   return check_hip(lrq::launch_act(in, in_dtype, rows, cols, ld, blk, out,
                                    (flags & LRQ_FLAG_POW2_SCALE) ? 1 : 0, (hipStream_t)stream),
                    "kernel launch");

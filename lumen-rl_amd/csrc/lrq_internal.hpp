@@ -173,7 +173,7 @@ hipError_t launch_cast(int dtype, const Desc& single, const Desc* descs, const u
                        int64_t units, hipStream_t stream);
 
 // Activation fake-quant.
-int64_t act_grid(const void* in, int dtype, int64_t rows, int64_t cols, int64_t ld);
+int64_t act_grid(int dtype, int64_t rows, int64_t cols, int64_t blk);
 hipError_t launch_act(const void* in, int dtype, int64_t rows, int64_t cols, int64_t ld, int64_t blk,
                       float* out, int pow2, hipStream_t stream);
 

@@ -97,6 +97,22 @@ def test_act_vs_oracle(dt, blk, pow2):
     assert np.array_equal(f32bits(out), want.view(np.uint32))
 
 
+@pytest.mark.parametrize("blk", [1, 16, 96, 100, 512, 1024, 3000])
+@pytest.mark.parametrize("dt", ["bf16", "f16", "f32"])
+def test_act_other_widths_vs_oracle(dt, blk):
+    """Block widths the vector kernels do not take (one wave per block), dense
+    and as a strided view, with NaN/inf/zero/subnormal blocks."""
+    cols = blk * max(1, 3000 // blk) if blk < 3000 else 6000
+    x = plant_edges(acts((40, cols + 8)), min(blk, 64))
+    t = to_dev(x, dt)
+    for pow2 in (False, True):
+        for v in (t[:, :cols].contiguous(), t[:, 8:]):
+            say("act other widths", dt, blk, pow2, tuple(v.shape), v.stride())
+            out = act_qdq(v, blk, pow2=pow2)
+            want = O.act_qdq(oracle_in(v), dt, blk, pow2)
+            assert np.array_equal(f32bits(out), want.view(np.uint32)), (dt, blk, pow2, v.stride())
+
+
 def test_act_vs_torch_reference_bf16():
     x = acts((64, 2048))
     t = to_dev(x, "bf16")
@@ -146,7 +162,7 @@ def test_act_empty_and_errors():
     with pytest.raises(ValueError, match="multiple of the block"):
         act_qdq(torch.ones(4, 200, device=DEV, dtype=torch.bfloat16), 128)
     with pytest.raises(ValueError, match="activation block must be"):
-        act_qdq(torch.ones(4, 256, device=DEV, dtype=torch.bfloat16), 16)
+        act_qdq(torch.ones(4, 256, device=DEV, dtype=torch.bfloat16), 0)
     with pytest.raises(ValueError):
         act_qdq(torch.ones(4, 256, dtype=torch.bfloat16))
 
@@ -184,6 +200,25 @@ def test_fp8_linear_matches_reference(dtype, pow2, bias):
     with torch.no_grad():
         yk = keep(x)
     assert yk.shape == (3, 17, 384) and torch.equal(yk.reshape(51, 384), y_ref)
+
+
+def test_fp8_linear_any_activation_block():
+    """activation_block_size = 96 (any divisor of in_features, fp8_rollout.py:36-44)
+    against the reference's op sequence."""
+    torch.manual_seed(4)
+    lin = nn.Linear(384, 200).to(DEV, torch.bfloat16)
+    cfg = FP8Config(precision="fp8")
+    mod = _FP8W8A8Linear(lin, WeightQuantizer(cfg), cfg, 96)
+    x = torch.from_numpy(acts((2, 9, 384))).to(DEV, torch.bfloat16)
+    q, s = T.quantize_tensor(lin.weight.data.cpu().float(), 96, False)
+    s16 = s.to(torch.bfloat16)
+    x_dq = T.act_qdq(x.cpu(), 96, False)
+    w_dq = T.dequantize_tensor(q, s16, 96).float()
+    y_ref = F.linear(x_dq.to(DEV), w_dq.to(DEV), lin.bias.data.float()).to(torch.bfloat16)
+    with torch.no_grad():
+        y = mod(x)
+    assert np.array_equal(mod.weight_fp8.cpu().view(torch.uint8).numpy(), q.view(torch.uint8).numpy())
+    assert torch.equal(y, y_ref)
 
 
 def test_fp8_linear_float64_activations():
