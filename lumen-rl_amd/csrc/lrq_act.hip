@@ -149,7 +149,8 @@ __global__ __launch_bounds__(256) void k_act_qdq(const void* __restrict__ in, in
 }
 
 // Any other block width B (cols % B == 0; the vector kernels take 32, 64,
-// 128 and 256): one wave per block, four per work-group.  The wave walks the
+// 128, 256 and, for 16-bit input, 512): one wave per block, four per
+// work-group.  The wave walks the
 // block's elements 64 at a time twice, for the amax and then for x_dq (the
 // second pass reads from L2); each pass's loads and float32 stores are
 // coalesced across the wave.
@@ -179,14 +180,16 @@ __global__ __launch_bounds__(256) void k_act_generic(const void* __restrict__ in
 
 constexpr int kActChunks = 2;
 
-// Blocks of 32, 64, 128 or 256 elements take the vector kernels: 16-bit input
-// the 8-per-lane one (any element alignment and row pitch: its 16-byte loads
-// take 2-byte-aligned addresses), float32 the 4-per-lane one.  Other widths
-// take k_act_generic, four blocks per work-group.
-bool act_vector_block(int64_t blk) { return blk == 32 || blk == 64 || blk == 128 || blk == 256; }
+// Blocks of 32, 64, 128 or 256 elements (16-bit input: also 512) take the
+// vector kernels: 16-bit input the 8-per-lane one (any element alignment and
+// row pitch: its 16-byte loads take 2-byte-aligned addresses), float32 the
+// 4-per-lane one.  Other widths take k_act_generic, four blocks per work-group.
+bool act_vector_block(int dtype, int64_t blk) {
+  return blk == 32 || blk == 64 || blk == 128 || blk == 256 || (blk == 512 && dtype != kF32);
+}
 
 int64_t act_grid(int dtype, int64_t rows, int64_t cols, int64_t blk) {
-  if (!act_vector_block(blk)) return (rows * (cols / blk) + 3) / 4;
+  if (!act_vector_block(dtype, blk)) return (rows * (cols / blk) + 3) / 4;
   const int64_t per_wg = dtype != kF32 ? 2048 : 1024 * kActChunks;
   return (rows * cols + per_wg - 1) / per_wg;
 }
@@ -196,7 +199,7 @@ static hipError_t launch_act_typed(const void* in, int64_t rows, int64_t cols, i
                                    float* out, int pow2, hipStream_t stream) {
   const dim3 grid((unsigned)act_grid(DT, rows, cols, blk)), block(256);
   const uint16_t* in16 = static_cast<const uint16_t*>(in);
-  if (!act_vector_block(blk)) {
+  if (!act_vector_block(DT, blk)) {
     hipLaunchKernelGGL((k_act_generic<DT, DENSE>), grid, block, 0, stream, in, rows, cols, ld, blk, out, pow2);
   } else if constexpr (DT != kF32) {
     switch (blk) {
@@ -204,6 +207,7 @@ static hipError_t launch_act_typed(const void* in, int64_t rows, int64_t cols, i
       case 64: hipLaunchKernelGGL((k_act_qdq8<DT, 8, DENSE>), grid, block, 0, stream, in16, rows, cols, ld, out, pow2); break;
       case 128: hipLaunchKernelGGL((k_act_qdq8<DT, 16, DENSE>), grid, block, 0, stream, in16, rows, cols, ld, out, pow2); break;
       case 256: hipLaunchKernelGGL((k_act_qdq8<DT, 32, DENSE>), grid, block, 0, stream, in16, rows, cols, ld, out, pow2); break;
+      case 512: hipLaunchKernelGGL((k_act_qdq8<DT, 64, DENSE>), grid, block, 0, stream, in16, rows, cols, ld, out, pow2); break;
       default: return hipErrorInvalidValue;
     }
   } else {

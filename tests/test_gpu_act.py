@@ -85,7 +85,7 @@ def test_act_golden(name):
 
 
 @pytest.mark.parametrize("dt", ["bf16", "f16", "f32"])
-@pytest.mark.parametrize("blk", [32, 64, 128, 256])
+@pytest.mark.parametrize("blk", [32, 64, 128, 256, 512])
 @pytest.mark.parametrize("pow2", [False, True])
 def test_act_vs_oracle(dt, blk, pow2):
     x = plant_edges(acts((300, 1024)), blk)
