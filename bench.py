@@ -14,6 +14,8 @@ already resident in HBM:
   c4: c2 shapes, Student-t(4) x 0.02/sqrt(2), MXFP8.
   c5: c2 shapes, N(0, 0.02^2) x per-row log-uniform[0.25, 4], MXFP4.
   c2r: c2 weights with the reference's own 1x128 blocks (scales [N, K/128]).
+  c2pc: c2 weights with per-channel scales (1xK blocks: quantize_tensor with
+       block_size = in_features), one grouped launch per row width.
   c2d: dequantize_state_dict of the c2r result: e4m3 codes + bf16 1x128 scales ->
        bf16 weights, ONE grouped launch.
   c2sd: the drop-in WeightQuantizer.quantize_state_dict on the c2 weights held
@@ -69,11 +71,12 @@ PROFILE_FOR = {"c1": "k_tile128_single_4096x4096_c1", "c2": "k_tile128_qwen3_8b_
                "act": "k_act_qdq_qwen3_8b_prefill_8192", "kv": "k_amax_qwen3_8b_qkv_scales",
                "cast": "k_cast_e4m3_qwen3_8b_state_dynamic_weight_loader",
                "c4d": "k_mx_dequant_qwen3_8b_mxfp8_to_bf16", "c2sd": "k_row_qwen3_8b_state_dict_dropin",
-               "rollout": "k_row_qwen3_8b_rollout_quantize_model",
+               "rollout": "k_row_qwen3_8b_rollout_quantize_model", "c2pc": "k_row_wide_qwen3_8b_per_channel",
                "f64": "k_row_f64_qwen3_8b_4_layers_quantize_tensor"}
 KERNEL_FOR = {"c1": "k_tile128", "c2": "k_tile128", "c3": "k_tile128", "c4": "k_mx", "c5": "k_mx",
               "c2r": "k_row", "c2d": "k_dequant", "act": "k_act_qdq8", "kv": "k_amax", "c2sd": "k_row", "bucket": "k_tile128",
-              "cast": "k_cast_e4m3", "c4d": "k_mx_dequant", "rollout": "k_row", "f64": "k_row_f64"}
+              "cast": "k_cast_e4m3", "c4d": "k_mx_dequant", "rollout": "k_row", "f64": "k_row_f64",
+              "c2pc": "k_row_wide"}
 PREFILL_TOKENS = 8192
 
 
@@ -199,7 +202,7 @@ def cpu_baseline(torch, ws, fmt, fmt_block, seconds, full_bytes=None):
     f64 = not isinstance(ws[0], (tuple, list)) and ws[0].dtype == torch.float64
     what = {
         "fp8_block": (f"oracle/torch_ref.py (weight_quantizer.py op order on "
-                      f"{fmt_block[0]}x{fmt_block[1]} blocks, "
+                      + (f"{fmt_block[0]}x{fmt_block[1]} blocks, " if fmt_block[1] else "1xK (whole-row) blocks, ")
                       + ("float64 arithmetic, no upcast)" if f64 else "fp32 upcast first)")),
         "fp8_dequant": "oracle/torch_ref.py (weight_quantizer.py:79-89 then the bf16 cast of :133)",
         "act": "oracle/torch_ref.py (fp8_rollout.py:53-72 op order)",
@@ -300,7 +303,7 @@ def _cpu_pass(torch, O, torch_ref, np, ws, fmt, fmt_block, threads):
                 q, s = torch_ref.quantize_tensor_tiles(x.float(), (128, 128))
             else:  # float64 weights keep float64 arithmetic (weight_quantizer.py:40-77)
                 q, s = torch_ref.quantize_tensor(x if x.dtype == torch.float64 else x.float(),
-                                                 fmt_block[1])
+                                                 fmt_block[1] or x.shape[-1])
             t_total += time.perf_counter() - t0
             done_bytes += x.numel() * x.element_size() + q.numel() + s.numel() * s.element_size()
         else:
@@ -471,6 +474,19 @@ def run(args):
         cpu_ws, cpu_blk, cpu_fmt = ws, blk, fmt
         extra = {"tensors": len(ws), "layers": 36, "elements": sum(w.numel() for w in ws),
                  "format": fmt, "launches_per_step": 1}
+    elif cfg == "c2pc":
+        # per-channel scales, quantize_tensor(w, block_size=in_features): one
+        # grouped launch per row width (1x4096 for six projections, 1x12288
+        # for down_proj), since a plan holds one block shape
+        ws, _ = qwen3_8b_set(torch, dev, args.seed, "normal")
+        by_k: dict = {}
+        for w in ws:
+            by_k.setdefault(w.shape[1], []).append(w)
+        plans = [ops.QuantPlan(g, "fp8_block", (1, k)) for k, g in sorted(by_k.items())]
+        workload = "qwen3-8b-linears-fp8-e4m3-per-channel"
+        cpu_ws, cpu_blk, cpu_fmt = ws, (1, 0), "fp8_block"
+        extra = {"tensors": len(ws), "layers": 36, "elements": sum(w.numel() for w in ws),
+                 "format": "fp8_block_1xK_per_channel", "launches_per_step": len(plans)}
     elif cfg == "f64":
         ws, _ = qwen3_8b_set(torch, dev, args.seed, "normal", layers=4)
         ws = [w.double() for w in ws]  # bf16 values widened exactly
@@ -953,7 +969,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--config", default="c2", choices=["c1", "c2", "c3", "c4", "c5", "c2r", "c2d", "c2sd", "bucket",
+    ap.add_argument("--config", default="c2", choices=["c1", "c2", "c3", "c4", "c5", "c2r", "c2pc", "c2d", "c2sd", "bucket",
                                                       "act", "kv", "cast", "c4d", "c2host", "casthost",
                                                       "rollout", "f64"])
     ap.add_argument("--seed", type=int, default=1000)
