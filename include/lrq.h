@@ -144,7 +144,7 @@ int lrq_mxfp4_quant(const void* in, int in_dtype, int64_t rows, int64_t cols, in
  *   in  : [rows, cols] in_dtype, element-aligned, any row stride ld;
  *   out : [rows, cols] float32, dense, 16-byte aligned;  blk any width that
  *         divides cols (32, 64, 128, 256 and, for 16-bit input, 512 on the
- *         vector kernels, others on a kernel of one wave per block).
+ *         vector kernels, others on kernels of one wave per block).
  */
 int lrq_act_qdq(const void* in, int in_dtype, int64_t rows, int64_t cols, int64_t ld, int64_t blk,
                 unsigned flags, float* out, lrq_stream_t stream);

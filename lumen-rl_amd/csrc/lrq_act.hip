@@ -178,12 +178,110 @@ __global__ __launch_bounds__(256) void k_act_generic(const void* __restrict__ in
   for (int64_t i = lane; i < blk; i += 64) gst_nt<float>(out + e0 + i, u2f(act_elem(load(i), bs)));
 }
 
+// Widths that are a multiple of one 16-byte chunk (8 elements of 16-bit
+// input, 4 of float32) up to 512 chunks: one wave per block, four per
+// work-group, lane l holding chunks l + 64 k (k < NCH) in registers, so the
+// block is read once.  Lanes past the block's chunks re-load its first chunk
+// and drop out of the amax.  The float32 results go out as 16-byte stores, each
+// store instruction writing whole lines (16-bit input: results exchanged
+// across the wave as in k_act_qdq8).
+template <int DT, int NCH, bool DENSE>
+__global__ __launch_bounds__(256) void k_act_wide(const void* __restrict__ in, int64_t rows, int64_t cols,
+                                                  int64_t ld, int64_t blk, float* __restrict__ out, int pow2) {
+  constexpr int EPL = DT == kF32 ? 4 : 8;  // elements per 16-byte chunk
+  const int64_t nb = rows * (cols / blk);
+  const int64_t bi = xcd_unit<kXcdRunStream>(blockIdx.x, gridDim.x) * 4 + (threadIdx.x >> 6);
+  if (bi >= nb) return;  // the whole wave: this kernel has no barrier
+  const int lane = threadIdx.x & 63;
+  const int g = (int)(blk / EPL);  // chunks per block
+  const int64_t e0 = bi * blk;
+  const char* src = static_cast<const char*>(in);
+  v4u v[NCH];
+#pragma unroll
+  for (int k = 0; k < NCH; ++k) {
+    const int c = lane + 64 * k;
+    v[k] = load_nt(src + act_offset(e0 + (int64_t)(c < g ? c : 0) * EPL, cols, ld, DENSE) * (DT == kF32 ? 4 : 2));
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  uint32_t a = 0u;
+#pragma unroll
+  for (int k = 0; k < NCH; ++k) {
+    if (lane + 64 * k >= g) continue;
+    const uint32_t w[4] = {v[k].x, v[k].y, v[k].z, v[k].w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      uint32_t m;
+      if constexpr (DT == kF32) {
+        m = w[i] & 0x7FFFFFFFu;
+      } else {
+        const uint32_t lo = DT == kBF16 ? f2u(bf16_lo(w[i])) : f2u(f16_to_f32(w[i] & 0xFFFFu));
+        const uint32_t hi = DT == kBF16 ? f2u(bf16_hi(w[i])) : f2u(f16_to_f32(w[i] >> 16));
+        const uint32_t ml = lo & 0x7FFFFFFFu, mh = hi & 0x7FFFFFFFu;
+        m = ml > mh ? ml : mh;
+      }
+      a = m > a ? m : a;
+    }
+  }
+  a = __builtin_amdgcn_readfirstlane(wave_max(a));
+  const BlockScale bs = block_scale<kF32>(a, pow2 != 0);
+#pragma unroll
+  for (int k = 0; k < NCH; ++k) {
+    if (64 * k >= g) break;  // wave-uniform: every lane takes part in the shuffles below
+    const int c = lane + 64 * k;
+    const uint32_t w[4] = {v[k].x, v[k].y, v[k].z, v[k].w};
+    if constexpr (DT == kF32) {
+      if (c < g) {
+        const v4u o = {act_elem(u2f(w[0]), bs), act_elem(u2f(w[1]), bs), act_elem(u2f(w[2]), bs),
+                       act_elem(u2f(w[3]), bs)};
+        __builtin_nontemporal_store(o, reinterpret_cast<v4u*>(out + e0 + (int64_t)c * EPL));
+      }
+    } else {
+      uint32_t o[8];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float lo = DT == kBF16 ? bf16_lo(w[i]) : f16_to_f32(w[i] & 0xFFFFu);
+        const float hi = DT == kBF16 ? bf16_hi(w[i]) : f16_to_f32(w[i] >> 16);
+        o[2 * i] = act_elem(lo, bs);
+        o[2 * i + 1] = act_elem(hi, bs);
+      }
+      // as k_act_qdq8: store h of lane t writes elements 256 h + 4 t .. + 3 of
+      // slot k's 512-element span (lane 32 h + t/2's chunk, half t & 1), so
+      // each store instruction writes whole lines
+      const bool odd = lane & 1;
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const int src = 32 * h + (lane >> 1);
+        uint32_t r[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const uint32_t lo = (uint32_t)__shfl((int)o[i], src, 64);
+          const uint32_t hi = (uint32_t)__shfl((int)o[4 + i], src, 64);
+          r[i] = odd ? hi : lo;
+        }
+        if (src + 64 * k < g)
+          __builtin_nontemporal_store(v4u{r[0], r[1], r[2], r[3]},
+                                      reinterpret_cast<v4u*>(out + e0 + 512 * k + 256 * h + 4 * lane));
+      }
+    }
+  }
+}
+
+// k_act_wide's chunk slots per lane for a block width (0: not a whole number
+// of 16-byte chunks, or wider than 512 chunks).
+int act_wide_slots(int dtype, int64_t blk) {
+  const int epl = dtype == kF32 ? 4 : 8;
+  if (blk % epl) return 0;
+  const int64_t g = blk / epl;
+  return g <= 64 ? 1 : g <= 128 ? 2 : g <= 256 ? 4 : g <= 512 ? 8 : 0;
+}
+
 constexpr int kActChunks = 2;
 
 // Blocks of 32, 64, 128 or 256 elements (16-bit input: also 512) take the
 // vector kernels: 16-bit input the 8-per-lane one (any element alignment and
 // row pitch: its 16-byte loads take 2-byte-aligned addresses), float32 the
-// 4-per-lane one.  Other widths take k_act_generic, four blocks per work-group.
+// 4-per-lane one.  Other widths take k_act_wide (whole 16-byte chunks, up to
+// 512 of them) or k_act_generic, four blocks per work-group either way.
 bool act_vector_block(int dtype, int64_t blk) {
   return blk == 32 || blk == 64 || blk == 128 || blk == 256 || (blk == 512 && dtype != kF32);
 }
@@ -200,7 +298,13 @@ static hipError_t launch_act_typed(const void* in, int64_t rows, int64_t cols, i
   const dim3 grid((unsigned)act_grid(DT, rows, cols, blk)), block(256);
   const uint16_t* in16 = static_cast<const uint16_t*>(in);
   if (!act_vector_block(DT, blk)) {
-    hipLaunchKernelGGL((k_act_generic<DT, DENSE>), grid, block, 0, stream, in, rows, cols, ld, blk, out, pow2);
+    switch (act_wide_slots(DT, blk)) {
+      case 1: hipLaunchKernelGGL((k_act_wide<DT, 1, DENSE>), grid, block, 0, stream, in, rows, cols, ld, blk, out, pow2); break;
+      case 2: hipLaunchKernelGGL((k_act_wide<DT, 2, DENSE>), grid, block, 0, stream, in, rows, cols, ld, blk, out, pow2); break;
+      case 4: hipLaunchKernelGGL((k_act_wide<DT, 4, DENSE>), grid, block, 0, stream, in, rows, cols, ld, blk, out, pow2); break;
+      case 8: hipLaunchKernelGGL((k_act_wide<DT, 8, DENSE>), grid, block, 0, stream, in, rows, cols, ld, blk, out, pow2); break;
+      default: hipLaunchKernelGGL((k_act_generic<DT, DENSE>), grid, block, 0, stream, in, rows, cols, ld, blk, out, pow2); break;
+    }
   } else if constexpr (DT != kF32) {
     switch (blk) {
       case 32: hipLaunchKernelGGL((k_act_qdq8<DT, 4, DENSE>), grid, block, 0, stream, in16, rows, cols, ld, out, pow2); break;
