@@ -266,6 +266,78 @@ __global__ __launch_bounds__(256) void k_act_wide(const void* __restrict__ in, i
   }
 }
 
+// Narrow widths of whole 16-byte chunks (g <= 32 of them): a block's chunks
+// sit on an aligned group of L = nextpow2(g) lanes (4 at least), so a wave
+// instruction holds 64/L blocks; each lane runs kActPadInstr instructions,
+// each on the wave's next 64/L blocks.  Lanes past g re-load their block's
+// first chunk and drop out of the amax; every lane of a group computes the
+// group's scale.
+constexpr int kActPadInstr = 4;
+template <int DT, int L, bool DENSE>
+__global__ __launch_bounds__(256) void k_act_pad(const void* __restrict__ in, int64_t rows, int64_t cols,
+                                                 int64_t ld, int64_t blk, float* __restrict__ out, int pow2) {
+  constexpr int EPL = DT == kF32 ? 4 : 8;  // elements per 16-byte chunk
+  constexpr int BPI = 64 / L;              // blocks per wave instruction
+  const int64_t nb = rows * (cols / blk);
+  const int lane = threadIdx.x & 63;
+  const int g = (int)(blk / EPL);
+  const int c = lane % L;
+  const int64_t b0 = (xcd_unit<kXcdRunStream>(blockIdx.x, gridDim.x) * 4 + (threadIdx.x >> 6)) *
+                         (kActPadInstr * BPI) + lane / L;
+  const char* src = static_cast<const char*>(in);
+  v4u v[kActPadInstr];
+#pragma unroll
+  for (int i = 0; i < kActPadInstr; ++i) {
+    const int64_t b = b0 + i * BPI;
+    const int64_t bb = b < nb ? b : nb - 1;
+    v[i] = load_nt(src + act_offset(bb * blk + (int64_t)(c < g ? c : 0) * EPL, cols, ld, DENSE) *
+                             (DT == kF32 ? 4 : 2));
+  }
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int i = 0; i < kActPadInstr; ++i) {
+    const int64_t b = b0 + i * BPI;
+    const uint32_t w[4] = {v[i].x, v[i].y, v[i].z, v[i].w};
+    float x[8];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      if constexpr (DT == kF32) {
+        x[j] = u2f(w[j]);
+      } else {
+        x[2 * j] = DT == kBF16 ? bf16_lo(w[j]) : f16_to_f32(w[j] & 0xFFFFu);
+        x[2 * j + 1] = DT == kBF16 ? bf16_hi(w[j]) : f16_to_f32(w[j] >> 16);
+      }
+    }
+    uint32_t a = 0u;
+#pragma unroll
+    for (int j = 0; j < EPL; ++j) {
+      const uint32_t m = f2u(x[j]) & 0x7FFFFFFFu;
+      a = m > a ? m : a;
+    }
+    a = group_max<L>(c < g ? a : 0u);  // the whole group is in or out of range
+    const BlockScale bs = block_scale<kF32>(a, pow2 != 0);
+    if (c < g && b < nb) {
+      float* dst = out + b * blk + (int64_t)c * EPL;
+      uint32_t o[8];
+#pragma unroll
+      for (int j = 0; j < EPL; ++j) o[j] = act_elem(x[j], bs);
+      __builtin_nontemporal_store(v4u{o[0], o[1], o[2], o[3]}, reinterpret_cast<v4u*>(dst));
+      if constexpr (EPL == 8)
+        __builtin_nontemporal_store(v4u{o[4], o[5], o[6], o[7]}, reinterpret_cast<v4u*>(dst + 4));
+    }
+  }
+}
+
+// k_act_pad's lanes per block for a width (0: not a whole number of 16-byte
+// chunks, or more than 32 of them).
+int act_pad_lanes(int dtype, int64_t blk) {
+  const int epl = dtype == kF32 ? 4 : 8;
+  if (blk % epl || blk / epl > 32) return 0;
+  int l = 4;
+  while (l < blk / epl) l *= 2;
+  return l;
+}
+
 // k_act_wide's chunk slots per lane for a block width (0: not a whole number
 // of 16-byte chunks, or wider than 512 chunks).
 int act_wide_slots(int dtype, int64_t blk) {
@@ -280,14 +352,20 @@ constexpr int kActChunks = 2;
 // Blocks of 32, 64, 128 or 256 elements (16-bit input: also 512) take the
 // vector kernels: 16-bit input the 8-per-lane one (any element alignment and
 // row pitch: its 16-byte loads take 2-byte-aligned addresses), float32 the
-// 4-per-lane one.  Other widths take k_act_wide (whole 16-byte chunks, up to
-// 512 of them) or k_act_generic, four blocks per work-group either way.
+// 4-per-lane one.  Other widths of whole 16-byte chunks take k_act_pad (up to
+// 32 chunks, several blocks per wave instruction) or k_act_wide (up to 512,
+// one block per wave); the rest k_act_generic (one block per wave).
 bool act_vector_block(int dtype, int64_t blk) {
   return blk == 32 || blk == 64 || blk == 128 || blk == 256 || (blk == 512 && dtype != kF32);
 }
 
 int64_t act_grid(int dtype, int64_t rows, int64_t cols, int64_t blk) {
-  if (!act_vector_block(dtype, blk)) return (rows * (cols / blk) + 3) / 4;
+  if (!act_vector_block(dtype, blk)) {
+    const int64_t nb = rows * (cols / blk);
+    const int l = act_pad_lanes(dtype, blk);
+    const int64_t per_wg = l ? 4 * kActPadInstr * (64 / l) : 4;
+    return (nb + per_wg - 1) / per_wg;
+  }
   const int64_t per_wg = dtype != kF32 ? 2048 : 1024 * kActChunks;
   return (rows * cols + per_wg - 1) / per_wg;
 }
@@ -297,7 +375,14 @@ static hipError_t launch_act_typed(const void* in, int64_t rows, int64_t cols, i
                                    float* out, int pow2, hipStream_t stream) {
   const dim3 grid((unsigned)act_grid(DT, rows, cols, blk)), block(256);
   const uint16_t* in16 = static_cast<const uint16_t*>(in);
-  if (!act_vector_block(DT, blk)) {
+  if (!act_vector_block(DT, blk) && act_pad_lanes(DT, blk)) {
+    switch (act_pad_lanes(DT, blk)) {
+      case 4: hipLaunchKernelGGL((k_act_pad<DT, 4, DENSE>), grid, block, 0, stream, in, rows, cols, ld, blk, out, pow2); break;
+      case 8: hipLaunchKernelGGL((k_act_pad<DT, 8, DENSE>), grid, block, 0, stream, in, rows, cols, ld, blk, out, pow2); break;
+      case 16: hipLaunchKernelGGL((k_act_pad<DT, 16, DENSE>), grid, block, 0, stream, in, rows, cols, ld, blk, out, pow2); break;
+      default: hipLaunchKernelGGL((k_act_pad<DT, 32, DENSE>), grid, block, 0, stream, in, rows, cols, ld, blk, out, pow2); break;
+    }
+  } else if (!act_vector_block(DT, blk)) {
     switch (act_wide_slots(DT, blk)) {
       case 1: hipLaunchKernelGGL((k_act_wide<DT, 1, DENSE>), grid, block, 0, stream, in, rows, cols, ld, blk, out, pow2); break;
       case 2: hipLaunchKernelGGL((k_act_wide<DT, 2, DENSE>), grid, block, 0, stream, in, rows, cols, ld, blk, out, pow2); break;

@@ -97,13 +97,14 @@ def test_act_vs_oracle(dt, blk, pow2):
     assert np.array_equal(f32bits(out), want.view(np.uint32))
 
 
-@pytest.mark.parametrize("blk", [1, 16, 96, 100, 512, 1024, 3000, 4096])
+@pytest.mark.parametrize("blk", [1, 16, 40, 96, 100, 200, 512, 1024, 3000, 4096])
 @pytest.mark.parametrize("dt", ["bf16", "f16", "f32"])
 def test_act_other_widths_vs_oracle(dt, blk):
-    """Block widths the vector kernels do not take (one wave per block: whole
-    16-byte chunks up to 512 of them held in registers, other widths walked
-    twice), dense, as a strided view and as a view one element off its 16-byte
-    alignment, with NaN/inf/zero/subnormal blocks."""
+    """Block widths the vector kernels do not take: whole 16-byte chunks on
+    padded lane groups (up to 32 chunks) or one wave per block (up to 512),
+    other widths walked twice by one wave per block; dense, as a strided view
+    and as a view one element off its 16-byte alignment, with
+    NaN/inf/zero/subnormal blocks."""
     cols = blk * max(1, 3000 // blk) if blk < 3000 else 2 * blk
     x = plant_edges(acts((40, cols + 8)), min(blk, 64))
     t = to_dev(x, dt)
