@@ -5,6 +5,10 @@
 // GEMM consumes; results match torch on x86 bit for bit (IEEE division per
 // element, x86 NaN/inf rules on blocks whose scale is not finite).
 //
+// Kernels by block width B: k_act_qdq8 (16-bit input, B = 32..512 powers of
+// two) and k_act_qdq (float32, B = 32..256), then for other widths k_act_pad
+// (whole 16-byte chunks, up to 32 per block), k_act_wide (up to 512) and
+// k_act_generic (any B).
 #include "lrq.h"
 #include "lrq_device.hpp"
 #include "lrq_internal.hpp"
