@@ -821,149 +821,6 @@ def run_copy(args):
                       "GBps": 2 * n / (ms * 1e-3) / 1e9}), flush=True)
 
 
-def run_ceiling(args):
-    """Copy-only ceilings beside the kernels they bound, on the same input.
-
-    liblrq_ceiling.so holds copy kernels with each quantization kernel's access
-    pattern (nontemporal 16-byte loads, the same work-group geometry and XCD
-    order, an XOR instead of the arithmetic).  For each row width K in (4096,
-    12288) one dense bf16 [2^30 / K, K] weight (2 GiB) is read:
-
-      tile256/512/1024: the 128x128 tile pattern of k_tile128 at 256, 512 or 1024
-                        threads per tile (8 bytes written per 16 read)
-      stream:           k_row's contiguous 1 KiB wave spans (the same 2:1 bytes),
-                        4 or 8 of them per lane
-      fill:             write-only, 2 bytes per element (k_dequant's store side)
-      widen:            k_dequant's 1:2 bytes, 8 read and 16 written per lane chunk
-      widen 2:4:        the same kernel over the activation fake-quant's bytes (2 read
-                        and 4 written per element), beside k_act_qdq8
-      read:             read-only (k_amax's load side)
-
-    each the best over a few LDS reservations that cap the work-groups per CU
-    (a bare copy at full residency can run slower than a kernel with more work
-    per load), and each is paired with the product kernel it bounds on the
-    same weight:
-    128x128 quantization (k_tile128, 512 threads), 1x128 quantization (k_row),
-    1x128 dequantization to bf16 (k_dequant: 1 byte read + 2 written per
-    element), the activation fake-quant (k_act_qdq8: bf16 in, float32 out) and
-    the per-tensor scale (k_amax and its 4-byte finishing launch).
-    GB/s = bytes moved / median launch time (HIP events on the launch stream,
-    `--steps` launches after `--warmup`).  Prints one JSON line per width.
-    """
-    import ctypes
-
-    import torch
-
-    ops = _ops()
-    path = os.path.join(ROOT, "lumen-rl_amd", "lumenrl_amd", "liblrq_ceiling.so")
-    if not os.path.exists(path):
-        raise SystemExit(f"{path} is missing: build it with `make -C lumen-rl_amd`")
-    C = ctypes.CDLL(path)
-    i64, vp = ctypes.c_int64, ctypes.c_void_p
-    ci = ctypes.c_int
-    C.lrqc_tile.argtypes = [vp, vp, i64, i64, ci, ci, vp]
-    C.lrqc_stream.argtypes = [vp, vp, i64, ci, ci, vp]
-    C.lrqc_fill.argtypes = [vp, i64, ci, vp]
-    C.lrqc_widen.argtypes = [vp, vp, i64, ci, vp]
-    C.lrqc_read.argtypes = [vp, i64, vp, ci, vp]
-    C.lrqc_read_partials.argtypes = [i64]
-    C.lrqc_read_partials.restype = i64
-    dev = torch.device("cuda", 0)
-    stream = torch.cuda.current_stream(dev)
-    sp = vp(stream.cuda_stream)
-
-    def ck(rc, what):
-        if rc != 0:
-            raise RuntimeError(f"{what}: HIP error {rc}")
-
-    def lds_cap(n):
-        """An LDS reservation that lets at most n work-groups share a CU's 160 KiB
-        (0: no reservation)."""
-        return 0 if n == 0 else 163840 // (n + 1) + 256
-
-    def best_ms(fn, caps):
-        """The fastest of fn(lds_bytes) over residency caps: (ms, cap)."""
-        return min((median_ms(lambda: fn(lds_cap(c))), c) for c in caps)
-
-    def median_ms(fn):
-        for _ in range(args.warmup):
-            fn()
-        ev = []
-        for _ in range(args.steps):
-            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            a.record(stream)
-            fn()
-            b.record(stream)
-            ev.append((a, b))
-        torch.cuda.synchronize()
-        t = sorted(a.elapsed_time(b) for a, b in ev)
-        return t[len(t) // 2]
-
-    gen = torch.Generator(device=dev).manual_seed(args.seed)
-    for K in (4096, 12288):
-        R = (1 << 30) // K // 128 * 128
-        n = R * K
-        log(f"[ceiling] K={K}: [{R}, {K}] bf16")
-        x = gen_weight(torch, R, K, gen, dev)
-        out8 = torch.empty(n, dtype=torch.uint8, device=dev)
-        out16 = torch.empty(n, dtype=torch.bfloat16, device=dev)
-        parts = torch.empty(C.lrqc_read_partials(2 * n), dtype=torch.int32, device=dev)
-        rows = []
-
-        def line(pattern, nbytes, best, kernel=None, kbytes=None, kms=None):
-            ms, cap = best
-            r = {"pattern": pattern, "GBps": round(nbytes / ms / 1e6, 1),
-                 "pct_peak": round(100 * nbytes / ms / 1e6 / HBM_PEAK_GBS, 1),
-                 "wg_per_cu_cap": cap or None}
-            if kernel is not None:
-                kg = kbytes / kms / 1e6
-                r.update({"kernel": kernel, "kernel_GBps": round(kg, 1), "kernel_vs_ceiling": round(kg / r["GBps"], 3)})
-            rows.append(r)
-
-        tile = {}
-        for t, caps in ((256, (0, 6, 4, 3)), (512, (0, 3, 2)), (1024, (0,))):
-            tile[t] = best_ms(lambda lds, t=t: ck(C.lrqc_tile(x.data_ptr(), out8.data_ptr(), R, K, t, lds, sp), "tile"),
-                              caps)
-        plan = ops.QuantPlan([x], "fp8_block", (128, 128))
-        q_ms = median_ms(plan.run)
-        qbytes = 3 * n + 4 * (n // 16384)
-        line("tile256", 3 * n, tile[256])
-        line("tile512", 3 * n, tile[512], "k_tile128 (128x128)", qbytes, q_ms)
-        line("tile1024", 3 * n, tile[1024])
-        del plan
-        caps = (0, 6, 5, 4, 3)
-        st = min(best_ms(lambda lds, nl=nl: ck(C.lrqc_stream(x.data_ptr(), out8.data_ptr(), n, nl, lds, sp), "stream"),
-                         caps) for nl in (4, 8))
-        plan = ops.QuantPlan([x], "fp8_block", (1, 128), scale_dtype=torch.bfloat16)
-        r_ms = median_ms(plan.run)
-        codes, scales = plan.run()[0]
-        line("stream", 3 * n, st, "k_row (1x128)", 3 * n + 2 * (n // 128), r_ms)
-        del plan
-        fill = best_ms(lambda lds: ck(C.lrqc_fill(out16.data_ptr(), 2 * n, lds, sp), "fill"), caps)
-        widen = best_ms(lambda lds: ck(C.lrqc_widen(out8.data_ptr(), out16.data_ptr(), n // 8, lds, sp), "widen"),
-                        caps)
-        dplan = ops.DequantPlan([(codes, scales)], (1, 128), torch.bfloat16)
-        d_ms = median_ms(dplan.run)
-        line("fill", 2 * n, fill)
-        line("widen", 3 * n, widen, "k_dequant (1x128 -> bf16)", 3 * n + 2 * (n // 128), d_ms)
-        del dplan, codes, scales
-        # the activation fake-quant's bytes: 2 in, 4 out per element (one 16-byte
-        # load of 8 bf16, two 16-byte stores of 8 float32 per lane chunk)
-        out32 = torch.empty(n, dtype=torch.float32, device=dev)
-        widen2 = best_ms(lambda lds: ck(C.lrqc_widen(x.data_ptr(), out32.data_ptr(), n // 4, lds, sp), "widen"),
-                         caps)
-        act_ms = median_ms(lambda: ops.act_qdq(x, 128, out=out32.view(R, K)))
-        line("widen 2:4", 6 * n, widen2, "k_act_qdq8 (1x128, bf16 -> float32)", 6 * n, act_ms)
-        del out32
-        rd = best_ms(lambda lds: ck(C.lrqc_read(x.data_ptr(), 2 * n, parts.data_ptr(), lds, sp), "read"), caps)
-        tplan = ops.TensorScalePlan([x])
-        a_ms = median_ms(tplan.run)
-        line("read", 2 * n, rd, "k_amax (+ finishing launch)", 2 * n, a_ms)
-        del tplan, x, out8, out16, parts
-        torch.cuda.empty_cache()
-        print(json.dumps({"mode": "ceiling", "K": K, "rows": R, "steps": args.steps, "patterns": rows}), flush=True)
-
-
 def main():
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -975,7 +832,7 @@ def main():
     ap.add_argument("--seed", type=int, default=1000)
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--mode", default="quant", choices=["quant", "copy", "ceiling"])
+    ap.add_argument("--mode", default="quant", choices=["quant", "copy"])
     ap.add_argument("--copy-bytes", type=int, default=1 << 30)
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -985,8 +842,6 @@ def main():
         sys.exit(2)
     if args.mode == "copy":
         run_copy(args)
-    elif args.mode == "ceiling":
-        run_ceiling(args)
     elif args.config in ("c2host", "casthost"):
         run_host(args)
     else:

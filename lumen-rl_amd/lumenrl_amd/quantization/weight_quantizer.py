@@ -48,6 +48,20 @@ def fp8_e4m3_max() -> float:
     return 448.0
 
 
+def _check_unfold(last: int, block_size: int) -> None:
+    """The errors ``flat.unfold(-1, block_size, block_size)`` raises on the
+    reference's 2-D ``[leading, last]`` view (:58-59, :85-86): a negative block,
+    a zero step, or a block wider than the row -- which includes every
+    zero-width row (``[N, 0]``, ``(0,)``) that passes the divisibility check.
+    Checked before any staging or device call."""
+    if block_size < 0:
+        raise RuntimeError(f"size is {block_size} but must be >= 0")
+    if block_size == 0:
+        raise RuntimeError("step is 0 but must be > 0")
+    if block_size > last:
+        raise RuntimeError(f"maximum size for tensor at dimension 1 is {last} but size is {block_size}")
+
+
 def _stage(t: Tensor) -> tuple[Tensor, torch.device | None]:
     """Device copy of a CPU tensor (and the device to return results to)."""
     if t.is_cuda:
@@ -77,6 +91,7 @@ class WeightQuantizer:
         last = tensor.shape[-1]
         if last % block_size != 0:
             raise ValueError(f"Last dim {last} must be divisible by block_size={block_size}")
+        _check_unfold(last, block_size)
         x, home = _stage(tensor)
         pow2 = self._config.use_weight_pow2_scale
         if x.dim() == 2:  # codes [N, K] and scales [N, K/B] as the kernel writes them
@@ -100,6 +115,7 @@ class WeightQuantizer:
     def _dequant(self, quantized: Tensor, scales: Tensor, block_size: int,
                  out_dtype: torch.dtype) -> Tensor:
         last = quantized.shape[-1]
+        _check_unfold(last, block_size)
         q, home = _stage(quantized)
         s = scales.to(q.device)
         if s.dtype == torch.float64:
@@ -153,6 +169,8 @@ class WeightQuantizer:
             return [done[i] for i in range(len(xs))]
 
         keys = [k for k, v in state_dict.items() if self._eligible(v)]
+        for k in keys:  # a [N, 0] weight reaches quantize_tensor's unfold (:105-109)
+            _check_unfold(state_dict[k].shape[1], 128)
         on_dev = [k for k in keys if state_dict[k].is_cuda]
         on_host = [k for k in keys if not state_dict[k].is_cuda]
         results = dict(zip(on_dev, quantize([state_dict[k] for k in on_dev])))
@@ -196,6 +214,8 @@ class WeightQuantizer:
                 continue
             scale_key = f"{key}_fp8_scales"
             if scale_key in state_dict:
+                if value.dim() > 0:  # dequantize_tensor's unfold (:132, :86)
+                    _check_unfold(value.shape[-1], 128)
                 pairs[key] = (value, state_dict[scale_key])
 
         def dequant(items: list[tuple[Tensor, Tensor]]) -> list[Tensor]:

@@ -476,28 +476,3 @@ def test_fp8_dequant_chunk_per_width():
     assert units(1152, 128, False) == -(-n // 4 // 512)
     assert units(1152, 36, False) == -(-n // 4 // 512)
     assert units(1152, 6, True) == -(-n // 256)
-
-
-def test_ceiling_library_checks_arguments_without_a_device():
-    """liblrq_ceiling.so (bench.py --mode ceiling's copy kernels) builds beside
-    liblrq.so and rejects shapes its kernels do not cover before any launch."""
-    path = os.path.join(os.path.dirname(_lib.LIB_PATH), "liblrq_ceiling.so")
-    C = ctypes.CDLL(path)
-    i64, vp, ci = ctypes.c_int64, ctypes.c_void_p, ctypes.c_int
-    C.lrqc_tile.argtypes = [vp, vp, i64, i64, ci, ci, vp]
-    C.lrqc_stream.argtypes = [vp, vp, i64, ci, ci, vp]
-    C.lrqc_widen.argtypes = [vp, vp, i64, ci, vp]
-    C.lrqc_fill.argtypes = [vp, i64, ci, vp]
-    C.lrqc_read.argtypes = [vp, i64, vp, ci, vp]
-    C.lrqc_read_partials.argtypes = [i64]
-    C.lrqc_read_partials.restype = i64
-    bad = 1  # hipErrorInvalidValue
-    assert C.lrqc_tile(None, None, 100, 128, 512, 0, None) == bad      # rows not a multiple of 128
-    assert C.lrqc_tile(None, None, 128, 128, 384, 0, None) == bad      # threads not 256/512/1024
-    assert C.lrqc_tile(None, None, 128, 128, 512, 70000, None) == bad  # LDS past 64 KiB
-    assert C.lrqc_stream(None, None, 8192, 8, 0, None) == bad          # 8 loads: 16384-element units
-    assert C.lrqc_stream(None, None, 8192, 5, 0, None) == bad
-    assert C.lrqc_widen(None, None, 100, 0, None) == bad
-    assert C.lrqc_fill(None, 1000, 0, None) == bad
-    assert C.lrqc_read(None, 1000, None, -1, None) == bad
-    assert C.lrqc_read_partials(1 << 30) == (1 << 30) // 8192

@@ -62,6 +62,61 @@ def test_validation_errors_match_reference_texts():
         wq.quantize_tensor(torch.zeros(2, 100), block_size=0)
 
 
+def _raised(fn):
+    try:
+        fn()
+    except Exception as e:  # noqa: BLE001 - the type and text are what is compared
+        return type(e), str(e)
+    return None
+
+
+@pytest.mark.parametrize("shape", [(4, 0), (0,), (0, 0), (2, 3, 0)])
+@pytest.mark.parametrize("block_size", [128, 64, -128, 0])
+def test_zero_width_rows_raise_as_the_reference(shape, block_size):
+    """Zero-width rows pass the divisibility check and then reach the
+    reference's ``unfold`` (weight_quantizer.py:51-59, :85-86), which raises
+    RuntimeError; the drop-in raises the same error before any staging or
+    device call (so this runs without a device).  ``[0, K]`` stays valid."""
+    from oracle import torch_ref
+
+    wq = WeightQuantizer(FP8Config())
+    x = torch.zeros(shape)
+    want = _raised(lambda: torch_ref.quantize_tensor(x, block_size))
+    assert want is not None and want[0] in (RuntimeError, ZeroDivisionError)
+    assert _raised(lambda: wq.quantize_tensor(x, block_size)) == want
+    q = torch.zeros(shape, dtype=torch.float8_e4m3fn)
+    s = torch.zeros(shape[:-1] + (0,))
+    want = _raised(lambda: torch_ref.dequantize_tensor(q, s, block_size))
+    assert want is not None and want[0] is RuntimeError
+    assert _raised(lambda: wq.dequantize_tensor(q, s, block_size)) == want
+
+
+def test_zero_width_state_dict_entry_raises_as_the_reference():
+    """A [N, 0] float weight passes quantize_state_dict's `in_features % 128`
+    rule (:105) and raises in quantize_tensor (:109); a [N, 0] codes entry with
+    its sidecar raises in dequantize_tensor (:132).  Both before any device work."""
+    from oracle import torch_ref
+
+    wq = WeightQuantizer(FP8Config())
+    sd = {"step": 1, "w": torch.zeros(4, 0)}
+    want = _raised(lambda: torch_ref.quantize_state_dict(sd))
+    assert want is not None and want[0] is RuntimeError
+    assert _raised(lambda: wq.quantize_state_dict(sd)) == want
+    qsd = {"w": torch.zeros(4, 0, dtype=torch.float8_e4m3fn), "w_fp8_scales": torch.zeros(4, 0)}
+    want = _raised(lambda: torch_ref.dequantize_state_dict(qsd))
+    assert want is not None and want[0] is RuntimeError
+    assert _raised(lambda: wq.dequantize_state_dict(qsd)) == want
+
+
+@pytest.mark.skipif(torch.cuda.is_available(), reason="checks the no-device failure")
+def test_zero_rows_stay_valid_without_reaching_unfold_errors():
+    """[0, K] is a valid input in the reference; the drop-in gets past the
+    unfold checks to its device requirement (no device here)."""
+    wq = WeightQuantizer(FP8Config())
+    with pytest.raises(RuntimeError, match="HIP device"):
+        wq.quantize_tensor(torch.zeros(0, 256))
+
+
 @pytest.mark.skipif(torch.cuda.is_available(), reason="checks the no-device failure")
 def test_no_device_fails_loudly():
     wq = WeightQuantizer(FP8Config())
