@@ -256,8 +256,11 @@ int lrq_tensor_scale_grouped(const void* host_table, const void* device_table, v
  *     one stream are safe (every partial is written before it is read); calls
  *     that overlap on one device (different streams, or threads without
  *     ordering) race and may return wrong scales.
- *   - The array's address is looked up once per device, on the first call
- *     that runs there.
+ *   - The array's address is looked up once per device, when
+ *     lrq_group_build_map() sets up a tensor-scale table there (or on the
+ *     first call on a device no such table was set up on).  A call captured
+ *     into a HIP graph after that set-up makes no runtime call beyond
+ *     hipStreamGetDevice and its two kernel launches.
  */
 #define LRQ_STATIC_WORKSPACE_BYTES (4u << 20)
 int lrq_tensor_scale_grouped_static(const void* host_table, const void* device_table,

@@ -43,10 +43,10 @@ constexpr uint32_t kMagic = 0x4C525154u;  // "LRQT"
 constexpr uint32_t kTableVersion = 4u;  // 4: LaunchCfg gained `pitched` and `chunk`
 // HIP takes a launch's thread count (work-groups x threads per work-group) as
 // a 32-bit value.  kMaxGrid is the limit for 256-thread work-groups;
-// max_units() gives it per kernel.
+// max_units() gives it for the work-group size of the launch `cfg` selects.
 constexpr int64_t kMaxGrid = 0xFFFFFFFFll / 256;
-int64_t max_units(int kernel) {
-  return 0xFFFFFFFFll / (kernel == lrq::kKernTile128 || kernel == lrq::kKernF64Tile ? lrq::kTileThreads : 256);
+int64_t max_units(const LaunchCfg& cfg) {
+  return 0xFFFFFFFFll / lrq::wg_threads(cfg.kernel, cfg.in_dtype, cfg.blk_c);
 }
 
 // Table layout, host and device alike: [header | n descriptors | map].  The
@@ -292,7 +292,7 @@ int run_single(const LaunchCfg& cfg, Desc& d, hipStream_t stream) {
   if (!lrq::plan_units(cfg, d))
     return fail(LRQ_ERR_ARG, "batch stride must equal rows*ld for this format");
   if (d.units == 0) return 0;
-  if (d.units > max_units(cfg.kernel)) return fail(LRQ_ERR_ARG, "tensor too large for one launch");
+  if (d.units > max_units(cfg)) return fail(LRQ_ERR_ARG, "tensor too large for one launch");
   d.unit0 = 0;
   return check_hip(lrq::launch(cfg, d, nullptr, nullptr, d.units, stream), "kernel launch");
 }
@@ -500,7 +500,7 @@ int plan_group(int fmt, const lrq_tensor* ts, int64_t n, int in_dtype, int64_t b
     for (int64_t i = 0; i < n; ++i)
       if (ts[i].cols % blk_c != 0) cfg.rows_dense = 0;
   }
-  if (limit && units > max_units(cfg.kernel)) return fail(LRQ_ERR_ARG, "group too large for one launch");
+  if (limit && units > max_units(cfg)) return fail(LRQ_ERR_ARG, "group too large for one launch");
   *cfg_out = cfg;
   *units_out = units;
   return 0;
@@ -522,7 +522,7 @@ int lrq_fp8_block_quant(const void* in, int in_dtype, int64_t batch, int64_t row
                           /*limit=*/false))
     return rc;
   if (units == 0) return 0;
-  if (units > max_units(cfg.kernel)) {
+  if (units > max_units(cfg)) {
     // More work-groups than one launch takes (small blocks on the one-block-per-
     // work-group generic kernel): one launch per matrix, then per band of rows
     // (whole block rows), each re-planned on its own.
@@ -541,7 +541,7 @@ int lrq_fp8_block_quant(const void* in, int in_dtype, int64_t batch, int64_t row
           return rc;
       return 0;
     }
-    const int64_t parts = units / max_units(cfg.kernel) + 2;
+    const int64_t parts = units / max_units(cfg) + 2;
     const int64_t band = (srows + parts - 1) / parts * blk_r;  // rows per launch
     if (band >= rows) return fail(LRQ_ERR_ARG, "one row of blocks exceeds a launch");
     for (int64_t r0 = 0; r0 < rows; r0 += band) {
@@ -695,6 +695,17 @@ int lrq_group_build_map(const void* host_table, void* device_table, lrq_stream_t
   memcpy(&h, host_table, sizeof(h));
   if (h.magic != kMagic || h.version != kTableVersion) return fail(LRQ_ERR_TABLE, "not an lrq table");
   if (!aligned(device_table, 256)) return fail(LRQ_ERR_ALIGN, "device table must be 256-byte aligned");
+  if (h.cfg.kernel == lrq::kKernAmax) {
+    // Set-up of a tensor-scale table: look up the static workspace's device
+    // address now, so lrq_tensor_scale_grouped_static makes no symbol lookup
+    // (a runtime call that is not a stream operation) when a caller captures it.
+    int d = -1;
+    if (int rc = check_hip(stream ? hipStreamGetDevice((hipStream_t)stream, &d) : hipGetDevice(&d),
+                           "device of the stream"))
+      return rc;
+    uint32_t* ws = nullptr;
+    if (int rc = check_hip(lrq::static_workspace(d, &ws), "static workspace address")) return rc;
+  }
   if (h.units == 0) return 0;
   char* dev = static_cast<char*>(device_table);
   const int64_t grid = (h.units + 255) / 256;

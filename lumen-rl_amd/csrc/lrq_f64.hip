@@ -385,7 +385,7 @@ __global__ __launch_bounds__(512) void k_tile_f64(Desc single, const Desc* __res
   __shared__ uint64_t red[8];
   Desc d;
   int64_t u;
-  pick_desc<kXcdRunTile>(single, descs, map, d, u);
+  pick_desc<kXcdRunTileF64>(single, descs, map, d, u);
   const int64_t per = d.units_r * d.units_c;
   const int64_t b = u / per;
   const int64_t rem = u - b * per;
@@ -611,14 +611,16 @@ hipError_t launch_f64(const LaunchCfg& cfg, const Desc& single, const Desc* desc
       case 4: hipLaunchKernelGGL((k_row_wide_f64<1, 4>), grid, block, 0, stream, single, descs, map, cfg.pow2, bw); break;
       case 2: hipLaunchKernelGGL((k_row_wide_f64<1, 2>), grid, block, 0, stream, single, descs, map, cfg.pow2, bw); break;
       case 1: hipLaunchKernelGGL((k_row_wide_f64<1, 1>), grid, block, 0, stream, single, descs, map, cfg.pow2, bw); break;
-      default:
-        if (cfg.blk_c <= 4096)
-          hipLaunchKernelGGL((k_row_wide_f64<4, 1>), grid, block, 0, stream, single, descs, map, cfg.pow2, bw);
-        else if (cfg.blk_c <= 8192)
-          hipLaunchKernelGGL((k_row_wide_f64<8, 1>), grid, dim3(512), 0, stream, single, descs, map, cfg.pow2, bw);
+      default: {  // one block of W = threads / 64 waves
+        const dim3 wg(wg_threads(kKernF64Wide, kF64, cfg.blk_c));
+        if (wg.x == 256)
+          hipLaunchKernelGGL((k_row_wide_f64<4, 1>), grid, wg, 0, stream, single, descs, map, cfg.pow2, bw);
+        else if (wg.x == 512)
+          hipLaunchKernelGGL((k_row_wide_f64<8, 1>), grid, wg, 0, stream, single, descs, map, cfg.pow2, bw);
         else
-          hipLaunchKernelGGL((k_row_wide_f64<16, 1>), grid, dim3(1024), 0, stream, single, descs, map, cfg.pow2, bw);
+          hipLaunchKernelGGL((k_row_wide_f64<16, 1>), grid, wg, 0, stream, single, descs, map, cfg.pow2, bw);
         break;
+      }
     }
     return hipGetLastError();
   }

@@ -602,7 +602,7 @@ static hipError_t launch_fp8_typed(const LaunchCfg& cfg, const Desc& single, con
       const int g = (int)cfg.blk_c;  // the block width
       const WideShape ws = wide_shape(DT, cfg.blk_c);
 #define LRQ_WIDE(W, P, NC)                                                                         \
-  hipLaunchKernelGGL((k_row_wide<DT, CDT, W, P, NC>), grid, dim3(W > 4 ? 64 * W : 256), 0, stream, single, \
+  hipLaunchKernelGGL((k_row_wide<DT, CDT, W, P, NC>), grid, dim3(wg_threads(kKernRowWide, DT, cfg.blk_c)), 0, stream, single, \
                      descs, map, cfg.pow2, cfg.scale_bf16, g)
       if (ws.nc == kWideChunks) {
         if (ws.w == 16) LRQ_WIDE(16, 1, kWideChunks);

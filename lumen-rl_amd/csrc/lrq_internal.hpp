@@ -81,7 +81,15 @@ constexpr int kTileThreads = 512;    // k_tile128: threads per 128x128 tile (512
 constexpr int kRowBlocks = 4;        // k_row: wave instructions per lane, one 1xB block each up to B = 512, sharing
                                      // one scale computation (4: 2 is 7% slower with bf16 scales, 3 slower with both)
 // XCD run length (xcd_unit) per kernel, in work units; sweeps over 8..128:
-constexpr int64_t kXcdRunTile = 32;    // k_tile128: 32 tiles = 1 MiB of bf16 (16 and 8 lose 6-7%, 64 and 128 1%)
+// k_tile128: runs of 4 tiles, so the 8 XCDs share every 32-tile group (one
+// 8 KiB row span of a K = 4096 band) and XCD x always reads its own 1 KiB
+// column slice of it (address bits 10-12 == x for 8 KiB-aligned rows).  Against
+// runs of 32 (whole K = 4096 bands per XCD): C2 80.1-80.9 % of 8 TB/s from
+// 77.6-79.2 %, its 36 down_proj (K = 12288) 81 % from 77-78 %, single 2 GiB
+// weights 81.4-82 % at K = 4096 and 12288; runs of 2, 6, 8 and 16 lose 5-10
+// points on C2.
+constexpr int64_t kXcdRunTile = 4;
+constexpr int64_t kXcdRunTileF64 = 32;  // k_tile_f64: 32 tiles (128 KiB each)
 constexpr int64_t kXcdRunRow = 16;     // k_row: 256 KiB of bf16 (32 loses 2%)
 constexpr int64_t kXcdRunMx = 64;      // k_mx: 512 KiB of bf16 (32 loses 2.5%, 128 ties)
 constexpr int64_t kXcdRunStream = 32;  // dequant, act, amax, copy, cast, generic kernels
@@ -106,6 +114,21 @@ constexpr int f64_pad_lanes(int64_t blk_c) {
   int l = 4;
   while (2 * l < blk_c) l *= 2;
   return l;
+}
+
+// Threads per work-group of `kernel` for 1xB blocks of width blk_c: 512 for
+// the tile kernels, 64 W for k_row_wide's 8- and 16-wave blocks, 512 or 1024
+// for k_row_wide_f64's blocks past 4096, else 256.  The launch code uses the
+// same rule, and the C ABI sizes its 32-bit thread-count guard by it.
+constexpr int wg_threads(int kernel, int in_dtype, int64_t blk_c) {
+  if (kernel == kKernTile128 || kernel == kKernF64Tile) return kTileThreads;
+  if (kernel == kKernRowWide) {
+    const WideShape ws = wide_shape(in_dtype, blk_c);
+    return ws.w > 4 ? 64 * ws.w : 256;
+  }
+  if (kernel == kKernF64Wide && f64_pad_lanes(blk_c) == 0 && f64_wide_blocks_per_wave(blk_c) == 0)
+    return blk_c <= 4096 ? 256 : blk_c <= 8192 ? 512 : 1024;
+  return 256;
 }
 
 // Descriptor and local work unit of this work-group: the single-tensor

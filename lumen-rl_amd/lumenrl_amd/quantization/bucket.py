@@ -83,6 +83,12 @@ class Bucket:
         self._plan_copies()
 
     def _plan_copies(self) -> None:
+        old = getattr(self, "copy_plan", None)
+        if old is not None and old._launch.captured:
+            # a captured fill() keeps the copy table's address: it must not be freed
+            raise RuntimeError("Bucket: a fill() of this bucket was captured into a HIP graph, which "
+                               "keeps its copy table; a pass-through tensor now lives in other "
+                               "storage, so build (and capture) a new writer instead")
         pairs, self._loose = [], []
         for e in self.copies:
             dst = self.buffer[e.offset:e.offset + e.nbytes]

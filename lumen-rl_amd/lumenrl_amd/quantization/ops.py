@@ -361,6 +361,9 @@ class _GroupLaunch:
         self.device = device
         self.units = int(L.lrq_group_units(self.host.data_ptr()))
         self.buffers: list[Tensor] = [self.dev]  # device memory the launches touch
+        # Set once a run is recorded into a HIP graph: the graph holds this
+        # table's device address, so the table must live and stay unchanged.
+        self.captured = False
 
     def _enter(self) -> None:
         """Order a launch on another stream after the table upload, and tell the
@@ -378,6 +381,7 @@ class _GroupLaunch:
     def run(self) -> None:
         with _on(self.device):
             self._enter()
+            self.captured |= torch.cuda.is_current_stream_capturing()
             rc = _lib.lib().lrq_quant_grouped(self.host.data_ptr(), self.dev.data_ptr(),
                                               _stream(self.device))
         _lib.check(rc, "lrq_quant_grouped")
@@ -388,6 +392,7 @@ class _GroupLaunch:
     def run_tensor_scale(self, workspace: Tensor) -> None:
         with _on(self.device):
             self._enter()
+            self.captured |= torch.cuda.is_current_stream_capturing()
             rc = _lib.lib().lrq_tensor_scale_grouped(self.host.data_ptr(), self.dev.data_ptr(),
                                                      workspace.data_ptr(), _nbytes(workspace),
                                                      _stream(self.device))
@@ -396,6 +401,7 @@ class _GroupLaunch:
     def run_tensor_scale_static(self) -> None:
         with _on(self.device):
             self._enter()
+            self.captured |= torch.cuda.is_current_stream_capturing()
             rc = _lib.lib().lrq_tensor_scale_grouped_static(self.host.data_ptr(), self.dev.data_ptr(),
                                                             _stream(self.device))
         _lib.check(rc, "lrq_tensor_scale_grouped_static")
@@ -660,7 +666,16 @@ class QuantPlan:
         self._bind(list(tensors))
 
     def _bind(self, tensors: list[Tensor]) -> None:
-        """Pack and upload the descriptor table for the tensors' current storage."""
+        """Pack and upload the descriptor table for the tensors' current storage.
+
+        Refused once a run of this plan was captured into a HIP graph: the graph
+        keeps the current table's address and the old inputs' pointers, so
+        replacing (and freeing) the table would leave it reading freed memory."""
+        launch = getattr(self, "_launch", None)
+        if launch is not None and launch.captured:
+            raise RuntimeError("QuantPlan: a run of this plan was captured into a HIP graph, which "
+                               "keeps its descriptor table; its inputs now live in other storage, so "
+                               "build (and capture) a new plan instead of re-binding this one")
         descs = (_lib.LrqTensor * len(tensors))()
         views = []
         for i, (t, (codes, scales)) in enumerate(zip(tensors, self.outputs)):

@@ -476,3 +476,29 @@ def test_fp8_dequant_chunk_per_width():
     assert units(1152, 128, False) == -(-n // 4 // 512)
     assert units(1152, 36, False) == -(-n // 4 // 512)
     assert units(1152, 6, True) == -(-n // 256)
+
+
+@pytest.mark.parametrize("dtype,blk_c,threads", [(0, 32768, 512), (0, 65536, 1024), (2, 65536, 1024),
+                                                 (3, 8192, 512), (3, 16384, 1024), (0, 16384, 256)])
+def test_group_limit_counts_the_wide_kernels_work_group_size(dtype, blk_c, threads):
+    """HIP takes a launch's thread count as 32 bits.  k_row_wide runs 512- or
+    1024-thread work-groups for its widest 1xB blocks (one block each) and
+    k_row_wide_f64 for float64 blocks past 4096, so a grouped table may hold at
+    most 0xFFFFFFFF // threads of them; one block more is refused at pack time,
+    before any device work (fake device pointers)."""
+    flags = _lib.FLAG_NATIVE_ARITH if dtype == 3 else 0
+    limit = 0xFFFFFFFF // threads
+
+    def pack(rows):
+        ts = _tensors([(1, rows, blk_c)])
+        need = L().lrq_group_table_bytes(_lib.FMT_FP8_BLOCK, ts, 1, dtype, 1, blk_c, flags)
+        if need < 0:
+            return need, None
+        buf = np.zeros(need, np.uint8)
+        return L().lrq_group_pack(_lib.FMT_FP8_BLOCK, ts, 1, dtype, 1, blk_c, flags, buf.ctypes.data, need), buf
+
+    rc, buf = pack(limit)
+    assert rc == 0, _lib.last_error()
+    assert L().lrq_group_units(buf.ctypes.data) == limit
+    rc, _ = pack(limit + 1)
+    assert rc == _lib.ERR_ARG and "too large" in _lib.last_error()

@@ -311,6 +311,27 @@ def test_rollout_quantizer_patch_and_restore():
         assert torch.equal(net(x), y0)
 
 
+def test_quantize_model_skips_a_failing_layer_and_patches_the_rest(caplog):
+    """One weight that cannot be quantized (a meta tensor) makes the grouped
+    batch raise; quantize_model then quantizes layer by layer, so that layer is
+    skipped with the reference's warning (fp8_rollout.py:130-136) and every
+    other eligible linear is patched with the reference's buffers."""
+    torch.manual_seed(11)
+    net = nn.Sequential(nn.Linear(256, 384), nn.Linear(384, 256), nn.Linear(256, 512)).to(DEV, torch.bfloat16)
+    net[1] = nn.Linear(384, 256, device="meta", dtype=torch.bfloat16)
+    rq = FP8RolloutQuantizer(FP8Config(precision="fp8"))
+    with caplog.at_level("WARNING"):
+        rq.quantize_model(net)
+    assert any("Failed to FP8-wrap 1" in r.getMessage() for r in caplog.records)
+    assert isinstance(net[1], nn.Linear)
+    for i in (0, 2):
+        m = net[i]
+        assert isinstance(m, _FP8W8A8Linear), i
+        q, s = T.quantize_tensor(rq._originals[str(i)].weight.data.cpu().float(), 128, False)
+        assert torch.equal(m.weight_fp8.cpu().view(torch.uint8), q.view(torch.uint8))
+        assert torch.equal(m.weight_scale.cpu().view(torch.int16), s.to(torch.bfloat16).view(torch.int16))
+
+
 def test_quantize_model_grouped_weights_equal_the_reference_ops():
     """quantize_model's grouped launches give every patched module the buffers of
     the reference's per-layer quantize_tensor (float32 upcast, bf16 scales), for

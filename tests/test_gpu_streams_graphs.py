@@ -123,6 +123,52 @@ def test_plan_built_under_capture_is_refused():
     assert torch.all(plan.outputs[0][0].view(torch.uint8) == 0)
 
 
+@pytest.mark.filterwarnings("ignore:The CUDA Graph is empty")
+def test_rebind_after_capture_is_refused():
+    """A captured run keeps the plan's descriptor table (the graph holds its
+    address).  Moving an input to other storage afterwards raises instead of
+    replacing and freeing that table; the stale graph is never replayed on the
+    moved input, and it still replays correctly on the planned inputs.  The
+    same holds for a transfer bucket's pass-through copy table."""
+    from lumenrl_amd.quantization import QuantizedBucketWriter
+
+    gen = torch.Generator(device=DEV).manual_seed(8)
+    ws = _layer(gen)
+    plan = QuantPlan(ws, "fp8_block", (128, 128))
+    norm = torch.ones(1024, dtype=torch.bfloat16, device=DEV)
+    named = [("l.q_proj.weight", ws[0]), ("l.input_layernorm.weight", norm)]
+    writer = QuantizedBucketWriter(named, bucket_bytes=4 << 20, fmt="fp8_block")
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):  # warm-up outside the capture
+        plan.run()
+        for b in writer:
+            b.fill()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        plan.run()
+        for b in writer:
+            b.fill()
+    table = plan._launch
+    moved = ws[1].clone()  # the same values in other storage
+    with pytest.raises(RuntimeError, match="captured into a HIP graph"):
+        plan.run([ws[0], moved, ws[2]])
+    assert plan._launch is table and plan.inputs[1] is ws[1]
+    norm.data = torch.full((1024,), 0.5, dtype=torch.bfloat16, device=DEV)  # a p.data swap
+    bucket = next(iter(writer))
+    with pytest.raises(RuntimeError, match="captured into a HIP graph"):
+        bucket.fill()
+    torch.cuda.synchronize()
+    for w in ws:
+        w.copy_((torch.randn(w.shape, generator=gen, device=DEV) * 0.03).to(w.dtype))
+    torch.cuda.synchronize()
+    graph.replay()
+    torch.cuda.synchronize()
+    _check_fp8_tiles(ws, plan.outputs)
+
+
 def test_random_shape_sweep():
     """Seeded random shapes, strides, dtypes and blocks through every kernel family."""
     rng = np.random.default_rng(2026)

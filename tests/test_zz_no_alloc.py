@@ -102,3 +102,34 @@ def test_static_rejects_oversized_table_before_device_work():
     assert L.lrq_group_workspace_bytes(host) > _lib.STATIC_WORKSPACE_BYTES
     rc = L.lrq_tensor_scale_grouped_static(host, ctypes.c_void_p(fake), None)
     assert rc == _lib.ERR_CAPACITY and "static workspace" in _lib.last_error()
+
+
+def test_static_entry_point_under_graph_capture():
+    """The use case the entry point exists for: a HIP graph that captures it.
+    The static workspace's address is looked up when the plan's table is set up
+    (lrq_group_build_map), so the capture records only the two launches; the
+    graph is replayed after eager changes to the weights, each replay checked
+    bit for bit against the caller-workspace entry point run eagerly."""
+    ws = weights([(1024, 4096), (256, 4096), (512, 2048)], torch.bfloat16, specials=False)
+    plan = TensorScalePlan(ws)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    say("[no_alloc] capture run_static")
+    with torch.cuda.graph(graph):  # no eager run_static before: capture is its first call here
+        plan.run_static()
+    for rep in range(3):
+        for i, w in enumerate(ws):
+            w.copy_(torch.from_numpy((RNG.standard_normal(tuple(w.shape)) * 0.01 * (rep + i + 1))
+                                     .astype(np.float32)).to(w.dtype).to(DEV))
+        if rep == 1:
+            ws[2][7, 9] = float("nan")
+        plan.scales.fill_(-1.0)
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        got = bits(plan.scales).copy()
+        plan.scales.fill_(-2.0)
+        ref = bits(plan.run())
+        torch.cuda.synchronize()
+        say("[no_alloc] replay", rep)
+        assert np.array_equal(got, ref), rep
