@@ -39,7 +39,10 @@ already resident in HBM:
        its own buffer.
 
 Prints ONE JSON line on stdout.  value = algorithmic bytes (bf16 in + codes +
-scales) per step / step time, in GB/s (1e9 B/s).  The roofline object uses the
+scales) per step / step time, in GB/s (1e9 B/s).  With --config c2 (the
+default) the line also carries `also`: c3, c4 and c5 timed on the device the
+same way after c2's set is freed (ms_per_step, step GB/s, kernel GB/s and its
+fraction of 8 TB/s; no CPU leg; --no-also skips them).  The roofline object uses the
 same bytes over the kernel's average launch time from HIP events on the launch
 stream.  cpu_baseline times the reference's op sequence in torch on the host
 CPU (oracle/torch_ref.py) over a bounded sample of the same weights.
@@ -425,21 +428,10 @@ class _ActLayer:
             self.ops.act_qdq(x, 128, out=out)
 
 
-# ---------------------------------------------------------------------------
-def run(args):
-    import torch
-
-    from lumenrl_amd.quantization import ops
-
-    if not torch.cuda.is_available():
-        log("bench.py needs a HIP device")
-        sys.exit(2)
-    dev = torch.device("cuda", 0)
-    torch.cuda.set_device(dev)
-    stream = torch.cuda.current_stream(dev)
-    cfg = args.config
-    t0 = time.time()
-
+def setup(torch, ops, cfg, args, dev):
+    """The workload of one config, resident on the device: plans (each with
+    run() and algorithmic_bytes), the input tensors, and what the JSON line and
+    the CPU leg need."""
     flush = None
     if cfg == "c2d":
         ws, _ = qwen3_8b_set(torch, dev, args.seed, "normal")
@@ -584,11 +576,16 @@ def run(args):
                  "launches_per_step": 48}
     else:
         raise SystemExit(f"unknown config {cfg}")
-    torch.cuda.synchronize()
-    step_bytes = sum(p.algorithmic_bytes for p in plans)
-    log(f"[bench] {workload}: {len(ws)} tensors, {step_bytes / 1e9:.3f} GB per step, "
-        f"setup {time.time() - t0:.1f}s")
+    return {"plans": plans, "ws": ws, "workload": workload, "extra": extra, "flush": flush,
+            "cpu": (cpu_ws, cpu_blk, cpu_fmt)}
 
+
+def measure(torch, ops, plans, flush, args, stream):
+    """Time exactly args.steps steps (after args.warmup untimed ones) of the
+    plans, bracketed by synchronizations, with HIP events on the launch stream
+    around every launch.  ms_per_step is the wall time per step (the launches'
+    summed event time when an L2 flush separates them); kern_ms is the mean
+    event time of one launch and `achieved` its algorithmic GB/s."""
     # A drop-in call (quantize_state_dict, load_weights) plans on the host
     # before and between its grouped launches.  Its kernel time spans its first
     # launch to the end of its last (the small table uploads between launches
@@ -653,6 +650,38 @@ def run(args):
         ms_per_step = wall * 1e3 / args.steps
     else:  # the L2 flush between launches is not part of the step
         ms_per_step = sum(launch_ms) / args.steps
+    ops._GroupLaunch.run = base_run
+    return {"ms_per_step": ms_per_step, "median_step_ms": median_step_ms, "kern_ms": kern_ms,
+            "achieved": achieved}
+
+
+
+# ---------------------------------------------------------------------------
+def run(args):
+    import torch
+
+    from lumenrl_amd.quantization import ops
+
+    if not torch.cuda.is_available():
+        log("bench.py needs a HIP device")
+        sys.exit(2)
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    stream = torch.cuda.current_stream(dev)
+    cfg = args.config
+    t0 = time.time()
+
+    w = setup(torch, ops, cfg, args, dev)
+    plans, ws, workload, extra, flush = w["plans"], w["ws"], w["workload"], w["extra"], w["flush"]
+    cpu_ws, cpu_blk, cpu_fmt = w["cpu"]
+    torch.cuda.synchronize()
+    step_bytes = sum(p.algorithmic_bytes for p in plans)
+    log(f"[bench] {workload}: {len(ws)} tensors, {step_bytes / 1e9:.3f} GB per step, "
+        f"setup {time.time() - t0:.1f}s")
+
+    r = measure(torch, ops, plans, flush, args, stream)
+    ms_per_step, median_step_ms, kern_ms, achieved = (r["ms_per_step"], r["median_step_ms"], r["kern_ms"],
+                                                      r["achieved"])
     value = step_bytes / (ms_per_step * 1e-3) / 1e9
     log(f"[bench] {ms_per_step:.4f} ms/step, {value:.1f} GB/s; kernel avg {kern_ms:.4f} ms "
         f"({achieved:.1f} GB/s = {achieved / HBM_PEAK_GBS:.1%} of 8 TB/s)")
@@ -698,7 +727,40 @@ def run(args):
         log("[bench] cpu baseline ...")
         result["cpu_baseline"] = cpu_baseline(torch, cpu_ws, cpu_fmt, cpu_blk, args.cpu_seconds,
                                               full_bytes=step_bytes)
+    if cfg == "c2" and not args.no_also:
+        del w, plans, ws, cpu_ws
+        result["also"] = also_configs(torch, ops, args, dev, stream)
     print(json.dumps(result), flush=True)
+
+
+ALSO = ("c3", "c4", "c5")
+
+
+def also_configs(torch, ops, args, dev, stream):
+    """The other BASELINE.json quantization configs timed on the device the
+    same way (HIP events around every launch, args.steps steps after
+    args.warmup), each set freed before the next is built: C3's 48 per-layer
+    expert launches, C4 (MXFP8) and C5 (MXFP4) on the whole Qwen3-8B set.
+    No CPU leg."""
+    out = {}
+    for c in ALSO:
+        torch.cuda.empty_cache()
+        t0 = time.time()
+        w = setup(torch, ops, c, args, dev)
+        torch.cuda.synchronize()
+        nb = sum(p.algorithmic_bytes for p in w["plans"])
+        r = measure(torch, ops, w["plans"], w["flush"], args, stream)
+        out[c] = {"workload": w["workload"], "kernel": KERNEL_FOR[c],
+                  "launches_per_step": w["extra"]["launches_per_step"],
+                  "algorithmic_bytes_per_step": nb, "ms_per_step": round(r["ms_per_step"], 5),
+                  "value": round(nb / (r["ms_per_step"] * 1e-3) / 1e9, 2),
+                  "achieved": round(r["achieved"], 2), "frac": round(r["achieved"] / HBM_PEAK_GBS, 4),
+                  "launch_ms": round(r["kern_ms"], 5)}
+        log(f"[bench] also {c} ({w['workload']}): {r['ms_per_step']:.4f} ms/step, kernel "
+            f"{r['achieved']:.1f} GB/s = {r['achieved'] / HBM_PEAK_GBS:.1%}, setup {time.time() - t0:.1f}s")
+        del w
+    torch.cuda.empty_cache()
+    return out
 
 
 def run_host(args):
@@ -832,6 +894,8 @@ def main():
     ap.add_argument("--seed", type=int, default=1000)
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-also", action="store_true",
+                    help="with --config c2: skip the C3/C4/C5 device timings of the `also` object")
     ap.add_argument("--mode", default="quant", choices=["quant", "copy"])
     ap.add_argument("--copy-bytes", type=int, default=1 << 30)
     args = ap.parse_args()
