@@ -6,7 +6,8 @@ already resident in HBM:
 
   c2 (default, the metric's config): the full Qwen3-8B linear set, 36 layers x
      {q,k,v,o,gate,up,down}, bf16 N(0, 0.02^2) with 0.1% +-U(0.5, 4) outliers,
-     -> FP8 E4M3 with one fp32 scale per 128x128 tile, ONE grouped launch.
+     -> FP8 E4M3 with one fp32 scale per 128x128 tile: one grouped plan, run as
+     7 launches of consecutive tensors (~3 GiB of bytes each).
   c1: one [4096, 4096] weight, 128x128 (L2/MALL flushed between launches).
   c3: Qwen3-30B-A3B experts, 48 layers x 128 experts (gate_up [E,1536,2048],
       down [E,2048,768]) with one zero and one inf tile per layer; one launch
@@ -17,7 +18,7 @@ already resident in HBM:
   c2pc: c2 weights with per-channel scales (1xK blocks: quantize_tensor with
        block_size = in_features), one grouped launch per row width.
   c2d: dequantize_state_dict of the c2r result: e4m3 codes + bf16 1x128 scales ->
-       bf16 weights, ONE grouped launch.
+       bf16 weights, one grouped plan.
   c2sd: the drop-in WeightQuantizer.quantize_state_dict on the c2 weights held
        in a device state dict (1x128 blocks, bf16 `_fp8_scales` sidecar, new
        outputs every call): the API path end to end, host work included.
@@ -43,8 +44,8 @@ scales) per step / step time, in GB/s (1e9 B/s).  With --config c2 (the
 default) the line also carries `also`: c3, c4 and c5 timed on the device the
 same way after c2's set is freed (ms_per_step, step GB/s, kernel GB/s and its
 fraction of 8 TB/s; no CPU leg; --no-also skips them).  The roofline object uses the
-same bytes over the kernel's average launch time from HIP events on the launch
-stream.  cpu_baseline times the reference's op sequence in torch on the host
+same bytes over the step's kernel time (`launch_ms`: HIP events on the launch
+stream around each plan's launches).  cpu_baseline times the reference's op sequence in torch on the host
 CPU (oracle/torch_ref.py) over a bounded sample of the same weights.
 """
 
@@ -428,6 +429,12 @@ class _ActLayer:
             self.ops.act_qdq(x, 128, out=out)
 
 
+def _launches(plans) -> int:
+    """Kernel launches one step of these grouped plans makes (a plan over many
+    tensors runs as several launches of consecutive tensors)."""
+    return sum(len(p._launch.parts) for p in plans)
+
+
 def setup(torch, ops, cfg, args, dev):
     """The workload of one config, resident on the device: plans (each with
     run() and algorithmic_bytes), the input tensors, and what the JSON line and
@@ -442,7 +449,7 @@ def setup(torch, ops, cfg, args, dev):
         workload = "qwen3-8b-linears-fp8-1x128-dequant-to-bf16"
         cpu_ws, cpu_blk, cpu_fmt = pairs, (1, 128), "fp8_dequant"
         extra = {"tensors": len(pairs), "layers": 36, "elements": sum(c.numel() for c, _ in pairs),
-                 "format": "fp8_dequant", "launches_per_step": 1}
+                 "format": "fp8_dequant", "launches_per_step": _launches(plans)}
     elif cfg == "c4d":
         ws, _ = qwen3_8b_set(torch, dev, args.seed, "student_t")
         qp = ops.QuantPlan(ws, "mxfp8", (1, 32))
@@ -454,7 +461,7 @@ def setup(torch, ops, cfg, args, dev):
         workload = "qwen3-8b-linears-mxfp8-dequant-to-bf16"
         cpu_ws, cpu_blk, cpu_fmt = pairs, (1, 32), "mx_dequant"
         extra = {"tensors": len(pairs), "layers": 36, "elements": sum(c.numel() for c, _ in pairs),
-                 "format": "mxfp8_dequant", "launches_per_step": 1}
+                 "format": "mxfp8_dequant", "launches_per_step": _launches(plans)}
     elif cfg in ("c2", "c4", "c5", "c2r"):
         kind = {"c2": "normal", "c4": "student_t", "c5": "rowscale", "c2r": "normal"}[cfg]
         fmt = {"c2": "fp8_block", "c4": "mxfp8", "c5": "mxfp4", "c2r": "fp8_block"}[cfg]
@@ -465,7 +472,7 @@ def setup(torch, ops, cfg, args, dev):
                     "c5": "qwen3-8b-linears-mxfp4", "c2r": "qwen3-8b-linears-fp8-e4m3-1x128"}[cfg]
         cpu_ws, cpu_blk, cpu_fmt = ws, blk, fmt
         extra = {"tensors": len(ws), "layers": 36, "elements": sum(w.numel() for w in ws),
-                 "format": fmt, "launches_per_step": 1}
+                 "format": fmt, "launches_per_step": _launches(plans)}
     elif cfg == "c2pc":
         # per-channel scales, quantize_tensor(w, block_size=in_features): one
         # grouped launch per row width (1x4096 for six projections, 1x12288

@@ -407,6 +407,58 @@ class _GroupLaunch:
         _lib.check(rc, "lrq_tensor_scale_grouped_static")
 
 
+# A grouped plan over many tensors runs as several launches of consecutive
+# tensors, each about this many algorithmic bytes (2 GiB of bf16 input for a
+# quantization).  On an MI355X the Qwen3-8B set (252 tensors, 20.8 GB) ran
+# 1-2 points of the HBM peak faster in 5-7 such launches than in one: 128x128
+# 81.5-81.8 % -> 82.5-82.7 %, 1x128 83.0 % -> 85.0 %, MXFP8 84.1 % -> 84.8 %
+# (14 launches: 82.0 %, 36: 79.6 %).  Splitting one 4 GiB tensor into row bands
+# gained nothing, so a tensor is never split.
+GROUP_LAUNCH_BYTES = 3 << 30
+
+
+def launch_ranges(sizes: Sequence[int], limit: Optional[int] = None) -> list[tuple[int, int]]:
+    """Consecutive ``[i, j)`` ranges of ``sizes`` (algorithmic bytes per tensor)
+    whose sums stay within ``limit`` (default ``GROUP_LAUNCH_BYTES``); a tensor
+    larger than the limit is a range of its own.  Every index is covered once,
+    in order."""
+    limit = GROUP_LAUNCH_BYTES if limit is None else limit
+    out, i, acc = [], 0, 0
+    for j, n in enumerate(sizes):
+        if j > i and acc + n > limit:
+            out.append((i, j))
+            i, acc = j, 0
+        acc += n
+    if i < len(sizes):
+        out.append((i, len(sizes)))
+    return out
+
+
+class _GroupLaunches:
+    """A plan's grouped launches: its tensors split by ``launch_ranges`` into
+    consecutive runs, each with its own table, run in order on the caller's
+    stream.  ``buffers[k]`` lists tensor k's plan-owned device buffers."""
+
+    def __init__(self, fmt: str, descs, sizes: Sequence[int], in_dtype: int, block: tuple[int, int],
+                 flags: int, device: torch.device, buffers: Optional[Sequence[Sequence[Tensor]]] = None) -> None:
+        self.parts: list[_GroupLaunch] = []
+        for i, j in launch_ranges(sizes):
+            sub = (_lib.LrqTensor * (j - i))(*descs[i:j])
+            part = _GroupLaunch(fmt, sub, j - i, in_dtype, block, flags, device)
+            if buffers is not None:
+                part.buffers += [b for k in range(i, j) for b in buffers[k]]
+            self.parts.append(part)
+        self.units = sum(p.units for p in self.parts)
+
+    @property
+    def captured(self) -> bool:
+        return any(p.captured for p in self.parts)
+
+    def run(self) -> None:
+        for p in self.parts:
+            p.run()
+
+
 class ChunkedLaunches:
     """Grouped launches issued while the caller is still collecting tensors.
 
@@ -688,11 +740,10 @@ class QuantPlan:
             descs[i].scales = scales.data_ptr()
             descs[i].batch, descs[i].rows, descs[i].cols = batch, rows, cols
             descs[i].ld, descs[i].batch_stride = ld, bstride
-        launch = _GroupLaunch(self.fmt, descs, len(tensors),
-                              _IN_DTYPES.get(self.dtype, _lib.DTYPE_F64), self._block,
-                              self._flags, self.device)
-        if self._owned:
-            launch.buffers += [t for pair in self.outputs for t in pair]
+        sizes = [_nbytes(t) + _nbytes(c) + _nbytes(sc) for t, (c, sc) in zip(tensors, self.outputs)]
+        launch = _GroupLaunches(self.fmt, descs, sizes, _IN_DTYPES.get(self.dtype, _lib.DTYPE_F64),
+                                self._block, self._flags, self.device,
+                                buffers=[list(pair) for pair in self.outputs] if self._owned else None)
         self._launch = launch
         self._views = views
         self.inputs = tensors
@@ -788,9 +839,9 @@ class DequantPlan:
             nbytes += _nbytes(c) + _nbytes(sc) + _nbytes(out)
         self.algorithmic_bytes = nbytes
         flags = _lib.FLAG_OUT_BF16 if out_dtype == torch.bfloat16 else 0
-        self._launch = _GroupLaunch("fp8_dequant", descs, len(pairs), _IN_DTYPES[sdt], (br, bc),
-                                    flags, dev)
-        self._launch.buffers += self.outputs
+        sizes = [_nbytes(c) + _nbytes(sc) + _nbytes(o) for (c, sc), o in zip(self.inputs, self.outputs)]
+        self._launch = _GroupLaunches("fp8_dequant", descs, sizes, _IN_DTYPES[sdt], (br, bc), flags, dev,
+                                      buffers=[[o] for o in self.outputs])
         self.units = self._launch.units
 
     def _init_mx(self, pairs, fmt: str, out_dtype: torch.dtype) -> None:
@@ -819,9 +870,9 @@ class DequantPlan:
             nbytes += _nbytes(c) + _nbytes(sc) + _nbytes(out)
         self.algorithmic_bytes = nbytes
         flags = _lib.FLAG_OUT_BF16 if out_dtype == torch.bfloat16 else 0
-        self._launch = _GroupLaunch(fmt + "_dequant", descs, len(pairs), _lib.DTYPE_BF16, (1, 32),
-                                    flags, dev)
-        self._launch.buffers += self.outputs
+        sizes = [_nbytes(c) + _nbytes(sc) + _nbytes(o) for (c, sc), o in zip(self.inputs, self.outputs)]
+        self._launch = _GroupLaunches(fmt + "_dequant", descs, sizes, _lib.DTYPE_BF16, (1, 32), flags, dev,
+                                      buffers=[[o] for o in self.outputs])
         self.units = self._launch.units
 
     def run(self) -> list[Tensor]:

@@ -281,6 +281,34 @@ def test_launch_chunks_cover_every_item_once_in_order(n):
     assert sizes == want
 
 
+from lumenrl_amd.quantization.ops import GROUP_LAUNCH_BYTES, launch_ranges  # noqa: E402
+
+
+@given(st.lists(st.integers(min_value=0, max_value=5000), max_size=60), st.integers(min_value=1, max_value=6000))
+@settings(max_examples=200, deadline=None)
+def test_launch_ranges_split_plans_into_maximal_runs(sizes, limit):
+    """A grouped plan's launches: consecutive runs of whole tensors covering
+    every tensor once, in order; each run within the byte limit unless it is a
+    single larger tensor, and no run could take the next tensor too."""
+    rs = launch_ranges(sizes, limit)
+    assert [k for i, j in rs for k in range(i, j)] == list(range(len(sizes)))
+    for n, (i, j) in enumerate(rs):
+        assert j > i
+        assert sum(sizes[i:j]) <= limit or j - i == 1
+        if n + 1 < len(rs):
+            assert sum(sizes[i:j + 1]) > limit
+
+
+def test_launch_ranges_of_the_qwen3_8b_set():
+    """The 252 Qwen3-8B linears (128x128 FP8: 3 bytes per element plus scales)
+    split into 7 launches of consecutive tensors under the default limit."""
+    shapes = [(4096, 4096), (1024, 4096), (1024, 4096), (4096, 4096), (12288, 4096), (12288, 4096),
+              (4096, 12288)] * 36
+    sizes = [3 * r * c + 4 * (r // 128) * (c // 128) for r, c in shapes]
+    rs = launch_ranges(sizes)
+    assert len(rs) == 7 and all(sum(sizes[i:j]) <= GROUP_LAUNCH_BYTES for i, j in rs)
+
+
 from lumenrl_amd.quantization.ops import ChunkedLaunches  # noqa: E402
 
 
