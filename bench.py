@@ -76,7 +76,8 @@ PROFILE_FOR = {"c1": "k_tile128_single_4096x4096_c1", "c2": "k_tile128_qwen3_8b_
                "cast": "k_cast_e4m3_qwen3_8b_state_dynamic_weight_loader",
                "c4d": "k_mx_dequant_qwen3_8b_mxfp8_to_bf16", "c2sd": "k_row_qwen3_8b_state_dict_dropin",
                "rollout": "k_row_qwen3_8b_rollout_quantize_model", "c2pc": "k_row_wide_qwen3_8b_per_channel",
-               "f64": "k_row_f64_qwen3_8b_4_layers_quantize_tensor"}
+               "f64": "k_row_f64_qwen3_8b_4_layers_quantize_tensor",
+               "bucket": "k_tile128_k_copy_qwen3_8b_state_bucket_sync"}
 KERNEL_FOR = {"c1": "k_tile128", "c2": "k_tile128", "c3": "k_tile128", "c4": "k_mx", "c5": "k_mx",
               "c2r": "k_row", "c2d": "k_dequant", "act": "k_act_qdq8", "kv": "k_amax", "c2sd": "k_row", "bucket": "k_tile128",
               "cast": "k_cast_e4m3", "c4d": "k_mx_dequant", "rollout": "k_row", "f64": "k_row_f64",
@@ -693,14 +694,14 @@ def run(args):
     log(f"[bench] {ms_per_step:.4f} ms/step, {value:.1f} GB/s; kernel avg {kern_ms:.4f} ms "
         f"({achieved:.1f} GB/s = {achieved / HBM_PEAK_GBS:.1%} of 8 TB/s)")
 
-    # HBM bytes per launch of the dominant kernel, from the committed rocprofv3
-    # FETCH_SIZE/WRITE_SIZE summary of this workload (copy-calibrated)
+    # HBM bytes per plan run (the span `launch_ms` times), from the committed
+    # rocprofv3 FETCH_SIZE/WRITE_SIZE summary of this workload (copy-calibrated)
     traffic = None
     pfile = os.path.join(ROOT, "profiles", PROFILE_FOR.get(cfg, "") + ".md")
     if os.path.exists(pfile):
         with open(pfile) as f:
             for line in f:
-                if line.startswith("hbm_bytes_per_launch:"):
+                if line.startswith("hbm_bytes_per_plan_run:"):
                     traffic = int(line.split(":", 1)[1])
 
     result = {
