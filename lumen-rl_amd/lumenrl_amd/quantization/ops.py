@@ -623,7 +623,9 @@ def _nbytes(t: Tensor) -> int:
 
 
 class QuantPlan:
-    """One kernel launch that quantizes a whole list of weights.
+    """Grouped kernel launches that quantize a whole list of weights: one launch
+    per run of consecutive tensors of at most ``GROUP_LAUNCH_BYTES`` (a tensor is
+    never split; a Qwen3-8B layer or a MoE layer's expert stacks is one launch).
 
     The plan allocates every output once (or takes caller-provided output
     views, e.g. slices of a transfer bucket) and uploads a small descriptor
@@ -788,7 +790,8 @@ class QuantPlan:
 
 
 class DequantPlan:
-    """One kernel launch that dequantizes a list of (codes, scales) pairs.
+    """Grouped kernel launches that dequantize a list of (codes, scales) pairs
+    (split between tensors as in ``QuantPlan``).
 
     fp32(code) * fp32(scale) per ``block_size`` block, written as ``out_dtype``
     (float32: dequantize_tensor; bfloat16: dequantize_state_dict's cast).
