@@ -699,12 +699,13 @@ int lrq_group_build_map(const void* host_table, void* device_table, lrq_stream_t
     // Set-up of a tensor-scale table: look up the static workspace's device
     // address now, so lrq_tensor_scale_grouped_static makes no symbol lookup
     // (a runtime call that is not a stream operation) when a caller captures it.
+    // Best effort: the caller-workspace entry point does not need it, and the
+    // static one repeats the lookup, and reports its failure, if this one failed.
     int d = -1;
-    if (int rc = check_hip(stream ? hipStreamGetDevice((hipStream_t)stream, &d) : hipGetDevice(&d),
-                           "device of the stream"))
-      return rc;
     uint32_t* ws = nullptr;
-    if (int rc = check_hip(lrq::static_workspace(d, &ws), "static workspace address")) return rc;
+    if ((stream ? hipStreamGetDevice((hipStream_t)stream, &d) : hipGetDevice(&d)) != hipSuccess ||
+        lrq::static_workspace(d, &ws) != hipSuccess)
+      (void)hipGetLastError();
   }
   if (h.units == 0) return 0;
   char* dev = static_cast<char*>(device_table);
