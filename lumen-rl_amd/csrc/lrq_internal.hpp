@@ -92,7 +92,9 @@ constexpr int64_t kXcdRunTile = 4;
 constexpr int64_t kXcdRunTileF64 = 32;  // k_tile_f64: 32 tiles (128 KiB each)
 constexpr int64_t kXcdRunRow = 16;     // k_row: 256 KiB of bf16 (32 loses 2%)
 constexpr int64_t kXcdRunMx = 64;      // k_mx: 512 KiB of bf16 (32 loses 2.5%, 128 ties)
-constexpr int64_t kXcdRunStream = 32;  // dequant, act, amax, copy, cast, generic kernels
+// dequant, act, amax, copy, cast, generic kernels: runs of 4, 8 and 16 lose
+// 2-10 points on dequantize, cast, activation and tensor-scale launches; 64 ties.
+constexpr int64_t kXcdRunStream = 32;
 constexpr int kCastLaneElems = 16;   // k_cast_e4m3: elements per lane
 constexpr int64_t kCastUnit = 256 * kCastLaneElems;  // k_cast_e4m3: elements per work-group
 constexpr int kAmaxLoads = 2;        // k_amax: 16-byte loads per lane (2 beat 1, 3, 4 and 8)
