@@ -40,7 +40,7 @@ bool pow2_block(int64_t b) { return b == 32 || b == 64 || b == 128 || b == 256 |
 bool row_block(int64_t b) { return pow2_block(b) || b == 1024 || b == 2048; }
 
 constexpr uint32_t kMagic = 0x4C525154u;  // "LRQT"
-constexpr uint32_t kTableVersion = 4u;  // 4: LaunchCfg gained `pitched` and `chunk`
+constexpr uint32_t kTableVersion = 5u;  // 5: k_tile128 descriptors carry their XCD run
 // HIP takes a launch's thread count (work-groups x threads per work-group) as
 // a 32-bit value.  kMaxGrid is the limit for 256-thread work-groups;
 // max_units() gives it for the work-group size of the launch `cfg` selects.
@@ -179,6 +179,7 @@ bool plan_units(const LaunchCfg& cfg, Desc& d) {
       d.units_r = (d.rows + cfg.blk_r - 1) / cfg.blk_r;
       d.units_c = (d.cols + cfg.blk_c - 1) / cfg.blk_c;
       d.units = d.batch * d.units_r * d.units_c;
+      if (cfg.kernel == kKernTile128) d.bpr = tile_run_log2(d.ld * esize(cfg.in_dtype));
       return true;
     case kKernF64Row: {  // 4 waves x f64_row_instr instructions of 128 doubles
       if (!fold_batch(d)) return false;

@@ -6,7 +6,8 @@
 // e4m3 + scale out).  Five kernels:
 //   k_tile128  : 128x128 tiles (the vLLM/ATOM `weight_scale_inv` layout), one
 //                512-thread work-group per tile, the tile held in VGPRs;
-//                tiles handed to XCDs in runs of kXcdRunTile (xcd_unit).
+//                tiles handed to XCDs in runs of 4 or 8 by row pitch
+//                (pick_desc_tile).
 //   k_row      : 1xB row blocks (the reference's own layout), ceil(B/8)
 //                consecutive lanes per block (padded to a power of two) so
 //                every wave instruction is one contiguous span; one scale
@@ -139,7 +140,7 @@ __global__ __launch_bounds__(T) void k_tile128(Desc single, const Desc* __restri
   __shared__ uint32_t red[T / 64];
   Desc d;
   int64_t u;
-  pick_desc<kXcdRunTile>(single, descs, map, d, u);
+  pick_desc_tile(single, descs, map, d, u);
 
   const int64_t per = d.units_r * d.units_c;
   const int64_t b = u / per;

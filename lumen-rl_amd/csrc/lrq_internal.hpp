@@ -21,7 +21,7 @@ struct Desc {
   int64_t units_c;   // tile kernel: tiles per row band; amax: 1 = 16-byte loads
   int64_t units_r;   // tile kernel: tile rows per matrix; amax: 1 = contiguous
   int64_t nblocks;   // row/MX kernels: number of blocks/groups
-  int64_t bpr;       // row/MX kernels: blocks (groups) per row
+  int64_t bpr;       // row/MX kernels: blocks (groups) per row; k_tile128: log2 of its XCD run
 };
 static_assert(sizeof(Desc) == 112, "Desc layout is part of the grouped table format");
 
@@ -80,15 +80,24 @@ constexpr WideShape wide_shape(int dtype, int64_t blk_c) {
 constexpr int kTileThreads = 512;    // k_tile128: threads per 128x128 tile (512 beat 256 and 1024)
 constexpr int kRowBlocks = 4;        // k_row: wave instructions per lane, one 1xB block each up to B = 512, sharing
                                      // one scale computation (4: 2 is 7% slower with bf16 scales, 3 slower with both)
-// XCD run length (xcd_unit) per kernel, in work units; sweeps over 8..128:
-// k_tile128: runs of 4 tiles, so the 8 XCDs share every 32-tile group (one
-// 8 KiB row span of a K = 4096 band) and XCD x always reads its own 1 KiB
-// column slice of it (address bits 10-12 == x for 8 KiB-aligned rows).  Against
-// runs of 32 (whole K = 4096 bands per XCD): C2 80.1-80.9 % of 8 TB/s from
-// 77.6-79.2 %, its 36 down_proj (K = 12288) 81 % from 77-78 %, single 2 GiB
-// weights 81.4-82 % at K = 4096 and 12288; runs of 2, 6, 8 and 16 lose 5-10
-// points on C2.
-constexpr int64_t kXcdRunTile = 4;
+// XCD run length (xcd_unit) per kernel, in work units; sweeps over 8..128.
+// k_tile128 takes a run per tensor (Desc::bpr, the log2 of it, from the
+// input's row pitch: tile_run_log2).  Rows of a multiple of 8 KiB take runs of
+// 4 tiles, so the 8 XCDs share every 32-tile group (one 8 KiB row span of a
+// K = 4096 band) and XCD x always reads its own 1 KiB column slice of it
+// (address bits 10-12 == x for 8 KiB-aligned rows).  Against runs of 32 (whole
+// K = 4096 bands per XCD): C2 80.1-80.9 % of 8 TB/s from 77.6-79.2 %, its 36
+// down_proj (K = 12288) 81 % from 77-78 %, single 2 GiB weights 81.4-82 % at
+// K = 4096 and 12288; runs of 2, 6, 8 and 16 lose 5-10 points on C2.  Other
+// pitches take runs of 8: the 48 Qwen3-30B-A3B expert layers (4 KiB gate_up
+// rows, 1.5 KiB down rows; one launch per layer) 82.5-82.8 % against
+// 81.8-82.3 % with runs of 4, interleaved in one process (runs of 16, 32 or
+// one tile row for the down rows: within 0.3 points of 8).
+constexpr int kTileRunLog2Wide = 2;    // rows of a multiple of 8 KiB: runs of 4
+constexpr int kTileRunLog2Narrow = 3;  // any other row pitch: runs of 8
+constexpr int tile_run_log2(int64_t pitch_bytes) {
+  return pitch_bytes % 8192 == 0 ? kTileRunLog2Wide : kTileRunLog2Narrow;
+}
 constexpr int64_t kXcdRunTileF64 = 32;  // k_tile_f64: 32 tiles (128 KiB each)
 constexpr int64_t kXcdRunRow = 16;     // k_row: 256 KiB of bf16 (32 loses 2%)
 constexpr int64_t kXcdRunMx = 64;      // k_mx: 512 KiB of bf16 (32 loses 2.5%, 128 ties)
@@ -149,6 +158,29 @@ __device__ __forceinline__ void pick_desc(const Desc& single, const Desc* descs,
     d = single;
     u = wg;
   }
+}
+
+// The 128x128 tile kernel's descriptor and local tile: xcd_unit over the
+// tensor's own tiles with its run of 2^Desc::bpr (shifts and masks only).  A
+// grouped tensor may start at any work-group; 8 consecutive work-groups still
+// visit each XCD once, so each run of 2^bpr tiles lands on one XCD.
+__device__ __forceinline__ void pick_desc_tile(const Desc& single, const Desc* descs,
+                                               const uint32_t* map, Desc& d, int64_t& u) {
+  const uint32_t wg = blockIdx.x;
+  uint32_t i;
+  if (map != nullptr) {
+    d = descs[map[wg]];
+    i = wg - (uint32_t)d.unit0;
+  } else {
+    d = single;
+    i = wg;
+  }
+  const uint32_t lg = (uint32_t)d.bpr, chunk = 8u << lg;
+  if (i < ((uint32_t)d.units & ~(chunk - 1u))) {
+    const uint32_t r = i & (chunk - 1u);
+    i = (i - r) + ((r & 7u) << lg) + (r >> 3);
+  }
+  u = i;
 }
 
 // Launch parameters common to every tensor of one launch.

@@ -124,6 +124,9 @@ def test_group_pack_tiles_qwen3_layer():
     assert buf.size == 256 + -(-7 * 112 // 256) * 256
     d = buf[256:256 + 7 * 112].view(np.int64).reshape(7, 14)
     assert np.array_equal(d[:, 8], np.cumsum([0] + tiles[:-1])) and np.array_equal(d[:, 9], tiles)
+    # each tile descriptor carries the log2 of its XCD run: 4 tiles for rows of
+    # a multiple of 8 KiB (every tensor here)
+    assert np.all(d[:, 13] == 2)
     # the device table adds 4 bytes of work-group -> tensor map per work-group
     assert L().lrq_group_device_bytes(buf.ctypes.data) == buf.size + 4 * units
     assert L().lrq_group_device_bytes(None) == _lib.ERR_ARG
@@ -175,6 +178,27 @@ def test_group_pack_rows_and_mx_units():
 def test_group_pack_expert_stack_single_descriptor():
     buf = _pack(_lib.FMT_FP8_BLOCK, [(128, 768, 2048), (128, 2048, 768)])
     assert L().lrq_group_units(buf.ctypes.data) == 128 * 6 * 16 + 128 * 16 * 6
+
+
+def test_tile_xcd_run_follows_the_row_pitch():
+    """k_tile128 descriptors: runs of 4 tiles (log2 2) when a row spans a
+    multiple of 8 KiB of input, runs of 8 (log2 3) for any other pitch."""
+    def runs(shapes, dtype=0, ld=None):
+        ts = _tensors(shapes)
+        if ld is not None:
+            for t, l in zip(ts, ld):
+                t.ld, t.batch_stride = l, t.rows * l
+        need = L().lrq_group_table_bytes(_lib.FMT_FP8_BLOCK, ts, len(shapes), dtype, 128, 128, 0)
+        buf = np.zeros(need, np.uint8)
+        assert L().lrq_group_pack(_lib.FMT_FP8_BLOCK, ts, len(shapes), dtype, 128, 128, 0,
+                                  buf.ctypes.data, need) == 0, _lib.last_error()
+        return list(buf[256:256 + len(shapes) * 112].view(np.int64).reshape(-1, 14)[:, 13])
+    # bf16: 8 KiB (K = 4096), 24 KiB, 4 KiB (K = 2048), 1.5 KiB (K = 768), 2 KiB
+    assert runs([(1, 256, 4096), (1, 256, 12288), (2, 256, 2048), (2, 256, 768), (1, 300, 1024)]) == [2, 2, 3, 3, 3]
+    # float32 input: K = 2048 rows are 8 KiB
+    assert runs([(1, 256, 2048), (1, 256, 768)], dtype=_lib.DTYPE_F32) == [2, 3]
+    # the pitch counts, not the width: K = 2048 views of K = 4096 rows keep runs of 4
+    assert runs([(1, 256, 2048), (1, 256, 2048)], ld=[4096, 3072]) == [2, 3]
 
 
 def test_group_pack_rejects_mixed_kernels_and_small_buffers():

@@ -465,6 +465,37 @@ def test_grouped_expert_stacks_single_launch():
         assert np.array_equal(scale_bits(s).reshape(-1), osc.view(np.uint32).reshape(-1))
 
 
+def test_tile_xcd_runs_at_odd_offsets_and_tails():
+    """The tile kernel remaps each tensor's tiles in runs of 4 (rows of a
+    multiple of 8 KiB) or 8 (other pitches), within the tensor: tensors that
+    start at work-groups off a run-chunk boundary, whole chunks followed by a
+    partial one, and a strided view whose pitch (not width) sets the run must
+    all match the oracle tile for tile."""
+    wide = weights((600, 4096))
+    shapes = [(300, 1000),        # 24 tiles, pitch 2000 B: runs of 8, all in the partial chunk
+              (1100, 2048),       # 144 tiles from work-group 24: 2 chunks of 64 + 16
+              (640, 4096),        # 160 tiles from 168 (168 % 32 = 8), runs of 4: 5 chunks
+              (2, 700, 768)]      # 72 tiles from 328: 1 chunk + 8
+    ws = [weights(s) for s in shapes]
+    ws[1][1000, 2000] = float("inf")
+    ws[3][1, 128:256, 384:512] = 0.0
+    views = [w.to(DEV) for w in ws]
+    views.append(wide.to(DEV)[:, 64:2112])  # 80 tiles, cols 2048 on 8 KiB rows: runs of 4
+    plan = ops.QuantPlan(views, "fp8_block", (128, 128))
+    assert plan.units == 24 + 144 + 160 + 72 + 80
+    plan.run()
+    torch.cuda.synchronize()
+    say("tile runs: grouped")
+    for w, (c, s) in zip(views, plan.outputs):
+        xh = host_bits(w)
+        oc, osc = O.fp8_block_quant(xh.reshape((-1,) + xh.shape[-2:]), "bf16", "f32", (128, 128))
+        assert np.array_equal(u8(c).reshape(oc.shape), oc)
+        assert np.array_equal(scale_bits(s).reshape(-1), osc.view(np.uint32).reshape(-1))
+    say("tile runs: single launches")
+    assert_fp8_matches_oracle(weights((1300, 1536)).to(DEV), (128, 128))  # 132 tiles: 2 chunks + 4
+    assert_fp8_matches_oracle(views[4], (128, 128))
+
+
 # ----------------------------------------------------------------------------
 # exhaustive (x, amax): every bf16 x against every finite bf16 amax
 # ----------------------------------------------------------------------------
