@@ -223,6 +223,10 @@ int lrq_group_build_map(const void* host_table, void* device_table, lrq_stream_t
 int lrq_quant_grouped(const void* host_table, const void* device_table, lrq_stream_t stream);
 /* work-groups of a packed table's launch (for bandwidth accounting) */
 int64_t lrq_group_units(const void* host_table);
+/* kernel a packed table launches, as an opaque id >= 0: a list split into
+ * several tables (consecutive tensors per launch) takes one kernel exactly when
+ * every table reports the same id, as lrq_group_pack() requires of one table */
+int lrq_group_kernel(const void* host_table);
 /*
  * Per-tensor FP8 scales of the KV-cache quantizer, for a table packed with
  * fmt LRQ_FMT_TENSOR_SCALE (blk_r, blk_c and flags are ignored):

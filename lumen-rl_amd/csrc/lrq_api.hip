@@ -805,6 +805,15 @@ int64_t lrq_group_units(const void* host_table) {
   return h.units;
 }
 
+int lrq_group_kernel(const void* host_table) {
+  g_err.clear();
+  if (!host_table) return fail(LRQ_ERR_ARG, "null table");
+  GroupHeader h;
+  memcpy(&h, host_table, sizeof(h));
+  if (h.magic != kMagic || h.version != kTableVersion) return fail(LRQ_ERR_TABLE, "not an lrq table");
+  return h.cfg.kernel;
+}
+
 const char* lrq_version(void) { return "lrq 0.1.0 gfx950"; }
 const char* lrq_last_error(void) { return g_err.c_str(); }
 

@@ -54,6 +54,7 @@ SIGNATURES = {
     "lrq_group_pack": (_CI, [_CI, ctypes.POINTER(LrqTensor), _I64, _CI, _I64, _I64, _CU, _VP, _I64]),
     "lrq_quant_grouped": (_CI, [_VP, _VP, _VP]),
     "lrq_group_units": (_I64, [_VP]),
+    "lrq_group_kernel": (_CI, [_VP]),
     "lrq_group_device_bytes": (_I64, [_VP]),
     "lrq_group_build_map": (_CI, [_VP, _VP, _VP]),
     "lrq_group_workspace_bytes": (_I64, [_VP]),

@@ -448,6 +448,14 @@ class _GroupLaunches:
             if buffers is not None:
                 part.buffers += [b for k in range(i, j) for b in buffers[k]]
             self.parts.append(part)
+        # One kernel for the whole list, as one table requires of its tensors,
+        # wherever the launches split it: the first tensor of the first part
+        # whose kernel differs is the first tensor that differs from tensor 0.
+        kinds = [int(_lib.lib().lrq_group_kernel(p.host.data_ptr())) for p in self.parts]
+        for (i, _), k in zip(launch_ranges(sizes), kinds):
+            if k != kinds[0]:
+                raise ValueError(f"tensor {i} needs a different kernel than tensor 0 "
+                                 "(alignment/shape); group it separately")
         self.units = sum(p.units for p in self.parts)
 
     @property

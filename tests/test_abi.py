@@ -180,6 +180,20 @@ def test_group_pack_expert_stack_single_descriptor():
     assert L().lrq_group_units(buf.ctypes.data) == 128 * 6 * 16 + 128 * 16 * 6
 
 
+def test_group_kernel_ids_tell_tables_apart():
+    """lrq_group_kernel: equal ids for tables of the same kernel, different ids
+    for the tile kernel and the generic one (K % 8 != 0); errors as the other
+    table readers."""
+    tile_a = _pack(_lib.FMT_FP8_BLOCK, [(1, 256, 256)])
+    tile_b = _pack(_lib.FMT_FP8_BLOCK, [(2, 128, 4096), (1, 300, 1024)])
+    generic = _pack(_lib.FMT_FP8_BLOCK, [(1, 256, 300)])
+    rows = _pack(_lib.FMT_FP8_BLOCK, [(1, 256, 256)], (1, 128))
+    ids = [L().lrq_group_kernel(b.ctypes.data) for b in (tile_a, tile_b, generic, rows)]
+    assert min(ids) >= 0 and ids[0] == ids[1] and len({ids[0], ids[2], ids[3]}) == 3
+    assert L().lrq_group_kernel(None) == _lib.ERR_ARG
+    assert L().lrq_group_kernel(np.zeros(256, np.uint8).ctypes.data) == _lib.ERR_TABLE
+
+
 def test_tile_xcd_run_follows_the_row_pitch():
     """k_tile128 descriptors: runs of 4 tiles (log2 2) when a row spans a
     multiple of 8 KiB of input, runs of 8 (log2 3) for any other pitch."""

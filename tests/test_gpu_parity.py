@@ -465,6 +465,26 @@ def test_grouped_expert_stacks_single_launch():
         assert np.array_equal(scale_bits(s).reshape(-1), osc.view(np.uint32).reshape(-1))
 
 
+def test_plan_mixing_kernels_raises_wherever_launches_split(monkeypatch):
+    """A plan whose tensors take different kernels (128x128 tiles with K % 8
+    != 0 take the generic kernel) raises ValueError whether the two tensors
+    share a launch or not."""
+    ws = [weights((256, 256)).to(DEV), weights((256, 300)).to(DEV)]
+    for limit in (ops.GROUP_LAUNCH_BYTES, 1):  # one launch; one launch per tensor
+        monkeypatch.setattr(ops, "GROUP_LAUNCH_BYTES", limit)
+        with pytest.raises(ValueError, match="tensor 1 needs a different kernel than tensor 0"):
+            ops.QuantPlan(ws, "fp8_block", (128, 128))
+    # each kind alone still plans and runs, split or not
+    plan = ops.QuantPlan([ws[0], weights((300, 512)).to(DEV)], "fp8_block", (128, 128))
+    assert len(plan._launch.parts) == 2
+    plan.run()
+    torch.cuda.synchronize()
+    for w, (c, s) in zip(plan.inputs, plan.outputs):
+        oc, osc = O.fp8_block_quant(host_bits(w)[None], "bf16", "f32", (128, 128))
+        assert np.array_equal(u8(c).reshape(oc.shape), oc)
+        assert np.array_equal(scale_bits(s).reshape(-1), osc.view(np.uint32).reshape(-1))
+
+
 def test_tile_xcd_runs_at_odd_offsets_and_tails():
     """The tile kernel remaps each tensor's tiles in runs of 4 (rows of a
     multiple of 8 KiB) or 8 (other pitches), within the tensor: tensors that
