@@ -44,8 +44,11 @@ scales) per step / step time, in GB/s (1e9 B/s).  With --config c2 (the
 default) the line also carries `also`: c3, c4 and c5 timed on the device the
 same way after c2's set is freed (ms_per_step, step GB/s, kernel GB/s and its
 fraction of 8 TB/s; no CPU leg; --no-also skips them).  The roofline object uses the
-same bytes over the step's kernel time (`launch_ms`: HIP events on the launch
-stream around each plan's launches).  cpu_baseline times the reference's op sequence in torch on the host
+same bytes over the step's kernel time (HIP events on the launch stream around
+each plan run, whose grouped launches run back to back): `launch_ms` is the mean
+launch (a run's event time over its launches), as rocprofv3 averages a kernel;
+`plan_run_ms` the run itself; `traffic` the profiled HBM bytes per launch beside
+`algorithmic_bytes_per_launch`.  cpu_baseline times the reference's op sequence in torch on the host
 CPU (oracle/torch_ref.py) over a bounded sample of the same weights.
 """
 
@@ -436,6 +439,12 @@ def _launches(plans) -> int:
     return sum(len(p._launch.parts) for p in plans)
 
 
+def _bucket_launches(writer) -> int:
+    """lrq launches of one sync through these buckets: each bucket's grouped
+    quantize launches and its one grouped copy of the pass-through tensors."""
+    return sum(_launches([plan for _, plan in b.plans]) + (b.copy_plan is not None) for b in writer)
+
+
 def setup(torch, ops, cfg, args, dev):
     """The workload of one config, resident on the device: plans (each with
     run() and algorithmic_bytes), the input tensors, and what the JSON line and
@@ -486,7 +495,7 @@ def setup(torch, ops, cfg, args, dev):
         workload = "qwen3-8b-linears-fp8-e4m3-per-channel"
         cpu_ws, cpu_blk, cpu_fmt = ws, (1, 0), "fp8_block"
         extra = {"tensors": len(ws), "layers": 36, "elements": sum(w.numel() for w in ws),
-                 "format": "fp8_block_1xK_per_channel", "launches_per_step": len(plans)}
+                 "format": "fp8_block_1xK_per_channel", "launches_per_step": _launches(plans)}
     elif cfg == "f64":
         ws, _ = qwen3_8b_set(torch, dev, args.seed, "normal", layers=4)
         ws = [w.double() for w in ws]  # bf16 values widened exactly
@@ -527,7 +536,8 @@ def setup(torch, ops, cfg, args, dev):
         extra = {"tensors": len(named), "buckets": len(writer), "layers": 36,
                  "elements": sum(w.numel() for w in ws),
                  "passthrough_tensors": sum(len(b.copies) for b in writer),
-                 "format": "fp8_block_128x128 + passthrough copies", "launches_per_step": len(writer)}
+                 "format": "fp8_block_128x128 + passthrough copies",
+                 "launches_per_step": _bucket_launches(writer)}
     elif cfg == "cast":
         named = qwen3_8b_state(torch, dev, args.seed)
         plans = [_LoaderCall(dict(named))]
@@ -591,9 +601,10 @@ def setup(torch, ops, cfg, args, dev):
 def measure(torch, ops, plans, flush, args, stream):
     """Time exactly args.steps steps (after args.warmup untimed ones) of the
     plans, bracketed by synchronizations, with HIP events on the launch stream
-    around every launch.  ms_per_step is the wall time per step (the launches'
+    around every plan run.  ms_per_step is the wall time per step (the runs'
     summed event time when an L2 flush separates them); kern_ms is the mean
-    event time of one launch and `achieved` its algorithmic GB/s."""
+    event time of one plan run (its grouped launches back to back) and
+    `achieved` its algorithmic GB/s."""
     # A drop-in call (quantize_state_dict, load_weights) plans on the host
     # before and between its grouped launches.  Its kernel time spans its first
     # launch to the end of its last (the small table uploads between launches
@@ -611,7 +622,13 @@ def measure(torch, ops, plans, flush, args, stream):
         return base_run(self)
 
     ops._GroupLaunch.run = timed_run
+    try:
+        return _timed_steps(torch, plans, flush, args, stream, inner)
+    finally:
+        ops._GroupLaunch.run = base_run
 
+
+def _timed_steps(torch, plans, flush, args, stream, inner):
     def step(ev_pairs=None):
         for p in plans:
             if flush is not None:
@@ -658,7 +675,6 @@ def measure(torch, ops, plans, flush, args, stream):
         ms_per_step = wall * 1e3 / args.steps
     else:  # the L2 flush between launches is not part of the step
         ms_per_step = sum(launch_ms) / args.steps
-    ops._GroupLaunch.run = base_run
     return {"ms_per_step": ms_per_step, "median_step_ms": median_step_ms, "kern_ms": kern_ms,
             "achieved": achieved}
 
@@ -694,15 +710,21 @@ def run(args):
     log(f"[bench] {ms_per_step:.4f} ms/step, {value:.1f} GB/s; kernel avg {kern_ms:.4f} ms "
         f"({achieved:.1f} GB/s = {achieved / HBM_PEAK_GBS:.1%} of 8 TB/s)")
 
-    # HBM bytes per plan run (the span `launch_ms` times), from the committed
-    # rocprofv3 FETCH_SIZE/WRITE_SIZE summary of this workload (copy-calibrated)
+    # Per launch, as rocprofv3 reports a kernel: a step makes `launches` launches
+    # (len(plans) plan runs, each timed by one event pair, its launches back to
+    # back), so the mean launch is a run's event time over its launches (the few
+    # us between a run's launches included).  HBM bytes per launch: the committed
+    # rocprofv3 FETCH_SIZE/WRITE_SIZE summary of this workload (copy-calibrated),
+    # per step, over the step's launches.
+    launches = extra["launches_per_step"]
+    per_run = launches / len(plans)
     traffic = None
     pfile = os.path.join(ROOT, "profiles", PROFILE_FOR.get(cfg, "") + ".md")
     if os.path.exists(pfile):
         with open(pfile) as f:
             for line in f:
-                if line.startswith("hbm_bytes_per_plan_run:"):
-                    traffic = int(line.split(":", 1)[1])
+                if line.startswith("hbm_bytes_per_step:"):
+                    traffic = round(int(line.split(":", 1)[1]) / launches)
 
     result = {
         "metric": metric_name(),
@@ -727,8 +749,11 @@ def run(args):
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
             "traffic": traffic,
+            "algorithmic_bytes_per_launch": round(step_bytes / launches),
             "kernel": KERNEL_FOR[cfg],
-            "launch_ms": round(kern_ms, 5),
+            "launch_ms": round(kern_ms / per_run, 5),
+            "launches_per_plan_run": round(per_run, 3),
+            "plan_run_ms": round(kern_ms, 5),
         },
     }
     if not args.no_cpu and cpu_ws:
@@ -763,7 +788,8 @@ def also_configs(torch, ops, args, dev, stream):
                   "algorithmic_bytes_per_step": nb, "ms_per_step": round(r["ms_per_step"], 5),
                   "value": round(nb / (r["ms_per_step"] * 1e-3) / 1e9, 2),
                   "achieved": round(r["achieved"], 2), "frac": round(r["achieved"] / HBM_PEAK_GBS, 4),
-                  "launch_ms": round(r["kern_ms"], 5)}
+                  "launch_ms": round(r["kern_ms"] * len(w["plans"]) / w["extra"]["launches_per_step"], 5),
+                  "plan_run_ms": round(r["kern_ms"], 5)}
         log(f"[bench] also {c} ({w['workload']}): {r['ms_per_step']:.4f} ms/step, kernel "
             f"{r['achieved']:.1f} GB/s = {r['achieved'] / HBM_PEAK_GBS:.1%}, setup {time.time() - t0:.1f}s")
         del w
