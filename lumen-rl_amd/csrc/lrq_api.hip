@@ -761,7 +761,8 @@ int lrq_tensor_scale_grouped(const void* host_table, const void* device_table, v
   if (workspace_bytes < h.units * 4)
     return fail(LRQ_ERR_CAPACITY, "workspace needs %lld bytes, have %lld", (long long)(h.units * 4),
                 (long long)workspace_bytes);
-  if (h.n > kMaxGrid) return fail(LRQ_ERR_ARG, "too many tensors for one launch");
+  if (h.n > 0xFFFFFFFFll / lrq::kScaleThreads)  // the finishing launch: a work-group per tensor
+    return fail(LRQ_ERR_ARG, "too many tensors for one launch");
   const char* dev = static_cast<const char*>(device_table);
   const Desc* descs = reinterpret_cast<const Desc*>(dev + h.desc_off);
   const uint32_t* map = reinterpret_cast<const uint32_t*>(dev + h.map_off);
@@ -782,7 +783,8 @@ int lrq_tensor_scale_grouped_static(const void* host_table, const void* device_t
   if (h.units > (int64_t)(LRQ_STATIC_WORKSPACE_BYTES / 4))
     return fail(LRQ_ERR_CAPACITY, "table needs %lld bytes of workspace, the static workspace holds %lld",
                 (long long)(h.units * 4), (long long)LRQ_STATIC_WORKSPACE_BYTES);
-  if (h.n > kMaxGrid) return fail(LRQ_ERR_ARG, "too many tensors for one launch");
+  if (h.n > 0xFFFFFFFFll / lrq::kScaleThreads)  // the finishing launch: a work-group per tensor
+    return fail(LRQ_ERR_ARG, "too many tensors for one launch");
   int dev = -1;
   if (int rc = check_hip(stream ? hipStreamGetDevice((hipStream_t)stream, &dev) : hipGetDevice(&dev),
                          "device of the stream"))

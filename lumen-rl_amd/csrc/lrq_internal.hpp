@@ -107,6 +107,7 @@ constexpr int64_t kXcdRunStream = 32;
 constexpr int kCastLaneElems = 16;   // k_cast_e4m3: elements per lane
 constexpr int64_t kCastUnit = 256 * kCastLaneElems;  // k_cast_e4m3: elements per work-group
 constexpr int kAmaxLoads = 2;        // k_amax: 16-byte loads per lane (2 beat 1, 3, 4 and 8)
+constexpr int kScaleThreads = 1024;  // k_tensor_scale: one work-group per tensor
 // k_row_f64: 1 KiB wave instructions per wave (128 doubles each); 4 beats 8 by
 // 8-10% on 1x128 blocks.  1x1024 and 1x2048 blocks take one block per wave.
 constexpr int kF64RowInstr = 4;

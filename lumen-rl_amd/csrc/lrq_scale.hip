@@ -171,7 +171,6 @@ __global__ __launch_bounds__(256) void k_amax(Desc single, const Desc* __restric
 // (a 2 GiB tensor has 262144 partials: 8 rounds instead of 1024 with one
 // 4-byte load per thread and round); the at most 3 before and 3 after are read
 // singly.
-constexpr int kScaleThreads = 1024;
 constexpr int kScaleLoads = 8;
 __global__ __launch_bounds__(kScaleThreads) void k_tensor_scale(const Desc* __restrict__ descs,
                                                                 const uint32_t* __restrict__ partial) {

@@ -456,6 +456,27 @@ def test_static_workspace_entry_rejects_oversized_table_before_any_hip_call():
     assert L().lrq_tensor_scale_grouped_static(host, ctypes.c_void_p(fake), None) == _lib.ERR_ARG
 
 
+def test_tensor_scale_tensor_count_limit_follows_the_finishing_work_groups():
+    """The finishing launch runs one 1024-thread work-group per tensor, so a
+    tensor-scale table of 2^32 / 1024 tensors is refused before any HIP call."""
+    n = 0xFFFFFFFF // 1024 + 1
+    fake = 1 << 20
+    arr = np.zeros((n, 8), np.int64)  # lrq_tensor: in, codes, scales, batch, rows, cols, ld, batch_stride
+    arr[:, 0] = fake + 16 * np.arange(n, dtype=np.int64)
+    arr[:, 2] = fake
+    arr[:, 3:8] = (1, 1, 8, 8, 8)
+    ts = arr.ctypes.data_as(ctypes.POINTER(_lib.LrqTensor))
+    need = L().lrq_group_table_bytes(_lib.FMT_TENSOR_SCALE, ts, n, _lib.DTYPE_BF16, 1, 1, 0)
+    assert need > 0, _lib.last_error()
+    host = np.zeros(need, np.uint8)
+    assert L().lrq_group_pack(_lib.FMT_TENSOR_SCALE, ts, n, _lib.DTYPE_BF16, 1, 1, 0,
+                              host.ctypes.data, need) == 0, _lib.last_error()
+    ws = L().lrq_group_workspace_bytes(host.ctypes.data)
+    rc = L().lrq_tensor_scale_grouped(host.ctypes.data, ctypes.c_void_p(fake), ctypes.c_void_p(fake), ws, None)
+    assert rc == _lib.ERR_ARG and "too many tensors" in _lib.last_error()
+    del host, arr
+
+
 def test_float64_input_needs_float64_arithmetic_and_the_fp8_block_format():
     fake = ctypes.c_void_p(0x10000)
     rc = L().lrq_fp8_block_quant(fake, _lib.DTYPE_F64, 1, 4, 128, 128, 512, 1, 128, fake, fake, 0, None)
