@@ -199,7 +199,7 @@ int lrq_mx_dequant(int fmt, const uint8_t* codes, const uint8_t* scales, int64_t
  * All tensors of a table share fmt, in_dtype, block shape and flags, and must
  * all qualify for the same kernel (the pack fails otherwise).
  * With fmt LRQ_FMT_FP8_DEQUANT the same tables drive the grouped inverse:
- * WeightQuantizer.dequantize_state_dict (weight_quantizer.py:117-134) in one launch.
+ * WeightQuantizer.dequantize_state_dict (weight_quantizer.py:117-134), one launch per table.
  */
 typedef struct lrq_tensor {
   const void* in;       /* device input */
