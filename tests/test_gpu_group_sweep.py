@@ -187,3 +187,46 @@ def _f64_case(rng, seed, case):
         assert np.array_equal(u8(outs[i][0]), oc[0]), (case, i)
         got_s = outs[i][1].cpu().numpy().view(np.uint64).reshape(-1)
         assert np.array_equal(got_s, osc[0].view(np.uint64).reshape(-1)), (case, i)
+
+
+@pytest.mark.parametrize("seed", [7, 8])
+def test_split_plans_equal_one_launch(seed, monkeypatch):
+    """Plans split into many launches of consecutive tensors (a ~256 KiB limit
+    instead of ~3 GiB) write every byte a one-launch plan writes: FP8 128x128
+    and 1x128, MXFP8, MXFP4 and the FP8 / MX dequant plans, on ragged strided
+    tensors; a re-bind to new storage keeps the split."""
+    rng = np.random.default_rng(seed)
+    ts = [_tensor(rng, int(rng.integers(1, 400)), 128 * int(rng.integers(1, 6)), "bf16", rng.random() < 0.3)
+          for _ in range(24)]
+
+    def plans(limit):
+        monkeypatch.setattr(ops, "GROUP_LAUNCH_BYTES", limit)
+        out = {"tile": ops.QuantPlan(ts, "fp8_block", (128, 128)),
+               "row": ops.QuantPlan(ts, "fp8_block", (1, 128), scale_dtype=torch.bfloat16),
+               "mx8": ops.QuantPlan(ts, "mxfp8", (1, 32)),
+               "mx4": ops.QuantPlan(ts, "mxfp4", (1, 32))}
+        for p in out.values():
+            p.run()
+        out["deq"] = ops.DequantPlan([(c, s) for c, s in out["row"].outputs], (1, 128), torch.bfloat16)
+        out["mxdeq"] = ops.DequantPlan(list(out["mx8"].outputs), (1, 32), torch.float32, fmt="mxfp8")
+        out["deq"].run()
+        out["mxdeq"].run()
+        torch.cuda.synchronize()
+        return out
+
+    one, split = plans(3 << 30), plans(256 << 10)
+    assert all(len(p._launch.parts) == 1 for p in one.values())
+    assert all(len(p._launch.parts) > 2 for p in split.values())
+    for k in ("tile", "row", "mx8", "mx4"):
+        for (c1, s1), (c2, s2) in zip(one[k].outputs, split[k].outputs):
+            assert np.array_equal(u8(c1), u8(c2)), k
+            assert np.array_equal(u8(s1), u8(s2)), k
+    for k in ("deq", "mxdeq"):
+        for o1, o2 in zip(one[k].outputs, split[k].outputs):
+            assert np.array_equal(u8(o1), u8(o2)), k
+    # new storage for every input: the split plan re-binds each of its launches
+    moved = [t.clone() for t in ts]
+    split["tile"].run(inputs=moved)
+    torch.cuda.synchronize()
+    for (c1, s1), (c2, s2) in zip(one["tile"].outputs, split["tile"].outputs):
+        assert np.array_equal(u8(c1), u8(c2)) and np.array_equal(u8(s1), u8(s2))
