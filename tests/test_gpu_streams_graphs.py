@@ -70,10 +70,16 @@ def test_plan_runs_on_the_current_stream():
     _check_fp8_tiles(ws, outs)
 
 
-def test_graph_replay_of_grouped_launches():
+@pytest.mark.parametrize("split", [False, True])
+def test_graph_replay_of_grouped_launches(split, monkeypatch):
+    """Captured grouped launches (one table, or a plan split into a launch per
+    tensor) replay against the eager result after the inputs change."""
     gen = torch.Generator(device=DEV).manual_seed(4)
     ws = _layer(gen)
+    if split:
+        monkeypatch.setattr(ops, "GROUP_LAUNCH_BYTES", 64 << 10)
     plan = QuantPlan(ws, "fp8_block", (128, 128))
+    assert len(plan._launch.parts) == (len(ws) if split else 1)
     scales = TensorScalePlan(ws)
     xa = (torch.randn(256, 1024, generator=gen, device=DEV)).to(torch.bfloat16)
     act_out = torch.empty(256, 1024, dtype=torch.float32, device=DEV)
