@@ -167,6 +167,7 @@ int main() {
   LRQ(lrq_quant_grouped(host_table.data(), dev_table, (lrq_stream_t)st));
   HIP(hipStreamSynchronize(st));
   bool same = lrq_group_units(host_table.data()) == (R[0] / 128) * (C[0] / 128) + (R[1] / 128) * (C[1] / 128);
+  same = same && lrq_group_kernel(host_table.data()) >= 0 && lrq_group_kernel(nullptr) == LRQ_ERR_ARG;
   for (int i = 0; i < 2; ++i) {
     const int64_t ns = (R[i] / 128) * (C[i] / 128);
     std::vector<uint8_t> got((size_t)(R[i] * C[i])), want(got.size());
