@@ -452,6 +452,9 @@ class _GroupLaunches:
         # wherever the launches split it: the first tensor of the first part
         # whose kernel differs is the first tensor that differs from tensor 0.
         kinds = [int(_lib.lib().lrq_group_kernel(p.host.data_ptr())) for p in self.parts]
+        for k in kinds:
+            if k < 0:
+                _lib.check(k, "lrq_group_kernel")
         for (i, _), k in zip(launch_ranges(sizes), kinds):
             if k != kinds[0]:
                 raise ValueError(f"tensor {i} needs a different kernel than tensor 0 "
