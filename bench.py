@@ -45,10 +45,10 @@ default) the line also carries `also`: c3, c4 and c5 timed on the device the
 same way after c2's set is freed (ms_per_step, step GB/s, kernel GB/s and its
 fraction of 8 TB/s; no CPU leg; --no-also skips them).  The roofline object uses the
 same bytes over the step's kernel time (HIP events on the launch stream around
-each plan run, whose grouped launches run back to back): `launch_ms` is the mean
-launch (a run's event time over its launches), as rocprofv3 averages a kernel;
-`plan_run_ms` the run itself; `traffic` the profiled HBM bytes per launch beside
-`algorithmic_bytes_per_launch`.  cpu_baseline times the reference's op sequence in torch on the host
+each span of back-to-back launches: a plan run, or a whole step of several plan
+runs): `launch_ms` is the mean launch (a span's event time over its launches),
+as rocprofv3 averages a kernel; `span_ms` the span itself; `traffic` the
+profiled HBM bytes per launch beside `algorithmic_bytes_per_launch`.  cpu_baseline times the reference's op sequence in torch on the host
 CPU (oracle/torch_ref.py) over a bounded sample of the same weights.
 """
 
@@ -601,10 +601,11 @@ def setup(torch, ops, cfg, args, dev):
 def measure(torch, ops, plans, flush, args, stream):
     """Time exactly args.steps steps (after args.warmup untimed ones) of the
     plans, bracketed by synchronizations, with HIP events on the launch stream
-    around every plan run.  ms_per_step is the wall time per step (the runs'
-    summed event time when an L2 flush separates them); kern_ms is the mean
-    event time of one plan run (its grouped launches back to back) and
-    `achieved` its algorithmic GB/s."""
+    around each event span: a plan run (its grouped launches back to back), or
+    the whole step when a step is several plan runs back to back.  ms_per_step
+    is the wall time per step (the spans' summed event time when an L2 flush
+    separates them); kern_ms is the mean event time of one span,
+    spans_per_step how many a step has, and `achieved` the algorithmic GB/s."""
     # A drop-in call (quantize_state_dict, load_weights) plans on the host
     # before and between its grouped launches.  Its kernel time spans its first
     # launch to the end of its last (the small table uploads between launches
@@ -629,7 +630,24 @@ def measure(torch, ops, plans, flush, args, stream):
 
 
 def _timed_steps(torch, plans, flush, args, stream, inner):
+    # A step of several back-to-back plan runs (C3's 48 per-layer launches) is
+    # one event span: an event pair around every 0.28 ms run read C3 0.7 points
+    # of HBM peak lower (timed in turns on an MI355X).  A single plan run, the
+    # drop-in calls and the L2-flushed C1 keep one span per plan run.
+    step_span = (flush is None and len(plans) > 1
+                 and not any(getattr(p, "launch_timed_inside", False) for p in plans))
+    step_bytes = sum(p.algorithmic_bytes for p in plans)
+
     def step(ev_pairs=None):
+        if step_span and ev_pairs is not None:
+            a = torch.cuda.Event(enable_timing=True)
+            b = torch.cuda.Event(enable_timing=True)
+            a.record(stream)
+            for p in plans:
+                p.run()
+            b.record(stream)
+            ev_pairs.append(([(a, b)], step_bytes))
+            return
         for p in plans:
             if flush is not None:
                 flush.zero_()
@@ -661,7 +679,7 @@ def _timed_steps(torch, plans, flush, args, stream, inner):
         step(evs)
     torch.cuda.synchronize()
     wall = time.perf_counter() - w0
-    per = len(plans)
+    per = 1 if step_span else len(plans)  # event spans per step
     if len(evs) != per * args.steps or not all(pairs for pairs, _ in evs):
         raise SystemExit("expected timed launches for every plan and step")
     launch_ms = [sum(a.elapsed_time(b) for a, b in pairs) for pairs, _ in evs]
@@ -676,7 +694,7 @@ def _timed_steps(torch, plans, flush, args, stream, inner):
     else:  # the L2 flush between launches is not part of the step
         ms_per_step = sum(launch_ms) / args.steps
     return {"ms_per_step": ms_per_step, "median_step_ms": median_step_ms, "kern_ms": kern_ms,
-            "achieved": achieved}
+            "achieved": achieved, "spans_per_step": per}
 
 
 
@@ -711,13 +729,13 @@ def run(args):
         f"({achieved:.1f} GB/s = {achieved / HBM_PEAK_GBS:.1%} of 8 TB/s)")
 
     # Per launch, as rocprofv3 reports a kernel: a step makes `launches` launches
-    # (len(plans) plan runs, each timed by one event pair, its launches back to
-    # back), so the mean launch is a run's event time over its launches (the few
-    # us between a run's launches included).  HBM bytes per launch: the committed
-    # rocprofv3 FETCH_SIZE/WRITE_SIZE summary of this workload (copy-calibrated),
-    # per step, over the step's launches.
+    # in r["spans_per_step"] event spans, each span's launches back to back, so
+    # the mean launch is a span's event time over its launches (the few us
+    # between back-to-back launches included).  HBM bytes per launch: the
+    # committed rocprofv3 FETCH_SIZE/WRITE_SIZE summary of this workload
+    # (copy-calibrated), per step, over the step's launches.
     launches = extra["launches_per_step"]
-    per_run = launches / len(plans)
+    per_run = launches / r["spans_per_step"]
     traffic = None
     pfile = os.path.join(ROOT, "profiles", PROFILE_FOR.get(cfg, "") + ".md")
     if os.path.exists(pfile):
@@ -752,8 +770,8 @@ def run(args):
             "algorithmic_bytes_per_launch": round(step_bytes / launches),
             "kernel": KERNEL_FOR[cfg],
             "launch_ms": round(kern_ms / per_run, 5),
-            "launches_per_plan_run": round(per_run, 3),
-            "plan_run_ms": round(kern_ms, 5),
+            "launches_per_span": round(per_run, 3),
+            "span_ms": round(kern_ms, 5),
         },
     }
     if not args.no_cpu and cpu_ws:
@@ -788,8 +806,8 @@ def also_configs(torch, ops, args, dev, stream):
                   "algorithmic_bytes_per_step": nb, "ms_per_step": round(r["ms_per_step"], 5),
                   "value": round(nb / (r["ms_per_step"] * 1e-3) / 1e9, 2),
                   "achieved": round(r["achieved"], 2), "frac": round(r["achieved"] / HBM_PEAK_GBS, 4),
-                  "launch_ms": round(r["kern_ms"] * len(w["plans"]) / w["extra"]["launches_per_step"], 5),
-                  "plan_run_ms": round(r["kern_ms"], 5)}
+                  "launch_ms": round(r["kern_ms"] * r["spans_per_step"] / w["extra"]["launches_per_step"], 5),
+                  "span_ms": round(r["kern_ms"], 5)}
         log(f"[bench] also {c} ({w['workload']}): {r['ms_per_step']:.4f} ms/step, kernel "
             f"{r['achieved']:.1f} GB/s = {r['achieved'] / HBM_PEAK_GBS:.1%}, setup {time.time() - t0:.1f}s")
         del w
