@@ -571,6 +571,63 @@ def test_exhaustive_pairs_f16_row_and_tile_kernels(arith):
         del xb, xd, c, s, oc, osc
 
 
+def _e4m3_midpoints() -> np.ndarray:
+    """The 126 rounding boundaries between consecutive non-negative e4m3 values."""
+    c = np.arange(0, 127)
+    e, m = c >> 3, c & 7
+    v = np.where(e == 0, m / 8.0 * 2.0 ** -6, (1.0 + m / 8.0) * 2.0 ** (e - 7.0))
+    return (v[:-1] + v[1:]) / 2.0
+
+
+@pytest.mark.parametrize("blk", [(1, 128), (128, 128)])
+def test_float32_quotients_next_to_e4m3_midpoints(blk):
+    """Float32 weights have no exhaustive sweep, so aim at the inputs where the
+    kernels' Markstein quotient could round differently from IEEE x/s: for
+    2000 scales across float32's range (and on both sides of the 2^-80 amax
+    guard), every x within 2 ulps of m*s for each e4m3 rounding boundary m,
+    both signs.  Codes and scales must equal the oracle's (IEEE division)."""
+    rng = np.random.default_rng(2024)
+    mids = _e4m3_midpoints()
+    amaxes = np.concatenate([2.0 ** rng.uniform(-120, 120, 1990),
+                             2.0 ** -80 * np.array([0.5, 0.999, 1.0, 1.001, 2.0]),
+                             np.array([448.0, 1.0, 3.0e38, 1.2e-38, 7.0])]).astype(np.float32)
+    per = blk[0] * 128
+    blocks = []
+    for a in amaxes:
+        s = np.float32(a) / np.float32(448.0)  # what the kernel derives (checked against the oracle's scales)
+        xs = (mids * np.float64(s)).astype(np.float32)
+        up1 = np.nextafter(xs, np.float32(np.inf))
+        dn1 = np.nextafter(xs, np.float32(0))
+        x = np.concatenate([xs, up1, np.nextafter(up1, np.float32(np.inf)),
+                            dn1, np.nextafter(dn1, np.float32(0))])
+        x = x[np.abs(x) <= a]
+        x = np.concatenate([x, -x])
+        take = np.zeros(per, np.float32)
+        n = min(per - 1, x.size)
+        take[0] = a
+        take[1:1 + n] = x[:n]
+        blocks.append(take.reshape(blk[0], 128))
+        for rest in range(per - 1, x.size, per - 1):  # the values that did not fit
+            more = np.zeros(per, np.float32)
+            chunk = x[rest:rest + per - 1]
+            more[0] = a
+            more[1:1 + chunk.size] = chunk
+            blocks.append(more.reshape(blk[0], 128))
+    xb = np.concatenate(blocks).astype(np.float32)
+    say("float32 midpoint neighbours", blk, xb.shape)
+    xd = torch.from_numpy(xb).to(DEV)
+    c, sc = ops.fp8_block_quant(xd, blk)
+    torch.cuda.synchronize()
+    oc, osc = O.fp8_block_quant(xb[None], "f32", "f32", blk)
+    got = u8(c).reshape(oc.shape)
+    bad = np.argwhere(got != oc)
+    if bad.size:
+        say("mismatches", bad.shape[0], [(float(xb.reshape(-1)[i]), hex(got.reshape(-1)[i]), hex(oc.reshape(-1)[i]))
+                                        for i in np.flatnonzero(got.reshape(-1) != oc.reshape(-1))[:6]])
+    assert bad.size == 0
+    assert np.array_equal(scale_bits(sc).reshape(-1), osc.view(np.uint32).reshape(-1))
+
+
 @pytest.mark.slow
 def test_exhaustive_pairs_tile_kernel():
     xb = exhaustive_blocks(128 * 128).reshape(-1, 128)
